@@ -1,0 +1,82 @@
+"""Shared test helpers: seeded masks and the dense-conv (torch fp64) check.
+
+The dense check is independent of the oracle's gather formula: it scatters the
+kept tokens into a zero-filled [B*T, C, H, W] grid, runs ``F.conv2d`` with
+``padding=1`` (the reference's own dense ``2d_conv`` adapter path,
+opentad/models/backbones/vit_sparse_adapter_poguise.py:372-412,484-490) and
+gathers the kept cells back. Gradients come from torch autograd of the same
+expression.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+
+def random_mask(rng: np.random.Generator, B, T, H, W, keep: float) -> np.ndarray:
+    """Keep cells uniformly at random; per frame exactly round(keep*H*W)."""
+    m = np.zeros((B, T, H * W), dtype=np.uint8)
+    k = int(round(keep * H * W))
+    for b in range(B):
+        for t in range(T):
+            m[b, t, rng.permutation(H * W)[:k]] = 1
+    return m.reshape(B, T, H, W)
+
+
+def topk_mask(rng: np.random.Generator, B, T, H, W, keep: float) -> np.ndarray:
+    """Per sample keep ceil(keep*T*H*W) cells by top-k of a U(0,1) score
+    (keep-set rule of vit_sparse_adapter_poguise.py:763,785-787)."""
+    n = T * H * W
+    k = math.ceil(keep * n)
+    score = rng.random((B, n))
+    m = np.zeros((B, n), dtype=np.uint8)
+    idx = np.argsort(-score, axis=1, kind="stable")[:, :k]
+    np.put_along_axis(m, idx, 1, axis=1)
+    return m.reshape(B, T, H, W)
+
+
+def w_std(w: torch.Tensor) -> torch.Tensor:
+    """(9, C_in, C_out) -> (C_out, C_in, 3, 3) with k = ky*3 + kx
+    (sparse_conv_layer.py:150-156)."""
+    nine, ci, co = w.shape
+    return w.permute(2, 1, 0).reshape(co, ci, 3, 3)
+
+
+def dense_reference(mask: np.ndarray, x: np.ndarray, w: np.ndarray, bias, go: np.ndarray,
+                    depthwise: bool = False):
+    """Dense fp64 conv on the zero-filled grid. Returns (y, gi, gw, gb) as numpy fp64.
+
+    ``x``/``go`` rows are the kept cells in flattened B*T*H*W order; ``w`` is
+    (9, C_in, C_out) or (9, C) for depthwise."""
+    B, T, H, W = mask.shape
+    flat = torch.from_numpy(np.flatnonzero(mask.reshape(-1)))
+    C = x.shape[1]
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    grid = torch.zeros(B * T * H * W, C, dtype=torch.float64)
+    grid = grid.index_copy(0, flat, xt)
+    grid = grid.view(B * T, H, W, C).permute(0, 3, 1, 2)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    if depthwise:
+        wk = wt.permute(1, 0).reshape(C, 1, 3, 3)
+        groups = C
+    else:
+        wk = w_std(wt)
+        groups = 1
+    bt = torch.tensor(bias, dtype=torch.float64, requires_grad=True) if bias is not None else None
+    y = F.conv2d(grid, wk, bt, padding=1, groups=groups)
+    y = y.permute(0, 2, 3, 1).reshape(B * T * H * W, -1).index_select(0, flat)
+    y.backward(torch.tensor(go, dtype=torch.float64))
+    gb = bt.grad.numpy() if bt is not None else None
+    return y.detach().numpy(), xt.grad.numpy(), wt.grad.numpy(), gb
+
+
+def kaiming_weight(rng: np.random.Generator, ci: int, co: int) -> np.ndarray:
+    """Kaiming-uniform(a=sqrt(5)) on a (C_out, C_in, 3, 3) tensor, re-laid out to
+    (9, C_in, C_out) (sparse_conv_layer.py:145-161)."""
+    fan_in = ci * 9
+    bound = 1.0 / math.sqrt(fan_in)  # gain*sqrt(3/fan_in) with a=sqrt(5)
+    t = rng.uniform(-bound, bound, size=(co, ci, 3, 3)).astype(np.float32)
+    return np.ascontiguousarray(t.reshape(co, ci, 9).transpose(2, 1, 0))
