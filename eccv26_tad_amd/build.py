@@ -1,0 +1,93 @@
+"""In-tree build of the SparseConv2D native code.
+
+* ``libsvtad_sparse.so``: every ``csrc/*.hip`` compiled by hipcc for gfx950.
+  This is the C-ABI library (``include/svtad_sparse.h``).
+* ``opentad_sparse_ops*.so``: the PyTorch extension (``csrc/torch_ext.cpp``,
+  host C++ compiled by g++ against torch's headers), linked to
+  ``libsvtad_sparse.so`` with an ``$ORIGIN`` rpath.
+
+Run ``python -m eccv26_tad_amd.build`` (or ``__graft_entry__.build()``).
+"""
+from __future__ import annotations
+
+import glob
+import os
+import subprocess
+import sys
+import sysconfig
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "libsvtad_sparse.so")
+EXT_SUFFIX = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+EXT = os.path.join(PKG, "opentad_sparse_ops" + EXT_SUFFIX)
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.path.join(ROCM, "bin", "hipcc")
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    # packed fp32 VALU ops stay off ("Build")
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-result",
+]
+
+
+def _run(cmd, **kw):
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, **kw)
+    out = "\n".join(l for l in r.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{out}")
+    return out
+
+
+def hip_cmd():
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    return [HIPCC, *HIP_FLAGS, *srcs, "-o", LIB + ".tmp"]
+
+
+def ext_cmd():
+    import pybind11
+    import torch.utils.cpp_extension as ce
+
+    inc = ce.include_paths()
+    libdir = ce.library_paths()[0]
+    py_inc = sysconfig.get_paths()["include"]
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           "-DTORCH_EXTENSION_NAME=opentad_sparse_ops", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-D_GLIBCXX_USE_CXX11_ABI=1"]
+    for p in inc + [pybind11.get_include(), py_inc, os.path.join(ROCM, "include")]:
+        cmd += ["-I", p]
+    cmd += [os.path.join(CSRC, "torch_ext.cpp"), "-o", EXT + ".tmp",
+            "-L", libdir, "-L", PKG, "-lsvtad_sparse", "-lc10", "-lc10_hip", "-ltorch",
+            "-ltorch_cpu", "-ltorch_python", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + libdir]
+    return cmd
+
+
+def build(verbose: bool = False) -> None:
+    """Compile the HIP library, then the torch extension against it."""
+    import torch  # noqa: F401  (fails early if torch is absent)
+
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    out = _run(hip_cmd(), cwd=ROOT)
+    if verbose and out.strip():
+        print(out)
+    os.replace(LIB + ".tmp", LIB)
+    cmd = ext_cmd()
+    cmd = [c if not c.startswith("-D_GLIBCXX_USE_CXX11_ABI") else f"-D_GLIBCXX_USE_CXX11_ABI={abi}"
+           for c in cmd]
+    out = _run(cmd, cwd=ROOT)
+    if verbose and out.strip():
+        print(out)
+    os.replace(EXT + ".tmp", EXT)
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print("built", LIB, EXT)

@@ -1,0 +1,186 @@
+// C-ABI entry points of the SparseConv2D convolution: argument checks, path
+// selection (MFMA for f16/bf16 shapes it handles, VALU otherwise) and the
+// backward-weight split plan.
+#include <stdio.h>
+#include <string.h>
+
+#include "sv_common.h"
+#include "sv_conv.h"
+#include "sv_internal.h"
+
+namespace svtad {
+
+static bool dtype_ok(int d) { return d >= SVTAD_F32 && d <= SVTAD_F64; }
+static size_t acc_bytes(int d) { return d == SVTAD_F64 ? 8 : 4; }
+
+static int check_common(const char* who, int64_t n, int c_in, int c_out, int64_t tpb, int dtype) {
+    static thread_local char buf[256];
+    if (c_in % 4 != 0 && c_in == c_out && strncmp(who, "dw_", 3) == 0) {
+        // depthwise: an even element count keeps the 16-bit atomics of the
+        // orphan pass inside the buffer (they update aligned 32-bit words)
+        snprintf(buf, sizeof(buf), "%s: C must be divisible by 4", who);
+        return set_error(SVTAD_ERR_INVALID, buf);
+    }
+    if (!dtype_ok(dtype)) {
+        snprintf(buf, sizeof(buf), "%s: unknown dtype %d", who, dtype);
+        return set_error(SVTAD_ERR_INVALID, buf);
+    }
+    if (n < 0 || c_in <= 0 || c_out <= 0 || tpb < 0) {
+        snprintf(buf, sizeof(buf), "%s: bad sizes n=%lld c_in=%d c_out=%d tokens_per_batch=%lld",
+                 who, (long long)n, c_in, c_out, (long long)tpb);
+        return set_error(SVTAD_ERR_INVALID, buf);
+    }
+    if (n >= (int64_t)INT32_MAX) {
+        snprintf(buf, sizeof(buf), "%s: n=%lld exceeds the int32 table range", who, (long long)n);
+        return set_error(SVTAD_ERR_UNSUPPORTED, buf);
+    }
+    return SVTAD_OK;
+}
+
+// Full conv plan: MFMA partials when the MFMA kernel handles the shape.
+static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
+    BwPlan p;
+    p.path = bw_mfma_supported(dtype, c_in, c_out) ? 1 : 0;
+    const int64_t tiles = p.path ? 9 * cdiv(c_in, 64) * cdiv(c_out, 64) : 9 * cdiv(c_in, 64) * cdiv(c_out, 64);
+    const int64_t target_wg = 1024;
+    int64_t splits = std::max<int64_t>(1, cdiv(target_wg, tiles));
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, n / 128));
+    int64_t rps = cdiv(std::max<int64_t>(n, 1), splits);
+    rps = cdiv(rps, 32) * 32;
+    splits = std::max<int64_t>(1, cdiv(n, rps));
+    p.splits = (int)splits;
+    p.rows_per_split = rps;
+    p.ws_bytes = (size_t)splits * ((size_t)9 * c_in * c_out + (size_t)c_out) * acc_bytes(dtype);
+    return p;
+}
+
+static BwPlan plan_dw_bw(int64_t n, int c, int dtype) {
+    BwPlan p;
+    p.path = 0;
+    const int64_t cblocks = cdiv(c, 64);
+    int64_t splits = std::max<int64_t>(1, cdiv(1024, cblocks));
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, n / 64));
+    int64_t rps = cdiv(std::max<int64_t>(n, 1), splits);
+    rps = cdiv(rps, 4) * 4;
+    splits = std::max<int64_t>(1, cdiv(n, rps));
+    p.splits = (int)splits;
+    p.rows_per_split = rps;
+    p.ws_bytes = (size_t)splits * ((size_t)9 * c + (size_t)c) * acc_bytes(dtype);
+    return p;
+}
+
+}  // namespace svtad
+
+using namespace svtad;
+
+extern "C" int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, const void* bias,
+                         int bias_mode, void* out, int64_t n, int c_in, int c_out,
+                         int64_t tokens_per_batch, int dtype, void* stream) {
+    int st = check_common("fwd", n, c_in, c_out, tokens_per_batch, dtype);
+    if (st) return st;
+    if (c_in % 4 != 0) return set_error(SVTAD_ERR_INVALID, "fwd: C_in must be divisible by 4");
+    if (bias_mode < SVTAD_BIAS_NONE || bias_mode > SVTAD_BIAS_AFTER)
+        return set_error(SVTAD_ERR_INVALID, "fwd: bad bias_mode");
+    if (bias_mode != SVTAD_BIAS_NONE && !bias)
+        return set_error(SVTAD_ERR_INVALID, "fwd: bias_mode needs a bias pointer");
+    if (n == 0) return SVTAD_OK;
+    if (!x || !nbr || !weight || !out) return set_error(SVTAD_ERR_INVALID, "fwd: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    if (gg_mfma_supported(dtype, c_in, c_out))
+        gg_mfma(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
+                tokens_per_batch, s);
+    else
+        gg_valu(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
+                tokens_per_batch, s);
+    return launch_status();
+}
+
+extern "C" int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight,
+                            void* grad_in, int64_t n, int c_in, int c_out, int64_t tokens_per_batch,
+                            int dtype, void* stream) {
+    int st = check_common("bwd_in", n, c_in, c_out, tokens_per_batch, dtype);
+    if (st) return st;
+    if (n == 0) return SVTAD_OK;
+    if (!grad_out || !nbr || !weight || !grad_in)
+        return set_error(SVTAD_ERR_INVALID, "bwd_in: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    // gi[j, ci] = sum_k sum_co go[src_t(j,k), co] * w[k][ci][co]
+    if (gg_mfma_supported(dtype, c_out, c_in))
+        gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
+                tokens_per_batch, s);
+    else
+        gg_valu(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
+                tokens_per_batch, s);
+    orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, s);
+    return launch_status();
+}
+
+extern "C" size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, int dtype) {
+    if (check_common("bwd_w_workspace_bytes", n, c_in, c_out, 0, dtype)) return 0;
+    return plan_bw(n, c_in, c_out, dtype).ws_bytes;
+}
+
+extern "C" int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,
+                           void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n,
+                           int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
+    int st = check_common("bwd_w", n, c_in, c_out, tokens_per_batch, dtype);
+    if (st) return st;
+    const BwPlan p = plan_bw(n, c_in, c_out, dtype);
+    if (!grad_w || !workspace || (n > 0 && (!grad_out || !x || !nbr)))
+        return set_error(SVTAD_ERR_INVALID, "bwd_w: null pointer");
+    if (workspace_bytes < p.ws_bytes)
+        return set_error(SVTAD_ERR_WORKSPACE, "bwd_w: workspace smaller than svtad_bwd_w_workspace_bytes()");
+    hipStream_t s = (hipStream_t)stream;
+    if (p.path == 1)
+        bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
+                tokens_per_batch, s);
+    else
+        bw_valu(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
+                tokens_per_batch, s);
+    return launch_status();
+}
+
+extern "C" int svtad_dw_fwd(const void* x, const int32_t* nbr, const void* weight, const void* bias,
+                            void* out, int64_t n, int c, int64_t tokens_per_batch, int dtype,
+                            void* stream) {
+    int st = check_common("dw_fwd", n, c, c, tokens_per_batch, dtype);
+    if (st) return st;
+    if (n == 0) return SVTAD_OK;
+    if (!x || !nbr || !weight || !out) return set_error(SVTAD_ERR_INVALID, "dw_fwd: null pointer");
+    dw_gather(dtype, MODE_FWD, x, nbr, weight, bias, out, n, c, tokens_per_batch, (hipStream_t)stream);
+    return launch_status();
+}
+
+extern "C" int svtad_dw_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight,
+                               void* grad_in, int64_t n, int c, int64_t tokens_per_batch, int dtype,
+                               void* stream) {
+    int st = check_common("dw_bwd_in", n, c, c, tokens_per_batch, dtype);
+    if (st) return st;
+    if (n == 0) return SVTAD_OK;
+    if (!grad_out || !nbr || !weight || !grad_in)
+        return set_error(SVTAD_ERR_INVALID, "dw_bwd_in: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    dw_gather(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, grad_in, n, c, tokens_per_batch, s);
+    orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, s);
+    return launch_status();
+}
+
+extern "C" size_t svtad_dw_bwd_w_workspace_bytes(int64_t n, int c, int dtype) {
+    if (check_common("dw_bwd_w_workspace_bytes", n, c, c, 0, dtype)) return 0;
+    return plan_dw_bw(n, c, dtype).ws_bytes;
+}
+
+extern "C" int svtad_dw_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,
+                              void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n,
+                              int c, int64_t tokens_per_batch, int dtype, void* stream) {
+    int st = check_common("dw_bwd_w", n, c, c, tokens_per_batch, dtype);
+    if (st) return st;
+    const BwPlan p = plan_dw_bw(n, c, dtype);
+    if (!grad_w || !workspace || (n > 0 && (!grad_out || !x || !nbr)))
+        return set_error(SVTAD_ERR_INVALID, "dw_bwd_w: null pointer");
+    if (workspace_bytes < p.ws_bytes)
+        return set_error(SVTAD_ERR_WORKSPACE, "dw_bwd_w: workspace smaller than svtad_dw_bwd_w_workspace_bytes()");
+    dw_bw(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c, tokens_per_batch,
+          (hipStream_t)stream);
+    return launch_status();
+}

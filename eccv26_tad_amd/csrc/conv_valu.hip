@@ -1,0 +1,462 @@
+// VALU (CUDA-core style) SparseConv2D kernels for every dtype. They carry the
+// fp32/fp64 paths, the depthwise variant, the orphan pass of bwd_in and the
+// row-split reduction of bwd_w; fp16/bf16 full convolutions normally take
+// the MFMA kernels in conv_mfma.hip instead.
+#include "sv_common.h"
+#include "sv_conv.h"
+#include "sv_internal.h"
+
+namespace svtad {
+
+// ---------------------------------------------------------------------------
+// Gathered GEMM: out[m, nn] = sum_k sum_c src[row(m,k), c] * B(k, c, nn)
+//   MODE_FWD  : row = src(m,k),   B(k,c,nn) = w[k][c][nn]  (c over c_in)
+//   MODE_BWDIN: row = src_t(m,k), B(k,c,nn) = w[k][nn][c]  (c over c_out)
+// Tile 64 x 64, 256 threads, 4 x 4 outputs per thread, K step 16.
+// ---------------------------------------------------------------------------
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void k_gg_valu(const T* __restrict__ src,
+                                                 const int32_t* __restrict__ nbr,
+                                                 const T* __restrict__ w,
+                                                 const void* __restrict__ bias, int bias_mode,
+                                                 T* __restrict__ out, int64_t n, int c_red,
+                                                 int n_out, int64_t tpb) {
+    typedef typename Acc<T>::type A;
+    __shared__ int32_t sidx[9][64];
+    __shared__ int any_k[9];
+    __shared__ A As[16][64 + 4];
+    __shared__ A Bs[16][64 + 4];
+    const int tid = threadIdx.x;
+    const int64_t row0 = (int64_t)blockIdx.x * 64;
+    const int col0 = blockIdx.y * 64;
+    if (tid < 9) any_k[tid] = 0;
+    __syncthreads();
+    for (int e = tid; e < 9 * 64; e += 256) {
+        const int k = e >> 6, m = e & 63;
+        const int64_t i = row0 + m;
+        int64_t r = -1;
+        if (i < n) r = MODE == MODE_FWD ? src_row(nbr, i, k, n, tpb) : src_row_t(nbr, i, k, n, tpb);
+        sidx[k][m] = (int32_t)r;
+        if (r >= 0) any_k[k] = 1;
+    }
+    __syncthreads();
+    const int ty = tid >> 4, tx = tid & 15;
+    A acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = 0;
+    for (int k = 0; k < 9; ++k) {
+        if (!any_k[k]) continue;  // uniform across the workgroup
+        const T* wk = w + (int64_t)k * c_red * n_out;
+        for (int c0 = 0; c0 < c_red; c0 += 16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e = tid + 256 * q;
+                const int m = e >> 4, c = e & 15;
+                const int32_t r = sidx[k][m];
+                A v = 0;
+                if (r >= 0 && c0 + c < c_red) v = to_acc<A>(src[(int64_t)r * c_red + c0 + c]);
+                As[c][m] = v;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int e = tid + 256 * q;
+                int c, nn;
+                if (MODE == MODE_FWD) { c = e >> 6; nn = e & 63; }
+                else { nn = e >> 4; c = e & 15; }
+                A v = 0;
+                if (c0 + c < c_red && col0 + nn < n_out) {
+                    v = MODE == MODE_FWD
+                            ? to_acc<A>(wk[(int64_t)(c0 + c) * n_out + col0 + nn])
+                            : to_acc<A>(wk[(int64_t)(col0 + nn) * c_red + c0 + c]);
+                }
+                Bs[c][nn] = v;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                A av[4], bv[4];
+#pragma unroll
+                for (int a = 0; a < 4; ++a) av[a] = As[c][ty * 4 + a];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) bv[b] = Bs[c][tx * 4 + b];
+#pragma unroll
+                for (int a = 0; a < 4; ++a)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) acc[a][b] += av[a] * bv[b];
+            }
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        const int64_t i = row0 + ty * 4 + a;
+        if (i >= n) continue;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int col = col0 + tx * 4 + b;
+            if (col >= n_out) continue;
+            A v = acc[a][b];
+            T o;
+            if (bias_mode == SVTAD_BIAS_FP32) {
+                o = from_acc<T>(v + ((const A*)bias)[col]);
+            } else if (bias_mode == SVTAD_BIAS_AFTER) {
+                o = from_acc<T>(to_acc<A>(from_acc<T>(v)) + to_acc<A>(((const T*)bias)[col]));
+            } else {
+                o = from_acc<T>(v);
+            }
+            out[i * n_out + col] = o;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Orphan pass of bwd_in: entries (i,k) -> j whose transpose (j, 8-k) -> i is
+// not in the table are not covered by the transposed gather; add them here
+// (after the gather kernel has stored gi) with atomics. Tables built from a
+// keep mask have none, so the pass only reads the table.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void atomic_add_out(float* p, float v) { atomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add_out(double* p, double v) { atomicAdd(p, v); }
+
+template <typename H>
+__device__ __forceinline__ void atomic_add_half(H* p, float v) {
+    // CAS on the aligned 32-bit word that holds the 16-bit value.
+    uintptr_t addr = (uintptr_t)p;
+    unsigned int* word = (unsigned int*)(addr & ~(uintptr_t)3);
+    const int shift = (addr & 2) ? 16 : 0;
+    unsigned int old = *word, assumed;
+    do {
+        assumed = old;
+        unsigned short bits = (unsigned short)((assumed >> shift) & 0xffffu);
+        H h = __builtin_bit_cast(H, bits);
+        H nh = (H)((float)h + v);
+        unsigned int nb = (unsigned int)__builtin_bit_cast(unsigned short, nh);
+        unsigned int nw = (assumed & ~(0xffffu << shift)) | (nb << shift);
+        old = atomicCAS(word, assumed, nw);
+    } while (old != assumed);
+}
+__device__ __forceinline__ void atomic_add_out(f16* p, float v) { atomic_add_half(p, v); }
+__device__ __forceinline__ void atomic_add_out(bf16* p, float v) { atomic_add_half(p, v); }
+
+template <typename T, bool DEPTHWISE>
+__global__ __launch_bounds__(256) void k_orphans(const T* __restrict__ go,
+                                                 const int32_t* __restrict__ nbr,
+                                                 const T* __restrict__ w, T* __restrict__ gi,
+                                                 int64_t n, int c_in, int c_out, int64_t tpb) {
+    typedef typename Acc<T>::type A;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n * 9) return;
+    const int64_t i = e / 9;
+    const int k = (int)(e - i * 9);
+    const int64_t j = src_row(nbr, i, k, n, tpb);
+    if (j < 0 || src_row(nbr, j, 8 - k, n, tpb) == i) return;
+    if (DEPTHWISE) {
+        for (int c = 0; c < c_in; ++c)
+            atomic_add_out(gi + j * c_in + c,
+                           to_acc<A>(go[i * c_in + c]) * to_acc<A>(w[(int64_t)k * c_in + c]));
+    } else {
+        const T* wk = w + (int64_t)k * c_in * c_out;
+        for (int ci = 0; ci < c_in; ++ci) {
+            A s = 0;
+            for (int co = 0; co < c_out; ++co)
+                s += to_acc<A>(go[i * c_out + co]) * to_acc<A>(wk[(int64_t)ci * c_out + co]);
+            atomic_add_out(gi + j * c_in + ci, s);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_w partials: ws[s][k][ci][co] = sum over rows of split s of
+// x[src(i,k), ci] * go[i, co]; ws_bias[s][co] = sum over the same rows of go.
+// Grid (co tiles, 9 * ci tiles, splits); tile 64 x 64, K (rows) step 16.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k_bw_valu(const T* __restrict__ go, const T* __restrict__ x,
+                                                 const int32_t* __restrict__ nbr,
+                                                 typename Acc<T>::type* __restrict__ ws,
+                                                 typename Acc<T>::type* __restrict__ ws_bias,
+                                                 int64_t n, int c_in, int c_out, int64_t tpb,
+                                                 int64_t rows_per_split, int n_ci_tiles) {
+    typedef typename Acc<T>::type A;
+    __shared__ int32_t sidx[16];
+    __shared__ A As[16][64 + 4];
+    __shared__ A Bs[16][64 + 4];
+    const int tid = threadIdx.x;
+    const int co0 = blockIdx.x * 64;
+    const int k = blockIdx.y / n_ci_tiles;
+    const int ci0 = (blockIdx.y - k * n_ci_tiles) * 64;
+    const int s = blockIdx.z;
+    const int64_t r_begin = (int64_t)s * rows_per_split;
+    const int64_t r_end = min(n, r_begin + rows_per_split);
+    const bool do_bias = ws_bias != nullptr && k == 4 && ci0 == 0;
+    const int ty = tid >> 4, tx = tid & 15;
+    A acc[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = 0;
+    A bsum = 0;
+    for (int64_t r0 = r_begin; r0 < r_end; r0 += 16) {
+        if (tid < 16) {
+            const int64_t i = r0 + tid;
+            sidx[tid] = i < r_end ? (int32_t)src_row(nbr, i, k, n, tpb) : -1;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = tid + 256 * q;
+            const int r = e >> 6, m = e & 63;
+            const int32_t src = sidx[r];
+            A v = 0;
+            if (src >= 0 && ci0 + m < c_in) v = to_acc<A>(x[(int64_t)src * c_in + ci0 + m]);
+            As[r][m] = v;
+            const int64_t i = r0 + r;
+            A g = 0;
+            if (i < r_end && co0 + m < c_out) g = to_acc<A>(go[i * c_out + co0 + m]);
+            Bs[r][m] = g;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            A av[4], bv[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) av[a] = As[r][ty * 4 + a];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) bv[b] = Bs[r][tx * 4 + b];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) acc[a][b] += av[a] * bv[b];
+        }
+        if (do_bias && tid < 64) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) bsum += Bs[r][tid];
+        }
+        __syncthreads();
+    }
+    A* dst = ws + ((int64_t)s * 9 + k) * c_in * c_out;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+        const int ci = ci0 + ty * 4 + a;
+        if (ci >= c_in) continue;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int co = co0 + tx * 4 + b;
+            if (co < c_out) dst[(int64_t)ci * c_out + co] = acc[a][b];
+        }
+    }
+    if (do_bias && tid < 64 && co0 + tid < c_out) ws_bias[(int64_t)s * c_out + co0 + tid] = bsum;
+}
+
+// Ordered sum of the split partials, rounded once: out[e] = T(sum_s ws[s][e]).
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void k_split_reduce(const A* __restrict__ ws, int64_t count,
+                                                      int splits, T* __restrict__ out) {
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < count;
+         e += (int64_t)gridDim.x * 256) {
+        A s = 0;
+        for (int q = 0; q < splits; ++q) s += ws[(int64_t)q * count + e];
+        out[e] = from_acc<T>(s);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Depthwise (groups = C): one thread per (row, channel).
+// ---------------------------------------------------------------------------
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void k_dw_gather(const T* __restrict__ src,
+                                                   const int32_t* __restrict__ nbr,
+                                                   const T* __restrict__ w,
+                                                   const T* __restrict__ bias,
+                                                   T* __restrict__ out, int64_t n, int c,
+                                                   int64_t tpb) {
+    typedef typename Acc<T>::type A;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n * c) return;
+    const int64_t i = e / c;
+    const int ch = (int)(e - i * c);
+    A s = bias ? to_acc<A>(bias[ch]) : (A)0;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const int64_t r = MODE == MODE_FWD ? src_row(nbr, i, k, n, tpb) : src_row_t(nbr, i, k, n, tpb);
+        if (r >= 0) s += to_acc<A>(src[r * c + ch]) * to_acc<A>(w[k * c + ch]);
+    }
+    out[e] = from_acc<T>(s);
+}
+
+// ws[s][k][c] = sum over rows of split s of go[i,c] * x[src(i,k), c];
+// ws_bias[s][c] = sum of go[i,c]. Grid (channel blocks of 64, splits);
+// 4 waves split the rows, lanes the channels.
+template <typename T>
+__global__ __launch_bounds__(256) void k_dw_bw(const T* __restrict__ go, const T* __restrict__ x,
+                                               const int32_t* __restrict__ nbr,
+                                               typename Acc<T>::type* __restrict__ ws,
+                                               typename Acc<T>::type* __restrict__ ws_bias,
+                                               int64_t n, int c, int64_t tpb,
+                                               int64_t rows_per_split) {
+    typedef typename Acc<T>::type A;
+    __shared__ A red[4][10][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int ch = blockIdx.x * 64 + lane;
+    const int s = blockIdx.y;
+    const int64_t r_begin = (int64_t)s * rows_per_split;
+    const int64_t r_end = min(n, r_begin + rows_per_split);
+    A acc[10];
+#pragma unroll
+    for (int k = 0; k < 10; ++k) acc[k] = 0;
+    if (ch < c) {
+        for (int64_t i = r_begin + wv; i < r_end; i += 4) {
+            const A g = to_acc<A>(go[i * c + ch]);
+            acc[9] += g;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                const int64_t r = src_row(nbr, i, k, n, tpb);
+                if (r >= 0) acc[k] += g * to_acc<A>(x[r * c + ch]);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 10; ++k) red[wv][k][lane] = acc[k];
+    __syncthreads();
+    if (wv == 0 && ch < c) {
+#pragma unroll
+        for (int k = 0; k < 10; ++k) {
+            const A v = red[0][k][lane] + red[1][k][lane] + red[2][k][lane] + red[3][k][lane];
+            if (k < 9) ws[((int64_t)s * 9 + k) * c + ch] = v;
+            else if (ws_bias) ws_bias[(int64_t)s * c + ch] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+
+template <typename T>
+static void launch_gg_valu(int mode, const void* src, const int32_t* nbr, const void* w,
+                           const void* bias, int bias_mode, void* out, int64_t n, int c_red,
+                           int n_out, int64_t tpb, hipStream_t s) {
+    dim3 grid((unsigned)cdiv(n, 64), (unsigned)cdiv(n_out, 64));
+    if (mode == MODE_FWD)
+        hipLaunchKernelGGL((k_gg_valu<T, MODE_FWD>), grid, dim3(256), 0, s, (const T*)src, nbr,
+                           (const T*)w, bias, bias_mode, (T*)out, n, c_red, n_out, tpb);
+    else
+        hipLaunchKernelGGL((k_gg_valu<T, MODE_BWDIN>), grid, dim3(256), 0, s, (const T*)src, nbr,
+                           (const T*)w, (const void*)nullptr, 0, (T*)out, n, c_red, n_out, tpb);
+}
+
+void gg_valu(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+             const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
+             int64_t tpb, hipStream_t s) {
+    switch (dtype) {
+        case SVTAD_F32: launch_gg_valu<float>(mode, src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s); break;
+        case SVTAD_F16: launch_gg_valu<f16>(mode, src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s); break;
+        case SVTAD_BF16: launch_gg_valu<bf16>(mode, src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s); break;
+        case SVTAD_F64: launch_gg_valu<double>(mode, src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s); break;
+    }
+}
+
+template <typename T>
+static void launch_orphans(bool dw, const void* go, const int32_t* nbr, const void* w, void* gi,
+                           int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
+    dim3 grid((unsigned)cdiv(n * 9, 256));
+    if (dw)
+        hipLaunchKernelGGL((k_orphans<T, true>), grid, dim3(256), 0, s, (const T*)go, nbr,
+                           (const T*)w, (T*)gi, n, c_in, c_out, tpb);
+    else
+        hipLaunchKernelGGL((k_orphans<T, false>), grid, dim3(256), 0, s, (const T*)go, nbr,
+                           (const T*)w, (T*)gi, n, c_in, c_out, tpb);
+}
+
+void orphans(int dtype, bool dw, const void* go, const int32_t* nbr, const void* w, void* gi,
+             int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
+    switch (dtype) {
+        case SVTAD_F32: launch_orphans<float>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
+        case SVTAD_F16: launch_orphans<f16>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
+        case SVTAD_BF16: launch_orphans<bf16>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
+        case SVTAD_F64: launch_orphans<double>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
+    }
+}
+
+template <typename T>
+static void launch_bw_valu(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                           void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out,
+                           int64_t tpb, hipStream_t s) {
+    typedef typename Acc<T>::type A;
+    A* part = (A*)ws;
+    A* part_b = gb ? part + (int64_t)p.splits * 9 * c_in * c_out : nullptr;
+    const int n_ci_tiles = (int)cdiv(c_in, 64);
+    dim3 grid((unsigned)cdiv(c_out, 64), (unsigned)(9 * n_ci_tiles), (unsigned)p.splits);
+    hipLaunchKernelGGL((k_bw_valu<T>), grid, dim3(256), 0, s, (const T*)go, (const T*)x, nbr, part,
+                       part_b, n, c_in, c_out, tpb, p.rows_per_split, n_ci_tiles);
+    const int64_t cnt = 9LL * c_in * c_out;
+    hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::min<int64_t>(cdiv(cnt, 256), 4096)),
+                       dim3(256), 0, s, (const A*)part, cnt, p.splits, (T*)gw);
+    if (gb)
+        hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)cdiv(c_out, 256)), dim3(256), 0, s,
+                           (const A*)part_b, (int64_t)c_out, p.splits, (T*)gb);
+}
+
+void bw_valu(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+             void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
+             hipStream_t s) {
+    switch (dtype) {
+        case SVTAD_F32: launch_bw_valu<float>(p, go, x, nbr, gw, gb, ws, n, c_in, c_out, tpb, s); break;
+        case SVTAD_F16: launch_bw_valu<f16>(p, go, x, nbr, gw, gb, ws, n, c_in, c_out, tpb, s); break;
+        case SVTAD_BF16: launch_bw_valu<bf16>(p, go, x, nbr, gw, gb, ws, n, c_in, c_out, tpb, s); break;
+        case SVTAD_F64: launch_bw_valu<double>(p, go, x, nbr, gw, gb, ws, n, c_in, c_out, tpb, s); break;
+    }
+}
+
+template <typename T>
+static void launch_dw(int mode, const void* src, const int32_t* nbr, const void* w,
+                      const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s) {
+    dim3 grid((unsigned)cdiv(n * c, 256));
+    if (mode == MODE_FWD)
+        hipLaunchKernelGGL((k_dw_gather<T, MODE_FWD>), grid, dim3(256), 0, s, (const T*)src, nbr,
+                           (const T*)w, (const T*)bias, (T*)out, n, c, tpb);
+    else
+        hipLaunchKernelGGL((k_dw_gather<T, MODE_BWDIN>), grid, dim3(256), 0, s, (const T*)src, nbr,
+                           (const T*)w, (const T*)nullptr, (T*)out, n, c, tpb);
+}
+
+void dw_gather(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+               const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s) {
+    switch (dtype) {
+        case SVTAD_F32: launch_dw<float>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
+        case SVTAD_F16: launch_dw<f16>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
+        case SVTAD_BF16: launch_dw<bf16>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
+        case SVTAD_F64: launch_dw<double>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
+    }
+}
+
+template <typename T>
+static void launch_dw_bw(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                         void* gw, void* gb, void* ws, int64_t n, int c, int64_t tpb,
+                         hipStream_t s) {
+    typedef typename Acc<T>::type A;
+    A* part = (A*)ws;
+    A* part_b = gb ? part + (int64_t)p.splits * 9 * c : nullptr;
+    dim3 grid((unsigned)cdiv(c, 64), (unsigned)p.splits);
+    hipLaunchKernelGGL((k_dw_bw<T>), grid, dim3(256), 0, s, (const T*)go, (const T*)x, nbr, part,
+                       part_b, n, c, tpb, p.rows_per_split);
+    hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)cdiv(9LL * c, 256)), dim3(256), 0, s,
+                       (const A*)part, 9LL * c, p.splits, (T*)gw);
+    if (gb)
+        hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)cdiv(c, 256)), dim3(256), 0, s,
+                           (const A*)part_b, (int64_t)c, p.splits, (T*)gb);
+}
+
+void dw_bw(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, void* gw,
+           void* gb, void* ws, int64_t n, int c, int64_t tpb, hipStream_t s) {
+    switch (dtype) {
+        case SVTAD_F32: launch_dw_bw<float>(p, go, x, nbr, gw, gb, ws, n, c, tpb, s); break;
+        case SVTAD_F16: launch_dw_bw<f16>(p, go, x, nbr, gw, gb, ws, n, c, tpb, s); break;
+        case SVTAD_BF16: launch_dw_bw<bf16>(p, go, x, nbr, gw, gb, ws, n, c, tpb, s); break;
+        case SVTAD_F64: launch_dw_bw<double>(p, go, x, nbr, gw, gb, ws, n, c, tpb, s); break;
+    }
+}
+
+}  // namespace svtad

@@ -1,0 +1,49 @@
+// Internal interface between the C-ABI dispatch (conv.hip) and the kernel
+// files (conv_valu.hip, conv_mfma.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+namespace svtad {
+
+enum { MODE_FWD = 0, MODE_BWDIN = 1 };
+
+// Row-split plan of a backward-weight reduction. Partials are stored as
+// [splits][9][c_in][c_out] (+ [splits][c_out] for the bias) in the
+// accumulator type.
+struct BwPlan {
+    int path;                 // 0 = VALU, 1 = MFMA
+    int splits;
+    int64_t rows_per_split;
+    size_t ws_bytes;
+};
+
+// gathered GEMM on the VALU (any dtype)
+void gg_valu(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+             const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
+             int64_t tpb, hipStream_t s);
+void orphans(int dtype, bool dw, const void* go, const int32_t* nbr, const void* w, void* gi,
+             int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s);
+void bw_valu(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+             void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
+             hipStream_t s);
+void dw_gather(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+               const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s);
+void dw_bw(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, void* gw,
+           void* gb, void* ws, int64_t n, int c, int64_t tpb, hipStream_t s);
+
+// MFMA path (f16 / bf16). Returns false when the shape is not handled, so the
+// caller falls back to the VALU kernels.
+bool gg_mfma_supported(int dtype, int c_red, int n_out);
+void gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+             const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
+             int64_t tpb, hipStream_t s);
+bool bw_mfma_supported(int dtype, int c_in, int c_out);
+void bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+             void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
+             hipStream_t s);
+
+}  // namespace svtad

@@ -1,0 +1,371 @@
+// `opentad_sparse_ops`: the PyTorch-ROCm extension module. Thin layer over the
+// C ABI in include/svtad_sparse.h: argument checks, output allocation through
+// the caching allocator, and the current HIP stream of the input's device.
+//
+// The five reference functions keep their names, argument order and meaning
+// (opentad/models/bricks/2d_sparse_v3_bind.cpp:8-14); the rest are additions
+// the autograd wrapper and the table utilities use.
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <tuple>
+
+#include "../../include/svtad_sparse.h"
+
+namespace {
+
+int dtype_code(const at::Tensor& t) {
+    switch (t.scalar_type()) {
+        case at::kFloat: return SVTAD_F32;
+        case at::kHalf: return SVTAD_F16;
+        case at::kBFloat16: return SVTAD_BF16;
+        case at::kDouble: return SVTAD_F64;
+        default: TORCH_CHECK(false, "opentad_sparse_ops: unsupported dtype ", t.scalar_type());
+    }
+    return -1;
+}
+
+void* stream_of(const at::Tensor& t) {
+    return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check_status(int st, const char* who) {
+    TORCH_CHECK(st == SVTAD_OK, "opentad_sparse_ops.", who, ": ", svtad_last_error(), " (status ",
+                st, ")");
+}
+
+void check_gpu(const at::Tensor& t, const char* name) {
+    TORCH_CHECK(t.is_cuda(), "opentad_sparse_ops: ", name, " must be a GPU tensor");
+}
+
+at::Tensor rows_view(const at::Tensor& t) {
+    TORCH_CHECK(t.dim() >= 1, "expected at least 1 dimension");
+    return t.contiguous();
+}
+
+int64_t n_rows(const at::Tensor& t) { return t.size(-1) == 0 ? 0 : t.numel() / t.size(-1); }
+
+at::Tensor table_i32(const at::Tensor& nbr, int64_t n) {
+    check_gpu(nbr, "neighbor_indices");
+    TORCH_CHECK(nbr.scalar_type() == at::kInt, "neighbor_indices must be int32, got ",
+                nbr.scalar_type());
+    TORCH_CHECK(nbr.numel() == n * 9, "neighbor_indices has ", nbr.numel(), " entries, expected ",
+                n, " x 9");
+    return nbr.contiguous();
+}
+
+bool bias_present(const c10::optional<at::Tensor>& b) { return b.has_value() && b->defined() && b->numel() > 0; }
+
+at::Tensor conv_fwd(const at::Tensor& x_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
+                    const c10::optional<at::Tensor>& bias_in, int64_t tpb, int bias_mode,
+                    int64_t c_out_arg) {
+    check_gpu(x_in, "x");
+    check_gpu(w_in, "weight");
+    at::Tensor x = rows_view(x_in);
+    const int64_t c_in = x.size(-1);
+    const int64_t n = n_rows(x);
+    TORCH_CHECK(w_in.dim() == 3 && w_in.size(0) == 9 && w_in.size(1) == c_in,
+                "weight must be (9, C_in, C_out) with C_in = ", c_in, ", got ", w_in.sizes());
+    const int64_t c_out = w_in.size(2);
+    TORCH_CHECK(c_out_arg < 0 || c_out_arg == c_out, "C_out argument ", c_out_arg,
+                " does not match weight.size(2) = ", c_out);
+    TORCH_CHECK(w_in.scalar_type() == x.scalar_type(), "x and weight dtypes differ: ",
+                x.scalar_type(), " vs ", w_in.scalar_type());
+    at::Tensor w = w_in.contiguous();
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    at::Tensor bias;
+    if (bias_mode != SVTAD_BIAS_NONE && bias_present(bias_in)) {
+        TORCH_CHECK(bias_in->numel() == c_out, "bias must have C_out = ", c_out, " elements");
+        const at::ScalarType bt = bias_mode == SVTAD_BIAS_FP32
+                                      ? (x.scalar_type() == at::kDouble ? at::kDouble : at::kFloat)
+                                      : x.scalar_type();
+        bias = bias_in->to(x.device(), bt).contiguous();
+    } else {
+        bias_mode = SVTAD_BIAS_NONE;
+    }
+    at::Tensor out = at::empty({n, c_out}, x.options());
+    const int st = svtad_fwd(x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                             bias.defined() ? bias.data_ptr() : nullptr, bias_mode, out.data_ptr(),
+                             n, (int)c_in, (int)c_out, tpb, dtype_code(x), stream_of(x));
+    check_status(st, "fwd");
+    return out;
+}
+
+}  // namespace
+
+// fwd(x, neighbor_indices, weight, C_out, tokens_per_batch) -> [N, C_out], no bias
+// (2d_sparse_v3.cu:751-822)
+at::Tensor op_fwd(const at::Tensor& x, const at::Tensor& nbr, const at::Tensor& w, int64_t c_out,
+                  int64_t tpb) {
+    return conv_fwd(x, nbr, w, c10::nullopt, tpb, SVTAD_BIAS_NONE, c_out);
+}
+
+// implicit_gemm_fwd_v2(x, neighbor_indices, weight, bias, tokens_per_batch); an empty
+// bias means no bias, bias is added in fp32 (implicit_gemm_v2.cu:197-300)
+at::Tensor op_implicit_gemm_fwd_v2(const at::Tensor& x, const at::Tensor& nbr, const at::Tensor& w,
+                                   const c10::optional<at::Tensor>& bias, int64_t tpb) {
+    return conv_fwd(x, nbr, w, bias, tpb, SVTAD_BIAS_FP32, -1);
+}
+
+// implicit_gemm_fwd_v2_chunked(..., chunk_size): same result; chunk_size was a
+// memory knob of the reference's host chunk loop (implicit_gemm_v2.cu:306-417),
+// which this implementation does not need.
+at::Tensor op_implicit_gemm_fwd_v2_chunked(const at::Tensor& x, const at::Tensor& nbr,
+                                           const at::Tensor& w,
+                                           const c10::optional<at::Tensor>& bias, int64_t tpb,
+                                           int64_t chunk_size) {
+    TORCH_CHECK(chunk_size > 0, "chunk_size must be positive, got ", chunk_size);
+    return conv_fwd(x, nbr, w, bias, tpb, SVTAD_BIAS_FP32, -1);
+}
+
+// fwd_bias(x, neighbor_indices, weight, bias, tokens_per_batch, bias_mode)
+at::Tensor op_fwd_bias(const at::Tensor& x, const at::Tensor& nbr, const at::Tensor& w,
+                       const c10::optional<at::Tensor>& bias, int64_t tpb, int64_t bias_mode) {
+    TORCH_CHECK(bias_mode >= 0 && bias_mode <= 2, "bias_mode must be 0, 1 or 2");
+    return conv_fwd(x, nbr, w, bias, tpb, (int)bias_mode, -1);
+}
+
+// bwd_in(grad_output, neighbor_indices, weight, n_kept, C_in, tokens_per_batch)
+// -> [n_kept, C_in] in grad_output's dtype (2d_sparse_v3.cu:824-835)
+at::Tensor op_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
+                     int64_t n_kept, int64_t c_in, int64_t tpb) {
+    check_gpu(go_in, "grad_output");
+    check_gpu(w_in, "weight");
+    at::Tensor go = rows_view(go_in);
+    const int64_t c_out = go.size(-1);
+    TORCH_CHECK(n_rows(go) == n_kept, "grad_output has ", n_rows(go), " rows, n_kept = ", n_kept);
+    TORCH_CHECK(w_in.dim() == 3 && w_in.size(0) == 9 && w_in.size(1) == c_in && w_in.size(2) == c_out,
+                "weight must be (9, ", c_in, ", ", c_out, "), got ", w_in.sizes());
+    TORCH_CHECK(w_in.scalar_type() == go.scalar_type(), "grad_output and weight dtypes differ");
+    at::Tensor w = w_in.contiguous();
+    at::Tensor nbr = table_i32(nbr_in, n_kept);
+    c10::DeviceGuard g(go.device());
+    at::Tensor gi = at::empty({n_kept, c_in}, go.options());
+    const int st = svtad_bwd_in(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(), gi.data_ptr(),
+                                n_kept, (int)c_in, (int)c_out, tpb, dtype_code(go), stream_of(go));
+    check_status(st, "bwd_in");
+    return gi;
+}
+
+// bwd_w_bias(grad_output, x, neighbor_indices, C_in, tokens_per_batch, with_bias)
+// -> (grad_weight [9, C_in, C_out] in x's dtype, grad_bias [C_out] or empty)
+std::tuple<at::Tensor, at::Tensor> op_bwd_w_bias(const at::Tensor& go_in, const at::Tensor& x_in,
+                                                 const at::Tensor& nbr_in, int64_t c_in,
+                                                 int64_t tpb, bool with_bias) {
+    check_gpu(go_in, "grad_output");
+    check_gpu(x_in, "x");
+    at::Tensor go = rows_view(go_in);
+    at::Tensor x = rows_view(x_in);
+    TORCH_CHECK(x.size(-1) == c_in, "x has ", x.size(-1), " channels, C_in = ", c_in);
+    const int64_t n = n_rows(x);
+    TORCH_CHECK(n_rows(go) == n, "grad_output has ", n_rows(go), " rows, x has ", n);
+    TORCH_CHECK(go.scalar_type() == x.scalar_type(), "grad_output and x dtypes differ");
+    const int64_t c_out = go.size(-1);
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    const int dt = dtype_code(x);
+    const size_t ws_bytes = svtad_bwd_w_workspace_bytes(n, (int)c_in, (int)c_out, dt);
+    TORCH_CHECK(ws_bytes > 0, "bwd_w: ", svtad_last_error());
+    at::Tensor ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
+    at::Tensor gw = at::empty({9, c_in, c_out}, x.options());
+    at::Tensor gb = with_bias ? at::empty({c_out}, x.options()) : at::Tensor();
+    const int st = svtad_bwd_w(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), gw.data_ptr(),
+                               with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
+                               (int)c_in, (int)c_out, tpb, dt, stream_of(x));
+    check_status(st, "bwd_w");
+    return {gw, with_bias ? gb : at::empty({0}, x.options())};
+}
+
+// bwd_w(grad_output, x, neighbor_indices, C_in, tokens_per_batch) -> [9, C_in, C_out]
+// (2d_sparse_v3.cu:837-850)
+at::Tensor op_bwd_w(const at::Tensor& go, const at::Tensor& x, const at::Tensor& nbr, int64_t c_in,
+                    int64_t tpb) {
+    return std::get<0>(op_bwd_w_bias(go, x, nbr, c_in, tpb, false));
+}
+
+// ---------------------------------------------------------------------------
+// depthwise (groups = C), weight (9, C)
+// ---------------------------------------------------------------------------
+
+at::Tensor op_dw_fwd(const at::Tensor& x_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
+                     const c10::optional<at::Tensor>& bias_in, int64_t tpb) {
+    check_gpu(x_in, "x");
+    at::Tensor x = rows_view(x_in);
+    const int64_t c = x.size(-1), n = n_rows(x);
+    TORCH_CHECK(w_in.dim() == 2 && w_in.size(0) == 9 && w_in.size(1) == c,
+                "depthwise weight must be (9, ", c, "), got ", w_in.sizes());
+    TORCH_CHECK(w_in.scalar_type() == x.scalar_type(), "x and weight dtypes differ");
+    at::Tensor w = w_in.contiguous();
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    at::Tensor bias;
+    if (bias_present(bias_in)) bias = bias_in->to(x.device(), x.scalar_type()).contiguous();
+    at::Tensor out = at::empty({n, c}, x.options());
+    const int st = svtad_dw_fwd(x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                                bias.defined() ? bias.data_ptr() : nullptr, out.data_ptr(), n, (int)c,
+                                tpb, dtype_code(x), stream_of(x));
+    check_status(st, "dw_fwd");
+    return out;
+}
+
+at::Tensor op_dw_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
+                        int64_t tpb) {
+    check_gpu(go_in, "grad_output");
+    at::Tensor go = rows_view(go_in);
+    const int64_t c = go.size(-1), n = n_rows(go);
+    TORCH_CHECK(w_in.dim() == 2 && w_in.size(0) == 9 && w_in.size(1) == c,
+                "depthwise weight must be (9, ", c, ")");
+    TORCH_CHECK(w_in.scalar_type() == go.scalar_type(), "grad_output and weight dtypes differ");
+    at::Tensor w = w_in.contiguous();
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(go.device());
+    at::Tensor gi = at::empty({n, c}, go.options());
+    const int st = svtad_dw_bwd_in(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                                   gi.data_ptr(), n, (int)c, tpb, dtype_code(go), stream_of(go));
+    check_status(st, "dw_bwd_in");
+    return gi;
+}
+
+std::tuple<at::Tensor, at::Tensor> op_dw_bwd_w(const at::Tensor& go_in, const at::Tensor& x_in,
+                                               const at::Tensor& nbr_in, int64_t tpb,
+                                               bool with_bias) {
+    check_gpu(go_in, "grad_output");
+    at::Tensor go = rows_view(go_in);
+    at::Tensor x = rows_view(x_in);
+    const int64_t c = x.size(-1), n = n_rows(x);
+    TORCH_CHECK(go.size(-1) == c && n_rows(go) == n, "grad_output must match x's shape");
+    TORCH_CHECK(go.scalar_type() == x.scalar_type(), "grad_output and x dtypes differ");
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    const int dt = dtype_code(x);
+    const size_t ws_bytes = svtad_dw_bwd_w_workspace_bytes(n, (int)c, dt);
+    TORCH_CHECK(ws_bytes > 0, "dw_bwd_w: ", svtad_last_error());
+    at::Tensor ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
+    at::Tensor gw = at::empty({9, c}, x.options());
+    at::Tensor gb = with_bias ? at::empty({c}, x.options()) : at::empty({0}, x.options());
+    const int st = svtad_dw_bwd_w(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), gw.data_ptr(),
+                                  with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
+                                  (int)c, tpb, dt, stream_of(x));
+    check_status(st, "dw_bwd_w");
+    return {gw, gb};
+}
+
+// ---------------------------------------------------------------------------
+// neighbor tables
+// ---------------------------------------------------------------------------
+
+// build_neighbor_table(mask [..., H, W] bool/uint8) -> int32 [N, 9]
+at::Tensor op_build_neighbor_table(const at::Tensor& mask_in) {
+    check_gpu(mask_in, "mask");
+    TORCH_CHECK(mask_in.dim() >= 2, "mask must be [..., H, W]");
+    TORCH_CHECK(mask_in.scalar_type() == at::kBool || mask_in.scalar_type() == at::kByte,
+                "mask must be bool or uint8");
+    at::Tensor mask = mask_in.contiguous();
+    if (mask.scalar_type() == at::kBool) mask = mask.view(at::kByte);
+    const int64_t h = mask.size(-2), w = mask.size(-1);
+    const int64_t frames = h * w == 0 ? 0 : mask.numel() / (h * w);
+    c10::DeviceGuard g(mask.device());
+    at::Tensor offs = at::empty({frames + 1}, mask.options().dtype(at::kInt));
+    void* s = stream_of(mask);
+    check_status(svtad_table_scan(mask.data_ptr<uint8_t>(), frames, (int)h, (int)w,
+                                  offs.data_ptr<int32_t>(), s),
+                 "build_neighbor_table");
+    const int64_t n = offs[frames].item<int32_t>();  // host sync: sizes the output
+    at::Tensor table = at::empty({n, 9}, mask.options().dtype(at::kInt));
+    check_status(svtad_table_fill(mask.data_ptr<uint8_t>(), offs.data_ptr<int32_t>(), frames, (int)h,
+                                  (int)w, table.data_ptr<int32_t>(), s),
+                 "build_neighbor_table");
+    return table;
+}
+
+// remap_neighbor_table(table [B, N_prev, 9] int32, keep_idx [B, N_new] int64) -> [B, N_new, 9]
+at::Tensor op_remap_neighbor_table(const at::Tensor& table_in, const at::Tensor& keep_in) {
+    check_gpu(table_in, "table");
+    check_gpu(keep_in, "keep_idx");
+    TORCH_CHECK(table_in.dim() == 3 && table_in.size(2) == 9, "table must be [B, N_prev, 9]");
+    TORCH_CHECK(table_in.scalar_type() == at::kInt, "table must be int32");
+    TORCH_CHECK(keep_in.dim() == 2 && keep_in.size(0) == table_in.size(0), "keep_idx must be [B, N_new]");
+    at::Tensor table = table_in.contiguous();
+    at::Tensor keep = keep_in.to(at::kLong).contiguous();
+    const int64_t B = table.size(0), n_prev = table.size(1), n_new = keep.size(1);
+    c10::DeviceGuard g(table.device());
+    at::Tensor mapping = at::empty({B * n_prev}, table.options());
+    at::Tensor out = at::empty({B, n_new, 9}, table.options());
+    check_status(svtad_remap_table(table.data_ptr<int32_t>(), B, n_prev, keep.data_ptr<int64_t>(),
+                                   n_new, mapping.data_ptr<int32_t>(), out.data_ptr<int32_t>(),
+                                   stream_of(table)),
+                 "remap_neighbor_table");
+    return out;
+}
+
+// transpose_neighbor_table(table [N, 9], tokens_per_batch) -> (table_t [N, 9], collisions [1])
+std::tuple<at::Tensor, at::Tensor> op_transpose_neighbor_table(const at::Tensor& table_in,
+                                                               int64_t tpb) {
+    check_gpu(table_in, "table");
+    TORCH_CHECK(table_in.scalar_type() == at::kInt, "table must be int32");
+    TORCH_CHECK(table_in.numel() % 9 == 0, "table must have 9 entries per row");
+    at::Tensor table = table_in.contiguous();
+    const int64_t n = table.numel() / 9;
+    c10::DeviceGuard g(table.device());
+    at::Tensor tt = at::empty({n, 9}, table.options());
+    at::Tensor coll = at::zeros({1}, table.options());
+    check_status(svtad_transpose_table(table.data_ptr<int32_t>(), n, tpb, tt.data_ptr<int32_t>(),
+                                       coll.data_ptr<int32_t>(), stream_of(table)),
+                 "transpose_neighbor_table");
+    return {tt, coll};
+}
+
+// validate_neighbor_table(table, bound) -> int32 [3] = (entries out of range, min, max)
+at::Tensor op_validate_neighbor_table(const at::Tensor& table_in, int64_t bound) {
+    check_gpu(table_in, "table");
+    TORCH_CHECK(table_in.scalar_type() == at::kInt, "table must be int32");
+    at::Tensor table = table_in.contiguous();
+    c10::DeviceGuard g(table.device());
+    at::Tensor stats = at::empty({3}, table.options());
+    check_status(svtad_validate_table(table.data_ptr<int32_t>(), table.numel(), bound,
+                                      stats.data_ptr<int32_t>(), stream_of(table)),
+                 "validate_neighbor_table");
+    return stats;
+}
+
+PYBIND11_MODULE(opentad_sparse_ops, m) {
+    m.doc() = "MI355X (gfx950) SparseConv2D: drop-in for the reference opentad_sparse_ops";
+    m.def("fwd", &op_fwd, "Forward", py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
+          py::arg("C_out"), py::arg("tokens_per_batch"));
+    m.def("bwd_in", &op_bwd_in, "Backward Input", py::arg("grad_output"),
+          py::arg("neighbor_indices"), py::arg("weight"), py::arg("n_kept"), py::arg("C_in"),
+          py::arg("tokens_per_batch"));
+    m.def("bwd_w", &op_bwd_w, "Backward Weight", py::arg("grad_output"), py::arg("x"),
+          py::arg("neighbor_indices"), py::arg("C_in"), py::arg("tokens_per_batch"));
+    m.def("implicit_gemm_fwd_v2", &op_implicit_gemm_fwd_v2, "Implicit GEMM forward (fused bias)",
+          py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"), py::arg("bias"),
+          py::arg("tokens_per_batch"));
+    m.def("implicit_gemm_fwd_v2_chunked", &op_implicit_gemm_fwd_v2_chunked,
+          "Implicit GEMM forward (chunk_size accepted, not needed)", py::arg("x"),
+          py::arg("neighbor_indices"), py::arg("weight"), py::arg("bias"),
+          py::arg("tokens_per_batch"), py::arg("chunk_size"));
+    m.def("fwd_bias", &op_fwd_bias, "Forward with bias_mode 0 none / 1 fp32 / 2 after rounding",
+          py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"), py::arg("bias"),
+          py::arg("tokens_per_batch"), py::arg("bias_mode"));
+    m.def("bwd_w_bias", &op_bwd_w_bias, "Backward weight and bias", py::arg("grad_output"),
+          py::arg("x"), py::arg("neighbor_indices"), py::arg("C_in"), py::arg("tokens_per_batch"),
+          py::arg("with_bias"));
+    m.def("dw_fwd", &op_dw_fwd, "Depthwise forward", py::arg("x"), py::arg("neighbor_indices"),
+          py::arg("weight"), py::arg("bias"), py::arg("tokens_per_batch"));
+    m.def("dw_bwd_in", &op_dw_bwd_in, "Depthwise backward input", py::arg("grad_output"),
+          py::arg("neighbor_indices"), py::arg("weight"), py::arg("tokens_per_batch"));
+    m.def("dw_bwd_w", &op_dw_bwd_w, "Depthwise backward weight and bias", py::arg("grad_output"),
+          py::arg("x"), py::arg("neighbor_indices"), py::arg("tokens_per_batch"),
+          py::arg("with_bias"));
+    m.def("build_neighbor_table", &op_build_neighbor_table, "Neighbor table from a keep mask",
+          py::arg("mask"));
+    m.def("remap_neighbor_table", &op_remap_neighbor_table, "Neighbor table remap after a prune",
+          py::arg("table"), py::arg("keep_idx"));
+    m.def("transpose_neighbor_table", &op_transpose_neighbor_table, "Transposed neighbor table",
+          py::arg("table"), py::arg("tokens_per_batch") = 0);
+    m.def("validate_neighbor_table", &op_validate_neighbor_table,
+          "(out-of-range count, min, max) of a neighbor table", py::arg("table"), py::arg("bound"));
+    m.def("version", []() { return std::string(svtad_version()); });
+}

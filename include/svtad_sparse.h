@@ -1,0 +1,173 @@
+/*
+ * svtad_sparse.h — C ABI of the MI355X (gfx950) SparseConv2D library
+ * (libsvtad_sparse.so).
+ *
+ * This is the drop-in boundary under the `opentad_sparse_ops` Python module.
+ * Each entry point below names the reference interface it replaces
+ * (paths relative to the pcr-upm/eccv26_tad repository root):
+ *   2d_sparse_v3_bind.cpp = opentad/models/bricks/2d_sparse_v3_bind.cpp
+ *   2d_sparse_v3.cu       = opentad/models/bricks/2d_sparse_v3.cu
+ *   implicit_gemm_v2.cu   = opentad/models/bricks/implicit_gemm_v2.cu
+ *   sparse_conv_layer.py  = opentad/models/bricks/sparse_conv_layer.py
+ *   poguise.py            = opentad/models/backbones/vit_sparse_adapter_poguise.py
+ *
+ * Conventions
+ *   - Every pointer argument is device memory, except where marked "host".
+ *     Buffers are owned by the caller and 16-byte aligned; the library
+ *     allocates nothing.
+ *   - `stream` is a hipStream_t (NULL = the null stream). Every kernel of a
+ *     call is enqueued on it; calls do not synchronise.
+ *   - Tensors are dense row-major: x [n, c_in], out [n, c_out],
+ *     nbr [n, 9] int32, weight [9, c_in, c_out] with k = ky*3 + kx
+ *     (sparse_conv_layer.py:136,150-156), depthwise weight [9, c].
+ *   - Neighbor entries: -1 = missing; otherwise the source row is
+ *     nbr[i*9+k] + off(i), off(i) = (i / tokens_per_batch) * tokens_per_batch
+ *     when tokens_per_batch > 0, else 0 (per-row rule, 2d_sparse_v3.cu:674-677).
+ *     Any other negative entry, or a source row >= n, is treated as missing
+ *     (the reference reads out of bounds there).
+ *   - Return value: SVTAD_OK (0), a negative SVTAD_ERR_* for a rejected
+ *     argument (message in svtad_last_error()), or a positive hipError_t from
+ *     a kernel launch.
+ *   - Accumulation is fp32 for f32/f16/bf16 and fp64 for f64; each output is
+ *     rounded once to `dtype` (round-to-nearest-even).
+ */
+#ifndef SVTAD_SPARSE_H
+#define SVTAD_SPARSE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum svtad_dtype { SVTAD_F32 = 0, SVTAD_F16 = 1, SVTAD_BF16 = 2, SVTAD_F64 = 3 };
+
+enum svtad_status {
+    SVTAD_OK = 0,
+    SVTAD_ERR_INVALID = -1,      /* bad shape, dtype or pointer */
+    SVTAD_ERR_WORKSPACE = -2,    /* workspace too small */
+    SVTAD_ERR_UNSUPPORTED = -3   /* valid request this build does not handle */
+};
+
+/* bias_mode of svtad_fwd */
+enum svtad_bias_mode {
+    SVTAD_BIAS_NONE = 0,
+    SVTAD_BIAS_FP32 = 1,   /* bias in the accumulator type (float32; float64 for
+                              SVTAD_F64) added before rounding
+                              (implicit_gemm_v2.cu:153-159, 291-294) */
+    SVTAD_BIAS_AFTER = 2   /* bias in `dtype`, added after rounding the conv to
+                              dtype, then rounded again: `output += bias`
+                              (sparse_conv_layer.py:86-87) */
+};
+
+/* Message of the last SVTAD_ERR_* returned on this host thread. */
+const char* svtad_last_error(void);
+const char* svtad_version(void);
+
+/*
+ * Forward SparseConv2D: out[i,co] = sum_k sum_ci x[src(i,k),ci] * w[k,ci,co]
+ * (+ bias per bias_mode; bias may be NULL when mode = NONE).
+ * Replaces `fwd` / launch_fwd (2d_sparse_v3_bind.cpp:9, 2d_sparse_v3.cu:751-822)
+ * with SVTAD_BIAS_NONE, and `implicit_gemm_fwd_v2` / `implicit_gemm_fwd_v2_chunked`
+ * (2d_sparse_v3_bind.cpp:12-13, implicit_gemm_v2.cu:197-300, 306-417) with
+ * SVTAD_BIAS_FP32. Requires c_in % 4 == 0 (sparse_conv_layer.py:39-42).
+ */
+int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, const void* bias,
+              int bias_mode, void* out, int64_t n, int c_in, int c_out,
+              int64_t tokens_per_batch, int dtype, void* stream);
+
+/*
+ * Backward-input: gi[src(i,k),ci] += sum_co go[i,co] * w[k,ci,co], as a
+ * scatter-free gather over the transposed table (entries whose transpose is
+ * not in the table are added afterwards with atomics).
+ * Replaces `bwd_in` / launch_bwd_in (2d_sparse_v3_bind.cpp:10,
+ * 2d_sparse_v3.cu:824-835). gi is fully written (no pre-zeroing needed).
+ */
+int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight, void* grad_in,
+                 int64_t n, int c_in, int c_out, int64_t tokens_per_batch, int dtype,
+                 void* stream);
+
+/* Workspace bytes needed by svtad_bwd_w for this shape. */
+size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, int dtype);
+
+/*
+ * Backward-weight: gw[k,ci,co] = sum_i go[i,co] * x[src(i,k),ci], as a
+ * deterministic per-offset reduction (row-split fp32 partials in `workspace`,
+ * then an ordered sum). If grad_bias is not NULL it also writes
+ * grad_bias[co] = sum_i go[i,co] (sparse_conv_layer.py:120-121).
+ * Replaces `bwd_w` / launch_bwd_w (2d_sparse_v3_bind.cpp:11, 2d_sparse_v3.cu:837-850).
+ */
+int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,
+                void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n, int c_in,
+                int c_out, int64_t tokens_per_batch, int dtype, void* stream);
+
+/*
+ * Depthwise variant (groups = c), weight [9, c]. No counterpart in the
+ * reference (SparseConv2d has no groups, sparse_conv_layer.py:126-141); same
+ * index semantics as above. bias (dtype `dtype`) may be NULL; it is added to
+ * the accumulator before rounding. Requires c % 4 == 0.
+ */
+int svtad_dw_fwd(const void* x, const int32_t* nbr, const void* weight, const void* bias,
+                 void* out, int64_t n, int c, int64_t tokens_per_batch, int dtype, void* stream);
+int svtad_dw_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight, void* grad_in,
+                    int64_t n, int c, int64_t tokens_per_batch, int dtype, void* stream);
+size_t svtad_dw_bwd_w_workspace_bytes(int64_t n, int c, int dtype);
+int svtad_dw_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,
+                   void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n, int c,
+                   int64_t tokens_per_batch, int dtype, void* stream);
+
+/*
+ * Neighbor table from a keep mask [n_frames, h, w] (uint8, nonzero = kept),
+ * in two steps so the caller can size the table:
+ *   1. svtad_table_scan writes frame_offsets[0..n_frames] (int32): the
+ *      exclusive prefix count of kept cells per frame; frame_offsets[n_frames]
+ *      is the total N.
+ *   2. svtad_table_fill writes table [N, 9]: for the kept cell p with rank r,
+ *      table[r,k] = rank(p + delta_k) if that cell is inside the frame and
+ *      kept, else -1, with k = (dy+1)*3 + (dx+1).
+ * For a full mask this is get_initial_neighbor_indices (poguise.py:1623-1670);
+ * for a pruned mask with sorted keep lists it equals that table after the
+ * Block remaps (poguise.py:913-977). Global indices (batch offsets included).
+ * Requires h*w <= 16384 and n_frames*h*w < 2^31.
+ */
+int svtad_table_scan(const uint8_t* mask, int64_t n_frames, int h, int w, int32_t* frame_offsets,
+                     void* stream);
+int svtad_table_fill(const uint8_t* mask, const int32_t* frame_offsets, int64_t n_frames, int h,
+                     int w, int32_t* table, void* stream);
+
+/*
+ * Table remap after a prune (poguise.py:913-977; internvideo_next.py:1447-1492):
+ * out[b*n_new+j, k] = mapping[table[b*n_prev + keep_idx[b,j], k]] for valid
+ * entries, where mapping[b*n_prev + keep_idx[b,j]] = b*n_new + j and -1
+ * elsewhere. keep_idx is int64 [B, n_new] (local indices into n_prev, as
+ * returned by topk); mapping_ws holds B*n_prev int32.
+ */
+int svtad_remap_table(const int32_t* table, int64_t batch, int64_t n_prev, const int64_t* keep_idx,
+                      int64_t n_new, int32_t* mapping_ws, int32_t* out, void* stream);
+
+/*
+ * Transposed table: table_t[j,k] = i for the entry with src(i,k) = j
+ * (global indices), -1 where no entry maps there. When several entries map to
+ * the same (j,k) one of them is kept and *collisions (device int32, caller
+ * zeroes it) counts the others. For mask-built tables table_t[j,k] equals
+ * table[j,8-k] and collisions stay 0.
+ */
+int svtad_transpose_table(const int32_t* table, int64_t n, int64_t tokens_per_batch,
+                          int32_t* table_t, int32_t* collisions, void* stream);
+
+/*
+ * Table validation (the checks of _validate_neighbor_indices,
+ * internvideo_next.py:41-70): stats[0] = number of entries that are neither
+ * -1 nor in [0, bound), stats[1] = min and stats[2] = max over the entries
+ * != -1 (INT32_MAX / INT32_MIN when there are none). stats is device int32[3];
+ * the call initialises it.
+ */
+int svtad_validate_table(const int32_t* table, int64_t n_entries, int64_t bound, int32_t* stats,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVTAD_SPARSE_H */

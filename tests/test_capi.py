@@ -1,0 +1,154 @@
+"""CPU checks of the C-ABI library and the extension module (no GPU compute).
+
+* libsvtad_sparse.so loads and exports every function include/svtad_sparse.h
+  declares.
+* Argument errors are rejected on the host, before any launch, with a message.
+* The torch extension exposes the reference's five functions plus the additions.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "eccv26_tad_amd", "libsvtad_sparse.so")
+HEADER = os.path.join(ROOT, "include", "svtad_sparse.h")
+
+I64 = ctypes.c_int64
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(svtad_\w+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail("libsvtad_sparse.so not built (run python -m eccv26_tad_amd.build)")
+    L = ctypes.CDLL(LIB)
+    L.svtad_last_error.restype = ctypes.c_char_p
+    L.svtad_version.restype = ctypes.c_char_p
+    L.svtad_bwd_w_workspace_bytes.restype = ctypes.c_size_t
+    L.svtad_dw_bwd_w_workspace_bytes.restype = ctypes.c_size_t
+    return L
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in svtad_sparse.h but not exported"
+
+
+def test_version(lib):
+    assert b"gfx950" in lib.svtad_version()
+
+
+def test_bad_dtype_rejected_on_host(lib):
+    st = lib.svtad_fwd(None, None, None, None, 0, None, I64(10), 8, 8, I64(0), 9, None)
+    assert st == -1
+    assert b"dtype" in lib.svtad_last_error()
+
+
+def test_bad_cin_rejected_on_host(lib):
+    st = lib.svtad_fwd(None, None, None, None, 0, None, I64(10), 6, 8, I64(0), 0, None)
+    assert st == -1
+    assert b"divisible by 4" in lib.svtad_last_error()
+
+
+def test_bias_mode_needs_pointer(lib):
+    st = lib.svtad_fwd(None, None, None, None, 1, None, I64(10), 8, 8, I64(0), 0, None)
+    assert st == -1 and b"bias" in lib.svtad_last_error()
+
+
+def test_negative_sizes_rejected(lib):
+    assert lib.svtad_bwd_in(None, None, None, None, I64(-1), 8, 8, I64(0), 0, None) == -1
+    assert lib.svtad_bwd_in(None, None, None, None, I64(4), 8, 8, I64(-3), 0, None) == -1
+
+
+def test_empty_input_is_a_noop(lib):
+    assert lib.svtad_fwd(None, None, None, None, 0, None, I64(0), 8, 8, I64(0), 1, None) == 0
+    assert lib.svtad_bwd_in(None, None, None, None, I64(0), 8, 8, I64(0), 1, None) == 0
+
+
+def test_workspace_sizes(lib):
+    for n, ci, co, dt in [(0, 8, 8, 0), (17248, 192, 192, 1), (13107, 512, 512, 2), (100, 48, 48, 3)]:
+        b = lib.svtad_bwd_w_workspace_bytes(I64(n), ci, co, dt)
+        acc = 8 if dt == 3 else 4
+        assert b >= (9 * ci * co + co) * acc
+        assert b % ((9 * ci * co + co) * acc) == 0
+    assert lib.svtad_dw_bwd_w_workspace_bytes(I64(17248), 192, 1) >= 10 * 192 * 4
+
+
+def test_workspace_too_small_rejected(lib):
+    buf = ctypes.create_string_buffer(16)
+    st = lib.svtad_bwd_w(None, None, None, buf, None, buf, ctypes.c_size_t(16), I64(0), 8, 8,
+                         I64(0), 0, None)
+    assert st == -2 and b"workspace" in lib.svtad_last_error()
+
+
+def test_table_limits_rejected(lib):
+    st = lib.svtad_table_scan(ctypes.create_string_buffer(8), I64(1), 200, 200,
+                              ctypes.create_string_buffer(8), None)
+    assert st == -3 and b"16384" in lib.svtad_last_error()
+
+
+def test_extension_module_api():
+    import eccv26_tad_amd  # noqa: F401
+    import opentad_sparse_ops as ops
+
+    for name in ("fwd", "bwd_in", "bwd_w", "implicit_gemm_fwd_v2", "implicit_gemm_fwd_v2_chunked"):
+        assert hasattr(ops, name)
+    for name in ("fwd_bias", "bwd_w_bias", "dw_fwd", "dw_bwd_in", "dw_bwd_w",
+                 "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
+                 "validate_neighbor_table"):
+        assert hasattr(ops, name)
+    import torch
+
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        ops.fwd(torch.zeros(4, 8), torch.zeros(4, 9, dtype=torch.int32), torch.zeros(9, 8, 8), 8, 0)
+
+
+def test_wrapper_module_shapes_and_init():
+    import math
+
+    import torch
+
+    from eccv26_tad_amd import SparseConv2d, SparseDepthwiseConv2d
+
+    torch.manual_seed(0)
+    m = SparseConv2d(48, 32)
+    assert m.weight.shape == (9, 48, 32) and m.bias.shape == (32,)
+    bound = 1 / math.sqrt(48 * 9)
+    assert float(m.weight.abs().max()) <= bound + 1e-7
+    assert float(m.bias.abs().max()) <= bound + 1e-7
+    assert set(m.state_dict()) == {"weight", "bias"}
+    assert SparseConv2d(16, 16, bias=False).bias is None
+    d = SparseDepthwiseConv2d(12)
+    assert d.weight.shape == (9, 12)
+
+
+def test_cin_not_divisible_by_4_raises():
+    import torch
+
+    from eccv26_tad_amd import SparseConv2dFunction
+
+    with pytest.raises(ValueError, match="divisible by 4"):
+        SparseConv2dFunction.apply(torch.zeros(2, 6), torch.zeros(2, 9, dtype=torch.int32),
+                                   torch.zeros(9, 6, 4), None, 0, 0)
+
+
+def test_legacy_weight_remap():
+    import torch
+
+    from eccv26_tad_amd import remap_legacy_sparse_conv_weights
+
+    legacy = torch.arange(8 * 9 * 4, dtype=torch.float32).view(8, 9, 4)
+    sd = {"blk.sparse_conv.weight": legacy, "other": torch.zeros(3)}
+    model = {"blk.sparse_conv.weight": torch.zeros(9, 8, 4), "other": torch.zeros(3)}
+    out = remap_legacy_sparse_conv_weights(sd, model)
+    assert out["blk.sparse_conv.weight"].shape == (9, 8, 4)
+    assert torch.equal(out["blk.sparse_conv.weight"][2, 5], legacy[5, 2])

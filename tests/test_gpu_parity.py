@@ -1,0 +1,434 @@
+"""GPU parity: the HIP kernels (through opentad_sparse_ops / the C ABI) against
+the CPU oracle on the same seeded inputs.
+
+Bar: bit-exact for the neighbor tables (integer work); max-scaled error
+max|got-ref|/max|ref| <= 1e-5 for fp32, <= 1e-2 for fp16/bf16, <= 1e-12 for
+fp64, against the fp64 oracle fed the same (rounded) inputs.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from tests.helpers import kaiming_weight, random_mask, topk_mask
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"float32": 1e-5, "float16": 1e-2, "bfloat16": 1e-2, "float64": 1e-12}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible")
+    import eccv26_tad_amd  # noqa: F401
+
+    return torch.device("cuda:0")
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _t(a, dev, dtype):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(dtype)
+
+
+def _np32(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _dt(name):
+    import torch
+
+    return getattr(torch, name)
+
+
+# ---------------------------------------------------------------------------
+# neighbor tables (bit-exact)
+# ---------------------------------------------------------------------------
+
+TABLE_SHAPES = [(1, 1, 1, 1), (1, 1, 3, 4), (2, 3, 14, 14), (2, 80, 14, 14), (4, 8, 16, 16),
+                (1, 2, 33, 17), (1, 1, 128, 128)]
+
+
+@pytest.mark.parametrize("shape", TABLE_SHAPES)
+@pytest.mark.parametrize("keep", [0.0, 0.1, 0.55, 1.0])
+def test_build_table_bit_exact(dev, oracle, shape, keep):
+    import opentad_sparse_ops as ops
+    import torch
+
+    _say("build_table", shape, keep)
+    rng = np.random.default_rng(hash((shape, keep)) & 0xffff)
+    mask = random_mask(rng, *shape, keep)
+    got = ops.build_neighbor_table(torch.from_numpy(mask).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got, oracle.build_table(mask))
+
+
+def test_build_table_bool_mask_and_initial(dev, oracle):
+    import torch
+
+    from eccv26_tad_amd import build_neighbor_table, get_initial_neighbor_indices
+
+    m = torch.ones(2, 3, 5, 7, dtype=torch.bool, device=dev)
+    np.testing.assert_array_equal(build_neighbor_table(m).cpu().numpy(),
+                                  oracle.ref_initial_table(5, 7, 3, 2).reshape(-1, 9))
+    init = get_initial_neighbor_indices(5, 7, 3, dev, 2, dtype=torch.int64)
+    assert init.dtype == torch.int64 and init.shape == (2, 105, 9)
+    np.testing.assert_array_equal(init.cpu().numpy(), oracle.ref_initial_table(5, 7, 3, 2))
+
+
+@pytest.mark.parametrize("sorted_keep", [True, False])
+def test_remap_bit_exact(dev, oracle, sorted_keep):
+    import torch
+
+    from eccv26_tad_amd import remap_neighbor_table
+
+    rng = np.random.default_rng(3)
+    B, T, H, W = 2, 16, 14, 14
+    table = oracle.ref_initial_table(H, W, T, B)
+    for keep_rate in (0.7, 0.5):
+        n_prev = table.shape[1]
+        k = math.ceil(keep_rate * n_prev)
+        if sorted_keep:
+            idx = oracle.ref_topk_sorted(rng.random((B, n_prev)), k)
+        else:
+            idx = np.stack([rng.permutation(n_prev)[:k] for _ in range(B)])
+        got = remap_neighbor_table(torch.from_numpy(table).to(dev), torch.from_numpy(idx).to(dev))
+        ref = oracle.ref_remap(table, idx)
+        np.testing.assert_array_equal(got.cpu().numpy(), ref)
+        table = ref
+
+
+def test_remap_int64_table(dev, oracle):
+    import torch
+
+    from eccv26_tad_amd import remap_neighbor_table
+
+    table = oracle.ref_initial_table(6, 6, 2, 2).astype(np.int64)
+    idx = oracle.ref_topk_sorted(np.random.default_rng(1).random((2, 72)), 30)
+    got = remap_neighbor_table(torch.from_numpy(table).to(dev), torch.from_numpy(idx).to(dev))
+    assert got.dtype == torch.int64
+    np.testing.assert_array_equal(got.cpu().numpy(), oracle.ref_remap(table, idx))
+
+
+def test_transpose_table(dev, oracle):
+    import torch
+
+    from eccv26_tad_amd import transpose_neighbor_table
+
+    mask = random_mask(np.random.default_rng(2), 2, 4, 14, 14, 0.4)
+    t = oracle.build_table(mask)
+    tt, coll = transpose_neighbor_table(torch.from_numpy(t).to(dev))
+    assert coll == 0
+    np.testing.assert_array_equal(tt.cpu().numpy(), t[:, ::-1])
+    dup = np.full((3, 9), -1, np.int32)
+    dup[:, 4] = [0, 0, 0]  # three entries map to (0, 4)
+    tt, coll = transpose_neighbor_table(torch.from_numpy(dup).to(dev))
+    assert coll == 2 and tt.cpu().numpy()[0, 4] in (0, 1, 2)
+
+
+def test_validate_table(dev, oracle):
+    import torch
+
+    from eccv26_tad_amd import validate_neighbor_table
+
+    t = oracle.ref_initial_table(4, 4, 2, 2)
+    tt = torch.from_numpy(t).to(dev)
+    validate_neighbor_table(tt, 32)
+    with pytest.raises(RuntimeError, match="second dim"):
+        validate_neighbor_table(tt, 31)
+    bad = t.copy()
+    bad[1, 3, 2] = 64
+    with pytest.raises(RuntimeError, match="out of bounds"):
+        validate_neighbor_table(torch.from_numpy(bad).to(dev), 32)
+
+
+# ---------------------------------------------------------------------------
+# convolution: forward / bwd_in / bwd_w / bias grad
+# ---------------------------------------------------------------------------
+
+def _conv_case(seed, shape, keep, ci, co, dtype, bias=True, clustered=False):
+    rng = np.random.default_rng(seed)
+    mask = topk_mask(rng, *shape, keep) if not clustered else random_mask(rng, *shape, keep)
+    n = int(mask.sum())
+    x = rng.standard_normal((n, ci)).astype(np.float32)
+    w = kaiming_weight(rng, ci, co)
+    b = rng.uniform(-0.5, 0.5, co).astype(np.float32) if bias else None
+    go = rng.standard_normal((n, co)).astype(np.float32)
+    return mask, x, w, b, go
+
+
+def _rounded(a, dt):
+    """Inputs rounded to the test dtype, back in fp32 (what the GPU sees)."""
+    import torch
+
+    return torch.from_numpy(a).to(dt).to(torch.float32).numpy()
+
+
+CONV_CASES = [
+    # (shape B,T,H,W), keep, C_in, C_out, dtype
+    ((1, 8, 14, 14), 0.5, 48, 48, "float32"),      # config 1
+    ((1, 8, 14, 14), 0.5, 48, 48, "float64"),
+    ((2, 4, 14, 14), 0.3, 64, 64, "float16"),
+    ((2, 4, 14, 14), 0.55, 192, 192, "float16"),   # config 2 channels
+    ((2, 4, 14, 14), 0.55, 192, 192, "bfloat16"),
+    ((2, 3, 16, 16), 0.25, 256, 256, "bfloat16"),  # config 4 channels
+    ((1, 2, 16, 16), 0.1, 512, 512, "bfloat16"),   # config 5 channels
+    ((1, 3, 7, 9), 0.6, 12, 20, "float32"),        # C_in % 8 != 0, odd C_out
+    ((1, 3, 7, 9), 0.6, 20, 36, "float16"),
+    ((2, 2, 14, 14), 1.0, 128, 96, "float16"),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}x{c[3]}-{c[4]}")
+def test_conv_fwd_bwd_vs_oracle(dev, oracle, case):
+    import opentad_sparse_ops as ops
+
+    shape, keep, ci, co, dname = case
+    _say("conv", case)
+    dt = _dt(dname)
+    mask, x, w, b, go = _conv_case(7, shape, keep, ci, co, dname)
+    x, w, b, go = (_rounded(a, dt) for a in (x, w, b, go))
+    t = oracle.build_table(mask)
+    X, W, Bb, G = (_t(a, dev, dt) for a in (x, w, b, go))
+    T = _t(t, dev, _dt("int32"))
+    tol = TOL[dname]
+    y = ops.implicit_gemm_fwd_v2(X, T, W, Bb, 0)
+    assert oracle.rel_err(_np32(y) if dname != "float64" else y.cpu().numpy(), oracle.fwd(x, t, w, b)) <= tol
+    y0 = ops.fwd(X, T, W, co, 0)
+    assert oracle.rel_err(y0.cpu().double().numpy(), oracle.fwd(x, t, w)) <= tol
+    gi = ops.bwd_in(G, T, W, x.shape[0], ci, 0)
+    assert gi.dtype == dt and gi.shape == (x.shape[0], ci)
+    assert oracle.rel_err(gi.cpu().double().numpy(), oracle.bwd_in(go, t, w)) <= tol
+    gw, gb = ops.bwd_w_bias(G, X, T, ci, 0, True)
+    assert gw.dtype == dt and gw.shape == (9, ci, co)
+    assert oracle.rel_err(gw.cpu().double().numpy(), oracle.bwd_w(go, x, t)) <= tol
+    assert oracle.rel_err(gb.cpu().double().numpy(), oracle.bias_grad(go)) <= tol
+    gw2 = ops.bwd_w(G, X, T, ci, 0)
+    assert oracle.rel_err(gw2.cpu().double().numpy(), oracle.bwd_w(go, x, t)) <= tol
+
+
+@pytest.mark.parametrize("dname", ["float32", "float16"])
+def test_local_indices_tokens_per_batch(dev, oracle, dname):
+    """Local indices with tokens_per_batch = 37 (not a multiple of 32, B = 3)."""
+    import opentad_sparse_ops as ops
+
+    dt = _dt(dname)
+    rng = np.random.default_rng(9)
+    B, nb = 3, 37
+    mask = np.zeros((B, 49), np.uint8)
+    for b in range(B):
+        mask[b, rng.permutation(49)[:nb]] = 1
+    mask = mask.reshape(B, 1, 7, 7)
+    t = oracle.build_table(mask)
+    local = t.copy()
+    for b in range(B):
+        blk = local[b * nb:(b + 1) * nb]
+        blk[blk >= 0] -= b * nb
+    ci = co = 16
+    x = _rounded(rng.standard_normal((B * nb, ci)).astype(np.float32), dt)
+    w = _rounded(kaiming_weight(rng, ci, co), dt)
+    go = _rounded(rng.standard_normal((B * nb, co)).astype(np.float32), dt)
+    X, W, G = (_t(a, dev, dt) for a in (x, w, go))
+    L = _t(local, dev, _dt("int32"))
+    tol = TOL[dname]
+    assert oracle.rel_err(_np32(ops.fwd(X, L, W, co, nb)), oracle.fwd(x, t, w)) <= tol
+    assert oracle.rel_err(_np32(ops.bwd_in(G, L, W, B * nb, ci, nb)), oracle.bwd_in(go, t, w)) <= tol
+    assert oracle.rel_err(_np32(ops.bwd_w(G, X, L, ci, nb)), oracle.bwd_w(go, x, t)) <= tol
+
+
+@pytest.mark.parametrize("dname", ["float32", "float16", "bfloat16"])
+def test_asymmetric_table_orphans(dev, oracle, dname):
+    """Tables that are not transposition-symmetric (duplicates, one-way links,
+    out-of-range entries) go through the orphan pass of bwd_in."""
+    import opentad_sparse_ops as ops
+
+    dt = _dt(dname)
+    rng = np.random.default_rng(13)
+    n, ci, co = 150, 32, 24
+    t = rng.integers(-1, n, size=(n, 9)).astype(np.int32)
+    t[rng.random((n, 9)) < 0.3] = -1
+    t[5, 2] = n + 40   # out of range -> missing
+    t[6, 3] = -7       # negative non-sentinel -> missing
+    x = _rounded(rng.standard_normal((n, ci)).astype(np.float32), dt)
+    w = _rounded(kaiming_weight(rng, ci, co), dt)
+    go = _rounded(rng.standard_normal((n, co)).astype(np.float32), dt)
+    X, W, G = (_t(a, dev, dt) for a in (x, w, go))
+    T = _t(t, dev, _dt("int32"))
+    tol = TOL[dname] * (1 if dname == "float32" else 2)
+    assert oracle.rel_err(_np32(ops.fwd(X, T, W, co, 0)), oracle.fwd(x, t, w)) <= tol
+    assert oracle.rel_err(_np32(ops.bwd_in(G, T, W, n, ci, 0)), oracle.bwd_in(go, t, w)) <= tol
+    assert oracle.rel_err(_np32(ops.bwd_w(G, X, T, ci, 0)), oracle.bwd_w(go, x, t)) <= tol
+
+
+def test_empty_and_isolated(dev, oracle):
+    import opentad_sparse_ops as ops
+    import torch
+
+    W = torch.randn(9, 16, 8, device=dev)
+    y = ops.fwd(torch.empty(0, 16, device=dev), torch.empty(0, 9, dtype=torch.int32, device=dev), W, 8, 0)
+    assert y.shape == (0, 8)
+    gw, gb = ops.bwd_w_bias(torch.empty(0, 8, device=dev), torch.empty(0, 16, device=dev),
+                            torch.empty(0, 9, dtype=torch.int32, device=dev), 16, 0, True)
+    assert float(gw.abs().max()) == 0.0 and float(gb.abs().max()) == 0.0
+    mask = np.zeros((1, 2, 6, 6), np.uint8)
+    mask[:, :, ::2, ::2] = 1
+    t = oracle.build_table(mask)
+    x = np.random.default_rng(0).standard_normal((t.shape[0], 16)).astype(np.float32)
+    y = ops.fwd(_t(x, dev, torch.float32), _t(t, dev, torch.int32), W, 8, 0)
+    ref = x.astype(np.float64) @ W[4].double().cpu().numpy()
+    assert oracle.rel_err(_np32(y), ref) <= 1e-5
+
+
+def test_chunked_api_matches(dev, oracle):
+    import opentad_sparse_ops as ops
+    import torch
+
+    mask, x, w, b, go = _conv_case(17, (1, 4, 14, 14), 0.5, 128, 128, "float16")
+    t = oracle.build_table(mask)
+    X, W, Bb = (_t(a, dev, torch.float16) for a in (x, w, b))
+    T = _t(t, dev, torch.int32)
+    y1 = ops.implicit_gemm_fwd_v2(X, T, W, Bb, 0)
+    y2 = ops.implicit_gemm_fwd_v2_chunked(X, T, W, Bb, 0, 4096)
+    y3 = ops.implicit_gemm_fwd_v2_chunked(X, T, W, torch.Tensor(), 0, 100)
+    assert torch.equal(y1, y2)
+    y4 = ops.fwd(X, T, W, 128, 0)
+    assert torch.equal(y3, y4)
+
+
+# ---------------------------------------------------------------------------
+# autograd wrapper (drop-in SparseConv2d)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ci,dname,autocast", [(48, "float32", False), (192, "float32", True),
+                                                (64, "float32", True), (256, "bfloat16", False)])
+def test_sparse_conv2d_module(dev, oracle, ci, dname, autocast):
+    import torch
+
+    from eccv26_tad_amd import SparseConv2d, build_neighbor_table
+
+    torch.manual_seed(0)
+    rng = np.random.default_rng(21)
+    B, T, H, W = 2, 4, 14, 14
+    mask = topk_mask(rng, B, T, H, W, 0.4)
+    table = build_neighbor_table(torch.from_numpy(mask).to(dev), batched=True)  # global, [B, N, 9]
+    nb = table.shape[1]
+    dt = _dt(dname)
+    m = SparseConv2d(ci, ci).to(dev).to(dt)
+    x = torch.randn(B, nb, ci, device=dev, dtype=dt, requires_grad=True)
+    go = torch.randn(B, nb, ci, device=dev, dtype=dt)
+    with torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+        y = m(x, table)
+    y.backward(go)
+    run_dt = torch.float16 if autocast else dt
+    xr = x.detach().to(run_dt).float().cpu().numpy().reshape(-1, ci)
+    wr = m.weight.detach().to(run_dt).float().cpu().numpy()
+    br = m.bias.detach().to(run_dt).float().cpu().numpy()
+    gr = go.to(run_dt).float().cpu().numpy().reshape(-1, ci)
+    t = table.reshape(-1, 9).cpu().numpy()
+    tol = TOL["float16" if autocast else dname]
+    assert y.dtype == run_dt
+    assert oracle.rel_err(_np32(y).reshape(-1, ci), oracle.fwd(xr, t, wr, br)) <= tol
+    assert oracle.rel_err(_np32(x.grad).reshape(-1, ci), oracle.bwd_in(gr, t, wr)) <= tol
+    assert m.weight.grad.dtype == m.weight.dtype
+    assert oracle.rel_err(_np32(m.weight.grad), oracle.bwd_w(gr, xr, t)) <= tol
+    assert oracle.rel_err(_np32(m.bias.grad), oracle.bias_grad(gr)) <= tol
+
+
+def test_module_local_table_heuristic(dev, oracle):
+    """A [B, N, 9] table of local indices makes the wrapper pass tokens_per_batch = N."""
+    import torch
+
+    from eccv26_tad_amd import SparseConv2d
+
+    rng = np.random.default_rng(4)
+    B, T, H, W = 3, 1, 9, 9
+    mask = np.zeros((B, 81), np.uint8)
+    for b in range(B):
+        mask[b, rng.permutation(81)[:30]] = 1
+    t = oracle.build_table(mask.reshape(B, T, H, W))
+    local = t.reshape(B, 30, 9).copy()
+    for b in range(B):
+        blk = local[b]
+        blk[blk >= 0] -= b * 30
+    m = SparseConv2d(16, 16).to(dev)
+    x = torch.randn(B, 30, 16, device=dev)
+    y_local = m(x, torch.from_numpy(local).to(dev))
+    y_global = m(x, torch.from_numpy(t.reshape(B, 30, 9)).to(dev))
+    assert torch.allclose(y_local, y_global, rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------------------
+# depthwise
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dname", ["float32", "float16", "bfloat16", "float64"])
+def test_depthwise_vs_oracle(dev, oracle, dname):
+    import opentad_sparse_ops as ops
+
+    dt = _dt(dname)
+    rng = np.random.default_rng(31)
+    mask = topk_mask(rng, 2, 4, 14, 14, 0.55)
+    n, c = int(mask.sum()), 192
+    t = oracle.build_table(mask)
+    x = _rounded(rng.standard_normal((n, c)).astype(np.float32), dt)
+    w = _rounded(rng.standard_normal((9, c)).astype(np.float32) * 0.3, dt)
+    b = _rounded(rng.standard_normal(c).astype(np.float32), dt)
+    go = _rounded(rng.standard_normal((n, c)).astype(np.float32), dt)
+    X, W, Bb, G = (_t(a, dev, dt) for a in (x, w, b, go))
+    T = _t(t, dev, _dt("int32"))
+    tol = TOL[dname]
+    y = ops.dw_fwd(X, T, W, Bb, 0)
+    assert oracle.rel_err(y.cpu().double().numpy(), oracle.dw_fwd(x, t, w, b)) <= tol
+    gi = ops.dw_bwd_in(G, T, W, 0)
+    assert oracle.rel_err(gi.cpu().double().numpy(), oracle.dw_bwd_in(go, t, w)) <= tol
+    gw, gb = ops.dw_bwd_w(G, X, T, 0, True)
+    assert oracle.rel_err(gw.cpu().double().numpy(), oracle.dw_bwd_w(go, x, t)) <= tol
+    assert oracle.rel_err(gb.cpu().double().numpy(), oracle.bias_grad(go)) <= tol
+
+
+def test_depthwise_module_grad(dev, oracle):
+    import torch
+
+    from eccv26_tad_amd import SparseDepthwiseConv2d
+
+    rng = np.random.default_rng(5)
+    mask = random_mask(rng, 1, 3, 8, 8, 0.5)
+    t = oracle.build_table(mask)
+    n = t.shape[0]
+    m = SparseDepthwiseConv2d(24).to(dev)
+    x = torch.randn(n, 24, device=dev, requires_grad=True)
+    y = m(x, torch.from_numpy(t).to(dev))
+    go = torch.randn_like(y)
+    y.backward(go)
+    w = m.weight.detach().cpu().numpy()
+    xn, gn = x.detach().cpu().numpy(), go.cpu().numpy()
+    assert oracle.rel_err(_np32(y), oracle.dw_fwd(xn, t, w, m.bias.detach().cpu().numpy())) <= 1e-5
+    assert oracle.rel_err(_np32(x.grad), oracle.dw_bwd_in(gn, t, w)) <= 1e-5
+    assert oracle.rel_err(_np32(m.weight.grad), oracle.dw_bwd_w(gn, xn, t)) <= 1e-5
+
+
+# ---------------------------------------------------------------------------
+# determinism
+# ---------------------------------------------------------------------------
+
+def test_backward_is_deterministic(dev, oracle):
+    import opentad_sparse_ops as ops
+    import torch
+
+    mask, x, w, b, go = _conv_case(41, (2, 8, 14, 14), 0.5, 192, 192, "float16")
+    t = oracle.build_table(mask)
+    X, W, G = (_t(a, dev, torch.float16) for a in (x, w, go))
+    T = _t(t, dev, torch.int32)
+    a1 = ops.bwd_in(G, T, W, x.shape[0], 192, 0)
+    a2 = ops.bwd_in(G, T, W, x.shape[0], 192, 0)
+    w1 = ops.bwd_w(G, X, T, 192, 0)
+    w2 = ops.bwd_w(G, X, T, 192, 0)
+    assert torch.equal(a1, a2) and torch.equal(w1, w2)
