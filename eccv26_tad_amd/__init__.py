@@ -1,7 +1,7 @@
 """MI355X-native SparseConv2D for SV-TAD (pcr-upm/eccv26_tad).
 
 Importing the package loads the in-tree native extension ``opentad_sparse_ops``
-(built by ``python -m eccv26_tad_amd.build``) and registers it under its
+(built by ``python eccv26_tad_amd/build.py``) and registers it under its
 top-level name, so reference code doing ``import opentad_sparse_ops`` gets
 this build. There is no CPU or Python fallback: a missing extension raises.
 """
@@ -23,7 +23,7 @@ def _load_extension():
     if not os.path.exists(path):
         raise ImportError(
             f"eccv26_tad_amd: native extension not built ({path} missing); "
-            "run `python -m eccv26_tad_amd.build`")
+            "run `python eccv26_tad_amd/build.py`")
     spec = importlib.util.spec_from_file_location("opentad_sparse_ops", path)
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)

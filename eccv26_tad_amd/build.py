@@ -6,7 +6,8 @@
   host C++ compiled by g++ against torch's headers), linked to
   ``libsvtad_sparse.so`` with an ``$ORIGIN`` rpath.
 
-Run ``python -m eccv26_tad_amd.build`` (or ``__graft_entry__.build()``).
+Run ``python eccv26_tad_amd/build.py`` (or ``__graft_entry__.build()``); the
+file is run by path because importing the package needs the built extension.
 """
 from __future__ import annotations
 

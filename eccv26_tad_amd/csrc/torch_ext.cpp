@@ -274,6 +274,7 @@ at::Tensor op_build_neighbor_table(const at::Tensor& mask_in) {
                  "build_neighbor_table");
     const int64_t n = offs[frames].item<int32_t>();  // host sync: sizes the output
     at::Tensor table = at::empty({n, 9}, mask.options().dtype(at::kInt));
+    if (n == 0) return table;
     check_status(svtad_table_fill(mask.data_ptr<uint8_t>(), offs.data_ptr<int32_t>(), frames, (int)h,
                                   (int)w, table.data_ptr<int32_t>(), s),
                  "build_neighbor_table");
