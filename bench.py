@@ -1,0 +1,355 @@
+"""SparseConv2D fwd+bwd benchmark on one MI355X.
+
+Workload (the ViT-B adapter bottleneck): B=2 samples x 80
+temporal slices x 14x14 grid, C_in = C_out = 192, fp16, 3x3 sparse conv with
+bias. Keep sets: per sample top-k of a seeded U(0,1) score (k = ceil(r*15680)),
+sorted; the neighbor table is built on the GPU from the keep mask.
+
+One step = the work of one training step of the op, exactly what
+SparseConv2dFunction.forward/backward run: forward (bias added in fp32),
+backward-input, backward-weight with the bias gradient. Inputs are resident in
+HBM before the timed region.
+
+Printed: ONE JSON line on stdout. ``value`` is the algorithmic HBM throughput
+of fwd+bwd (GB/s) at the headline keep rate; ``sweep`` holds us / GB/s /
+TFLOP/s / speedup over a dense 3x3 conv (MIOpen, same shape) for every keep
+rate; ``roofline`` covers the dominant kernel, timed with HIP events on the
+stream it is launched on; ``cpu_baseline`` times the OpenMP fp32 port of the
+reference dataflow (oracle/, kind "port") on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "f32": 157.3, "f64": 78.6}
+KEEPS = (0.10, 0.25, 0.40, 0.55, 0.70, 1.00)
+B, T, H, W, C = 2, 80, 14, 14, 192
+SEED = 1002  # 1000 + config id
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_mask(keep: float):
+    """[B, T, H, W] uint8 keep mask: per sample top-k (k = ceil(keep*T*H*W)) of a
+    seeded U(0,1) score, the keep-set rule of vit_sparse_adapter_poguise.py:763,785-787."""
+    import torch
+
+    g = torch.Generator().manual_seed(SEED)
+    n = T * H * W
+    k = math.ceil(keep * n)
+    score = torch.rand(B, n, generator=g)
+    idx = torch.topk(score, k, dim=1).indices
+    m = torch.zeros(B, n, dtype=torch.uint8)
+    m.scatter_(1, idx, 1)
+    return m.view(B, T, H, W)
+
+
+def op_bytes(n, ci, co, s):
+    """Algorithmic HBM bytes of each pass (unique compulsory traffic):
+    activations read/written once per pass, the int32 table (36 B/row) once per
+    pass, the weight once per pass, bias / bias grad."""
+    wsz = 9 * ci * co
+    fwd = n * ci * s + n * co * s + 36 * n + wsz * s + 4 * co
+    bwd_in = n * co * s + n * ci * s + 36 * n + wsz * s
+    bwd_w = n * co * s + n * ci * s + 36 * n + wsz * s + co * s
+    return {"fwd": fwd, "bwd_in": bwd_in, "bwd_w": bwd_w}
+
+
+def time_events(fn, reps, warm=3):
+    """Average ms per call of fn() from HIP events on torch's current stream,
+    the stream the extension launches on."""
+    import torch
+
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+class Problem:
+    def __init__(self, keep, dev, dtype):
+        import torch
+
+        import eccv26_tad_amd as sv
+
+        self.ops = sv.ops
+        self.keep = keep
+        self.mask = make_mask(keep).to(dev)
+        self.table = sv.build_neighbor_table(self.mask)
+        self.n = int(self.table.shape[0])
+        g = torch.Generator().manual_seed(SEED + 1)
+        bound = 1.0 / math.sqrt(9 * C)
+        self.x = torch.randn(self.n, C, generator=g).to(dev, dtype)
+        self.w = ((torch.rand(9, C, C, generator=g) * 2 - 1) * bound).to(dev, dtype)
+        self.b = ((torch.rand(C, generator=g) * 2 - 1) * bound).to(dev, dtype)
+        self.go = torch.randn(self.n, C, generator=g).to(dev, dtype)
+        self.valid = int((self.table >= 0).sum())
+
+    def fwd(self):
+        return self.ops.fwd_bias(self.x, self.table, self.w, self.b, 0, 1)
+
+    def bwd_in(self):
+        return self.ops.bwd_in(self.go, self.table, self.w, self.n, C, 0)
+
+    def bwd_w(self):
+        return self.ops.bwd_w_bias(self.go, self.x, self.table, C, 0, True)
+
+    def step(self):
+        y = self.fwd()
+        gi = self.bwd_in()
+        gw, gb = self.bwd_w()
+        return y, gi, gw, gb
+
+
+def dense_ms(dev, dtype, reps):
+    """Dense 3x3 conv (MIOpen) fwd + input grad + weight grad + bias grad on the
+    full [B*T, C, H, W] grid; best of NCHW and channels_last."""
+    import torch
+    import torch.nn.functional as F
+
+    torch.backends.cudnn.benchmark = True
+    g = torch.Generator().manual_seed(SEED + 2)
+    best = None
+    for fmt in (torch.contiguous_format, torch.channels_last):
+        x = torch.randn(B * T, C, H, W, generator=g).to(dev, dtype).contiguous(memory_format=fmt)
+        x.requires_grad_(True)
+        w = (torch.randn(C, C, 3, 3, generator=g) * 0.02).to(dev, dtype).contiguous(memory_format=fmt)
+        w.requires_grad_(True)
+        b = torch.zeros(C, device=dev, dtype=dtype, requires_grad=True)
+        dy = torch.randn(B * T, C, H, W, generator=g).to(dev, dtype).contiguous(memory_format=fmt)
+
+        def run():
+            y = F.conv2d(x, w, b, padding=1)
+            gx, gw, gb = torch.autograd.grad(y, (x, w, b), dy)
+            return gx
+
+        t = time_events(run, reps, warm=5)
+        best = t if best is None else min(best, t)
+    return best
+
+
+def cpu_baseline(budget_s: float):
+    """The OpenMP fp32 port of the reference dataflow (oracle/sv_oracle.c,
+    svo_fwd_f32 / svo_bwd_in_f32 / svo_bwd_w_f32) on the host cores, on the
+    same workload at the headline keep rate, repeated until about budget_s."""
+    import numpy as np
+
+    from oracle import sv_oracle
+
+    sv_oracle.lib()
+    keep = 0.55
+    mask = make_mask(keep).numpy()
+    table = sv_oracle.build_table(mask)
+    n = table.shape[0]
+    rng = np.random.default_rng(SEED)
+    x = rng.standard_normal((n, C), dtype=np.float32)
+    w = (rng.random((9, C, C), dtype=np.float32) * 2 - 1) / math.sqrt(9 * C)
+    b = (rng.random(C, dtype=np.float32) * 2 - 1) / math.sqrt(9 * C)
+    go = rng.standard_normal((n, C), dtype=np.float32)
+    port = sv_oracle.Fp32Port(n, C, C)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        port.fwd(x, table, w, b)
+        port.bwd(go, x, table, w)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 50:
+            break
+    per = el / steps
+    by = sum(op_bytes(n, C, C, 4).values())
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(by / per / 1e9, 3), "unit": "GB/s",
+        "cores": sv_oracle.num_threads(), "kind": "port",
+        "sample": (f"fp32 fwd+bwd of the same config-2 workload at keep {keep} (N={n}), "
+                   f"{steps} step(s) in {el:.1f} s, {per * 1e3:.1f} ms/step; "
+                   f"host {cpu} ({platform.machine()})"),
+        "ms_per_step": round(per * 1e3, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--keep", type=float, default=0.55, help="headline keep rate")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only; the SparseConv2D path has no "
+              "collective (multi-GPU sharding is described, not run). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    dtype, dname, s = torch.float16, "f16", 2
+
+    log(f"bench: building problem keep={args.keep}")
+    prob = Problem(args.keep, dev, dtype)
+    n = prob.n
+    by = op_bytes(n, C, C, s)
+    total_bytes = sum(by.values())
+    flops_9n = 3 * 2 * 9 * n * C * C
+    flops_useful = 3 * 2 * prob.valid * C * C
+
+    # table build (mask already resident): scan + fill
+    import eccv26_tad_amd as sv
+
+    table_ms = time_events(lambda: sv.build_neighbor_table(prob.mask), 20)
+
+    # timed fwd+bwd steps
+    log(f"bench: N={n}, warmup {args.warmup}, steps {args.steps}")
+    for _ in range(args.warmup):
+        prob.step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(args.steps):
+        prob.step()
+    e_ev.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = s_ev.elapsed_time(e_ev) / args.steps
+    log(f"bench: {ms * 1e3:.1f} us/step (wall {wall / args.steps * 1e3:.1f} us/step)")
+
+    # HIP graph replay of the same step
+    graph_ms = None
+    try:
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            for _ in range(3):
+                ref = prob.step()
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            outs = prob.step()
+        for _ in range(3):
+            gr.replay()
+            torch.cuda.synchronize()
+            eager = prob.step()
+            torch.cuda.synchronize()
+            for a, b in zip(outs, eager):
+                if not torch.equal(a, b):
+                    raise RuntimeError("graph replay differs from eager")
+        graph_ms = time_events(gr.replay, args.steps)
+        del gr
+    except Exception as exc:  # reported, not fatal
+        log(f"bench: graph replay skipped: {exc}")
+
+    # per-pass timing; the dominant pass names the roofline kernel
+    phases = {p: time_events(getattr(prob, p), max(args.steps, 20)) for p in ("fwd", "bwd_in", "bwd_w")}
+    dom = max(phases, key=phases.get)
+    f_pass = 2 * 9 * n * C * C
+    t_dom = phases[dom] * 1e-3
+    mfma_t = f_pass / (MFMA_PEAK_TFLOPS[dname] * 1e12)
+    hbm_t = by[dom] / (HBM_PEAK_GBS * 1e9)
+    if mfma_t >= hbm_t:
+        roof = {"bound": "mfma", "achieved": round(f_pass / t_dom / 1e12, 3),
+                "peak": MFMA_PEAK_TFLOPS[dname], "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": round(by[dom] / t_dom / 1e9, 3),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s"}
+    roof["frac"] = round(roof["achieved"] / roof["peak"], 5)
+    roof["traffic"] = None
+    roof["kernel_pass"] = dom
+    roof["pass_us"] = round(phases[dom] * 1e3, 2)
+
+    dense = None if args.no_dense else dense_ms(dev, dtype, 20)
+
+    sweep = []
+    if not args.no_sweep:
+        for kr in KEEPS:
+            p = prob if abs(kr - args.keep) < 1e-9 else Problem(kr, dev, dtype)
+            t = time_events(p.step, 20)
+            b2 = sum(op_bytes(p.n, C, C, s).values())
+            f9 = 3 * 2 * 9 * p.n * C * C
+            fu = 3 * 2 * p.valid * C * C
+            row = {"keep": kr, "n": p.n, "hit_rate": round(p.valid / (9 * p.n), 4),
+                   "us": round(t * 1e3, 2), "gbs": round(b2 / (t * 1e-3) / 1e9, 1),
+                   "tflops_9n": round(f9 / (t * 1e-3) / 1e12, 2),
+                   "roofline_frac": round(max(b2 / (HBM_PEAK_GBS * 1e9),
+                                              fu / (MFMA_PEAK_TFLOPS[dname] * 1e12)) / (t * 1e-3), 4)}
+            if dense is not None:
+                row["speedup_vs_dense"] = round(dense / t, 3)
+            sweep.append(row)
+            if p is not prob:
+                del p
+            log(f"bench: sweep {row}")
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    out = {
+        "metric": "SparseConv2D fwd+bwd µs & HBM GB/s (% roofline), speedup vs dense @10-55% keep",
+        "value": round(total_bytes / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_step": round(ms * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dname,
+        "data": "synthetic (seeded top-k keep masks, N(0,1) activations, uniform weights)",
+        "config": {"workload": "SparseConv2D fwd+bwd, ViT-B adapter bottleneck (BASELINE config 2)",
+                   "grid": f"B{B} x T{T} x {H}x{W}", "channels": C, "keep": args.keep, "n_kept": n,
+                   "hit_rate": round(prob.valid / (9 * n), 4), "bias": True},
+        "hbm_frac": round(total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "tflops_9n": round(flops_9n / (ms * 1e-3) / 1e12, 3),
+        "tflops_useful": round(flops_useful / (ms * 1e-3) / 1e12, 3),
+        "roofline_frac": round(max(total_bytes / (HBM_PEAK_GBS * 1e9),
+                                   flops_useful / (MFMA_PEAK_TFLOPS[dname] * 1e12)) / (ms * 1e-3), 4),
+        "graph_us_per_step": round(graph_ms * 1e3, 2) if graph_ms else None,
+        "pass_us": {k: round(v * 1e3, 2) for k, v in phases.items()},
+        "table_build_us": round(table_ms * 1e3, 2),
+        "dense_us": round(dense * 1e3, 2) if dense is not None else None,
+        "speedup_vs_dense": round(dense / ms, 3) if dense is not None else None,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
