@@ -31,8 +31,8 @@ HIP_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
-    # packed fp32 VALU ops stay off ("Build")
+    # packed fp32 VALU ops stay off: some of their forms have given wrong
+    # results on this hardware, so the compiler must not form them
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]
@@ -47,9 +47,21 @@ def _run(cmd, **kw):
     return out
 
 
-def hip_cmd():
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    return [HIPCC, *HIP_FLAGS, *srcs, "-o", LIB + ".tmp"]
+def hip_sources():
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def obj_path(src):
+    return os.path.join(PKG, "_build", os.path.basename(src) + ".o")
+
+
+def hip_compile_cmd(src):
+    return [HIPCC, *HIP_FLAGS, "-c", src, "-o", obj_path(src)]
+
+
+def hip_link_cmd():
+    return [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC",
+            *[obj_path(s) for s in hip_sources()], "-o", LIB + ".tmp"]
 
 
 def ext_cmd():
@@ -75,10 +87,19 @@ def build(verbose: bool = False) -> None:
     """Compile the HIP library, then the torch extension against it."""
     import torch  # noqa: F401  (fails early if torch is absent)
 
+    from concurrent.futures import ThreadPoolExecutor
+
     abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
-    out = _run(hip_cmd(), cwd=ROOT)
-    if verbose and out.strip():
-        print(out)
+    os.makedirs(os.path.join(PKG, "_build"), exist_ok=True)
+    srcs = hip_sources()
+    # one hipcc per source file, in parallel (the MFMA file dominates)
+    with ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 4)) as ex:
+        outs = list(ex.map(lambda src: _run(hip_compile_cmd(src), cwd=ROOT), srcs))
+    out = _run(hip_link_cmd(), cwd=ROOT)
+    if verbose:
+        for o in outs + [out]:
+            if o.strip():
+                print(o)
     os.replace(LIB + ".tmp", LIB)
     cmd = ext_cmd()
     cmd = [c if not c.startswith("-D_GLIBCXX_USE_CXX11_ABI") else f"-D_GLIBCXX_USE_CXX11_ABI={abi}"

@@ -11,6 +11,8 @@
 namespace svtad {
 
 static bool dtype_ok(int d) { return d >= SVTAD_F32 && d <= SVTAD_F64; }
+// The MFMA kernels read operands as 16-byte vectors.
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 static size_t acc_bytes(int d) { return d == SVTAD_F64 ? 8 : 4; }
 
 static int check_common(const char* who, int64_t n, int c_in, int c_out, int64_t tpb, int dtype) {
@@ -37,16 +39,27 @@ static int check_common(const char* who, int64_t n, int c_in, int c_out, int64_t
     return SVTAD_OK;
 }
 
-// Full conv plan: MFMA partials when the MFMA kernel handles the shape.
+// Full conv plan. Rows are split so that the partial-tile workgroups fill the
+// chip (about 256 of them) without splits shorter than 256 rows, and so that
+// no split is longer than 2048 rows.
 static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     BwPlan p;
-    p.path = bw_mfma_supported(dtype, c_in, c_out) ? 1 : 0;
-    const int64_t tiles = p.path ? 9 * cdiv(c_in, 64) * cdiv(c_out, 64) : 9 * cdiv(c_in, 64) * cdiv(c_out, 64);
-    const int64_t target_wg = 1024;
-    int64_t splits = std::max<int64_t>(1, cdiv(target_wg, tiles));
-    splits = std::min<int64_t>(splits, std::max<int64_t>(1, n / 128));
+    p.path = bw_mfma_supported(dtype, n, c_in, c_out) ? 1 : 0;
+    int tm = 64, tn = 64;
+    if (p.path) bw_mfma_tiles(c_in, c_out, &tm, &tn);
+    const int64_t tiles = 9 * cdiv(c_in, tm) * cdiv(c_out, tn);
+    int64_t splits;
+    if (p.path) {
+        splits = std::max<int64_t>(cdiv(n, kMaxSplitRows - 128),
+                                   std::min<int64_t>(cdiv(256, tiles), cdiv(n, 256)));
+    } else {
+        splits = std::min<int64_t>(cdiv(1024, tiles), std::max<int64_t>(1, n / 128));
+    }
+    splits = std::max<int64_t>(1, splits);
     int64_t rps = cdiv(std::max<int64_t>(n, 1), splits);
-    rps = cdiv(rps, 32) * 32;
+    // whole pairs of 64-row stages: a split's row list (at most
+    // kMaxSplitRows) is read two 64-row stages per iteration by the MFMA kernel
+    rps = cdiv(rps, 128) * 128;
     splits = std::max<int64_t>(1, cdiv(n, rps));
     p.splits = (int)splits;
     p.rows_per_split = rps;
@@ -73,22 +86,37 @@ static BwPlan plan_dw_bw(int64_t n, int c, int dtype) {
 
 using namespace svtad;
 
+extern "C" size_t svtad_fwd_workspace_bytes(int c_in, int c_out, int dtype) {
+    if (!dtype_ok(dtype) || c_in <= 0 || c_out <= 0) return 0;
+    return gg_mfma_workspace(dtype, c_in, c_out);
+}
+
+extern "C" size_t svtad_bwd_in_workspace_bytes(int c_in, int c_out, int dtype) {
+    if (!dtype_ok(dtype) || c_in <= 0 || c_out <= 0) return 0;
+    return gg_mfma_workspace(dtype, c_out, c_in);
+}
+
 extern "C" int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, const void* bias,
-                         int bias_mode, void* out, int64_t n, int c_in, int c_out,
-                         int64_t tokens_per_batch, int dtype, void* stream) {
+                         int bias_mode, void* out, void* workspace, size_t workspace_bytes,
+                         int64_t n, int c_in, int c_out, int64_t tokens_per_batch, int dtype,
+                         void* stream) {
     int st = check_common("fwd", n, c_in, c_out, tokens_per_batch, dtype);
     if (st) return st;
     if (c_in % 4 != 0) return set_error(SVTAD_ERR_INVALID, "fwd: C_in must be divisible by 4");
-    if (bias_mode < SVTAD_BIAS_NONE || bias_mode > SVTAD_BIAS_AFTER)
+    if (bias_mode < SVTAD_BIAS_NONE || bias_mode > SVTAD_BIAS_PRE)
         return set_error(SVTAD_ERR_INVALID, "fwd: bad bias_mode");
     if (bias_mode != SVTAD_BIAS_NONE && !bias)
         return set_error(SVTAD_ERR_INVALID, "fwd: bias_mode needs a bias pointer");
+    const size_t need = gg_mfma_workspace(dtype, c_in, c_out);
+    if (need && (!workspace || workspace_bytes < need))
+        return set_error(SVTAD_ERR_WORKSPACE, "fwd: workspace smaller than svtad_fwd_workspace_bytes()");
     if (n == 0) return SVTAD_OK;
     if (!x || !nbr || !weight || !out) return set_error(SVTAD_ERR_INVALID, "fwd: null pointer");
     hipStream_t s = (hipStream_t)stream;
-    if (gg_mfma_supported(dtype, c_in, c_out))
+    if (gg_mfma_supported(dtype, c_in, c_out) && al16(x) && al16(weight) && al16(out) &&
+        (!need || al16(workspace)))
         gg_mfma(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
-                tokens_per_batch, s);
+                tokens_per_batch, need ? workspace : nullptr, s);
     else
         gg_valu(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
                 tokens_per_batch, s);
@@ -96,18 +124,22 @@ extern "C" int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, 
 }
 
 extern "C" int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight,
-                            void* grad_in, int64_t n, int c_in, int c_out, int64_t tokens_per_batch,
-                            int dtype, void* stream) {
+                            void* grad_in, void* workspace, size_t workspace_bytes, int64_t n,
+                            int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
     int st = check_common("bwd_in", n, c_in, c_out, tokens_per_batch, dtype);
     if (st) return st;
+    const size_t need = gg_mfma_workspace(dtype, c_out, c_in);
+    if (need && (!workspace || workspace_bytes < need))
+        return set_error(SVTAD_ERR_WORKSPACE, "bwd_in: workspace smaller than svtad_bwd_in_workspace_bytes()");
     if (n == 0) return SVTAD_OK;
     if (!grad_out || !nbr || !weight || !grad_in)
         return set_error(SVTAD_ERR_INVALID, "bwd_in: null pointer");
     hipStream_t s = (hipStream_t)stream;
     // gi[j, ci] = sum_k sum_co go[src_t(j,k), co] * w[k][ci][co]
-    if (gg_mfma_supported(dtype, c_out, c_in))
+    if (gg_mfma_supported(dtype, c_out, c_in) && al16(grad_out) && al16(weight) && al16(grad_in) &&
+        (!need || al16(workspace)))
         gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
-                tokens_per_batch, s);
+                tokens_per_batch, need ? workspace : nullptr, s);
     else
         gg_valu(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
                 tokens_per_batch, s);
@@ -125,9 +157,10 @@ extern "C" int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* n
                            int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
     int st = check_common("bwd_w", n, c_in, c_out, tokens_per_batch, dtype);
     if (st) return st;
-    const BwPlan p = plan_bw(n, c_in, c_out, dtype);
+    BwPlan p = plan_bw(n, c_in, c_out, dtype);
     if (!grad_w || !workspace || (n > 0 && (!grad_out || !x || !nbr)))
         return set_error(SVTAD_ERR_INVALID, "bwd_w: null pointer");
+    if (p.path == 1 && !(al16(grad_out) && al16(x))) p.path = 0;  // same workspace layout
     if (workspace_bytes < p.ws_bytes)
         return set_error(SVTAD_ERR_WORKSPACE, "bwd_w: workspace smaller than svtad_bwd_w_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;

@@ -1,14 +1,1088 @@
-// MFMA (matrix core) SparseConv2D kernels for f16 / bf16.
+// MFMA (matrix core) SparseConv2D kernels for f16 / bf16 on gfx950.
+//
+// All three GEMM shapes of the op run on v_mfma_f32_16x16x32_{f16,bf16}
+// (fp32 accumulate):
+//   forward      out[m, n]    = sum_k sum_c x[src(m,k), c]   * w[k][c][n]
+//   bwd-input    gi[m, n]     = sum_k sum_c go[src_t(m,k), c] * w[k][n][c]
+//   bwd-weight   gw[k][ci][co] = sum_i x[src(i,k), ci] * go[i, co]
+// Operand tiles are staged through LDS with the reduction index contiguous
+// ([row][32 k-values], pitch 40 elements = 80 bytes, so the 16 lanes that
+// read one fragment column hit 16 distinct 16-byte slots), which makes every
+// MFMA fragment a single 16-byte LDS read. Operands whose reduction index is
+// strided in HBM (w in the forward, both operands of bwd-weight) are
+// transposed while being written into LDS. Two LDS buffers alternate so the
+// global loads of step t+1 are in flight while step t runs on the matrix
+// cores.
+//
+// MFMA lane layout used (16x16 output tile, 64 lanes): lane l supplies row
+// l%16 of A and column l%16 of B with 8 reduction values at slot l/16; it
+// receives C[(l/16)*4 + j][l%16], j = 0..3. A and B use the same slot
+// mapping, so the pairing of reduction values matches by construction.
 #include "sv_common.h"
 #include "sv_conv.h"
 
 namespace svtad {
 
-bool gg_mfma_supported(int, int, int) { return false; }
-void gg_mfma(int, int, const void*, const int32_t*, const void*, const void*, int, void*, int64_t,
-             int, int, int64_t, hipStream_t) {}
-bool bw_mfma_supported(int, int, int) { return false; }
-void bw_mfma(int, const BwPlan&, const void*, const void*, const int32_t*, void*, void*, void*,
-             int64_t, int, int, int64_t, hipStream_t) {}
+typedef unsigned short u16;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <typename T> struct MfmaOp;
+template <> struct MfmaOp<f16> {
+    static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                      __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+    }
+};
+template <> struct MfmaOp<bf16> {
+    static __device__ __forceinline__ f32x4 run(u32x4 a, u32x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                       __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    }
+};
+
+constexpr int KS = 32;     // reduction values per step
+constexpr int PITCH = 40;  // LDS row pitch in 16-bit elements
+
+__device__ __forceinline__ u16 half_of(const u32x4& v, int j) {
+    const unsigned w = v[j >> 1];
+    return (u16)((j & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// Buffer loads: a raw buffer resource over [base, base + bytes); a load whose
+// offset is at or beyond `bytes` returns zeros without touching memory, so
+// missing neighbors and tile edges need neither branches nor a zero row.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOOB = 0x80000000u;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Workgroup -> tile mapping that keeps consecutive tiles on one XCD.
+// Workgroups are dispatched round-robin over the 8 XCDs (wg b runs on XCD
+// b % 8); tile t = (XCD-major rank of b) so XCD x owns a contiguous range of
+// tiles and the rows those tiles gather stay in its L2.
+__device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t g) {
+    const int64_t q = g >> 3, r = g & 7, x = b & 7, j = b >> 3;
+    return x * q + (x < r ? x : r) + j;
+}
+
+// ---------------------------------------------------------------------------
+// Gathered GEMM (forward / backward-input)
+// ---------------------------------------------------------------------------
+template <typename T, int MODE, int WGM, int WGN, int FM, int FN>
+__global__ __launch_bounds__(WGM* WGN * 64) void k_gg_mfma(
+    const T* __restrict__ src, const int32_t* __restrict__ nbr, const T* __restrict__ w,
+    const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n, int c_red,
+    int n_out, int64_t tpb, int n_col_tiles, int64_t n_tiles) {
+    constexpr int NT = WGM * WGN * 64;
+    constexpr int BM = WGM * FM * 16;
+    constexpr int BN = WGN * FN * 16;
+    constexpr int A_CHUNKS = BM * 4;                  // 16-byte chunks of an A tile
+    constexpr int A_PER = (A_CHUNKS + NT - 1) / NT;
+    constexpr int B_ITEMS = MODE == MODE_FWD ? 2 * BN : BN * 4;
+    constexpr int B_PER = (B_ITEMS + NT - 1) / NT;
+
+    __shared__ __align__(16) u16 As[2][BM][PITCH];
+    __shared__ __align__(16) u16 Bs[2][BN][PITCH];
+    __shared__ int32_t sidx[9][BM];
+    __shared__ int kvalid[9];
+    __shared__ int klist[9];
+    __shared__ int nk_s;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int64_t tile = xcd_tile(blockIdx.x, n_tiles);
+    const int64_t row0 = (tile / n_col_tiles) * BM;
+    const int col0 = (int)(tile % n_col_tiles) * BN;
+
+    if (tid < 9) kvalid[tid] = 0;
+    __syncthreads();
+    for (int e = tid; e < 9 * BM; e += NT) {
+        const int k = e / BM, m = e - k * BM;
+        const int64_t i = row0 + m;
+        int64_t r = -1;
+        if (i < n) r = MODE == MODE_FWD ? src_row(nbr, i, k, n, tpb) : src_row_t(nbr, i, k, n, tpb);
+        sidx[k][m] = (int32_t)r;
+        if (r >= 0) kvalid[k] = 1;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int c = 0;
+        for (int k = 0; k < 9; ++k)
+            if (kvalid[k]) klist[c++] = k;
+        nk_s = c;
+    }
+    __syncthreads();
+    const int nc = (c_red + KS - 1) / KS;
+    const int steps = nk_s * nc;
+
+    u32x4 ra[A_PER];
+    u32x4 rb[B_PER][MODE == MODE_FWD ? 2 : 1];
+    const u32x4 zero = {0u, 0u, 0u, 0u};
+
+    auto load = [&](int t) {
+        const int k = klist[t / nc];
+        const int c0 = (t % nc) * KS;
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = tid + q * NT;
+            u32x4 v = zero;
+            if (e < A_CHUNKS) {
+                const int m = e >> 2, part = e & 3;
+                const int32_t r = sidx[k][m];
+                const int c = c0 + part * 8;
+                if (r >= 0 && c < c_red) v = *(const u32x4*)(src + (int64_t)r * c_red + c);
+            }
+            ra[q] = v;
+        }
+        const T* wk = w + (int64_t)k * c_red * n_out;
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) {
+            const int e = tid + q * NT;
+            if constexpr (MODE == MODE_FWD) {
+                // w[k][c][n]: rows c (reduction), n contiguous; two rows per item
+                u32x4 v0 = zero, v1 = zero;
+                if (e < B_ITEMS) {
+                    const int cp = e & 15, g = e >> 4;
+                    const int c = c0 + 2 * cp, nn = col0 + g * 8;
+                    if (c < c_red && nn < n_out) {
+                        v0 = *(const u32x4*)(wk + (int64_t)c * n_out + nn);
+                        v1 = *(const u32x4*)(wk + (int64_t)(c + 1) * n_out + nn);
+                    }
+                }
+                rb[q][0] = v0;
+                if constexpr (MODE == MODE_FWD) rb[q][1] = v1;
+            } else {
+                // w[k][n][c] seen as B[c][n]: rows n with c contiguous
+                u32x4 v = zero;
+                if (e < B_ITEMS) {
+                    const int nl = e >> 2, part = e & 3;
+                    const int nn = col0 + nl, c = c0 + part * 8;
+                    if (nn < n_out && c < c_red) v = *(const u32x4*)(wk + (int64_t)nn * c_red + c);
+                }
+                rb[q][0] = v;
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = tid + q * NT;
+            if (e < A_CHUNKS) *(u32x4*)&As[buf][e >> 2][(e & 3) * 8] = ra[q];
+        }
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) {
+            const int e = tid + q * NT;
+            if (e >= B_ITEMS) continue;
+            if constexpr (MODE == MODE_FWD) {
+                const int cp = e & 15, g = e >> 4;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const unsigned lo = half_of(rb[q][0], j);
+                    const unsigned hi = half_of(rb[q][1], j);
+                    *(unsigned*)&Bs[buf][g * 8 + j][2 * cp] = lo | (hi << 16);
+                }
+            } else {
+                *(u32x4*)&Bs[buf][e >> 2][(e & 3) * 8] = rb[q][0];
+            }
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int arow = wm * FM * 16 + (lane & 15);
+    const int brow = wn * FN * 16 + (lane & 15);
+    const int kof = (lane >> 4) * 8;
+
+    if (steps > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < steps; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < steps) load(t + 1);
+        u32x4 fa[FM], fb[FN];
+#pragma unroll
+        for (int a = 0; a < FM; ++a) fa[a] = *(const u32x4*)&As[buf][arow + a * 16][kof];
+#pragma unroll
+        for (int b = 0; b < FN; ++b) fb[b] = *(const u32x4*)&Bs[buf][brow + b * 16][kof];
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fa[a], fb[b], acc[a][b]);
+        if (t + 1 < steps) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds C[(lane/16)*4 + j][lane%16] of each 16x16 tile
+#pragma unroll
+    for (int b = 0; b < FN; ++b) {
+        const int col = col0 + wn * FN * 16 + b * 16 + (lane & 15);
+        if (col >= n_out) continue;
+        float bv = 0.f;
+        if (bias_mode == SVTAD_BIAS_FP32) bv = ((const float*)bias)[col];
+        else if (bias_mode != SVTAD_BIAS_NONE) bv = (float)((const T*)bias)[col];
+#pragma unroll
+        for (int a = 0; a < FM; ++a) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t i = row0 + wm * FM * 16 + a * 16 + (lane >> 4) * 4 + j;
+                if (i >= n) continue;
+                const float v = acc[a][b][j];
+                T o;
+                if (bias_mode == SVTAD_BIAS_PRE || bias_mode == SVTAD_BIAS_FP32) o = (T)(v + bv);
+                else if (bias_mode == SVTAD_BIAS_AFTER) o = (T)((float)(T)v + bv);
+                else o = (T)v;
+                out[i * n_out + col] = o;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Wide gathered GEMM (forward / backward-input) for reduction widths CR in
+// {64, 128, 192, 256, 512}: a workgroup owns BM = FM*16 rows and BN = 4*FN*16
+// output columns; each of its 4 waves owns FN*16 of the columns and all BM
+// rows. Per neighbor offset k, the BM gathered source rows (all CR values)
+// are staged once in LDS (two slices alternate, the next slice's loads are in
+// flight while the current one is consumed); B fragments come straight from
+// global memory (L2-resident weights), D steps ahead in a register ring.
+//   B operand for both modes: the weight in MFMA fragment order (k_pack_frag).
+// ---------------------------------------------------------------------------
+template <typename T, int MODE, int CR, int FM, int FN, int D, int WS>
+__global__ __launch_bounds__(256 * WS) void k_gg_wide(
+    const T* __restrict__ src, const int32_t* __restrict__ nbr, const T* __restrict__ wb,
+    const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n, int n_out,
+    int64_t tpb, int n_col_tiles, int64_t n_tiles) {
+    // WS wave sets of 4 waves share the tile; set h takes the offsets
+    // klist[h], klist[h + WS], ... so WS independent load streams are in
+    // flight per workgroup. The sets' accumulators are summed through LDS.
+    constexpr int BM = FM * 16;
+    constexpr int BN = 4 * FN * 16;
+    constexpr int NC = CR / KS;
+    constexpr int RP = CR + 8;  // LDS row pitch (elements): odd multiple of 16 bytes
+    constexpr int CPR = CR / 8;  // 16-byte chunks per row
+    constexpr int A_CHUNKS = BM * CPR;
+    constexpr int A_PER = (A_CHUNKS + 255) / 256;
+    static_assert(NC % D == 0, "ring depth must divide the steps of a slice");
+    static_assert(WS == 1 || (size_t)BM * BN * 4 <= sizeof(u16) * 2 * BM * RP,
+                  "the partial accumulators of a set must fit in its A buffers");
+
+    __shared__ __align__(16) u16 As[WS][2][BM][RP];
+    __shared__ uint32_t soff[9][BM];  // byte offset of the gathered row, kOOB if missing
+    __shared__ int kvalid[9];
+    __shared__ int klist[10];
+    __shared__ int nk_s;
+
+    const int tid = threadIdx.x;
+    const int set = tid >> 8, ltid = tid & 255;
+    const int lane = tid & 63, wave = ltid >> 6;
+    const int64_t tile = xcd_tile(blockIdx.x, n_tiles);
+    const int64_t row0 = (tile / n_col_tiles) * BM;
+    const int col0 = (int)(tile % n_col_tiles) * BN;
+
+    if (tid < 9) kvalid[tid] = 0;
+    __syncthreads();
+    for (int e = tid; e < 9 * BM; e += 256 * WS) {
+        const int k = e / BM, m = e - k * BM;
+        const int64_t i = row0 + m;
+        int64_t r = -1;
+        if (i < n) r = MODE == MODE_FWD ? src_row(nbr, i, k, n, tpb) : src_row_t(nbr, i, k, n, tpb);
+        soff[k][m] = r >= 0 ? (uint32_t)r * (uint32_t)(CR * 2) : kOOB;
+        if (r >= 0) kvalid[k] = 1;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int c = 0;
+        for (int k = 0; k < 9; ++k)
+            if (kvalid[k]) klist[c++] = k;
+        for (int q = c; q < 10; ++q) klist[q] = klist[c > 0 ? c - 1 : 0];
+        nk_s = c;
+    }
+    __syncthreads();
+    const int nk = nk_s;
+    const int nk_set = nk > set ? (nk - set + WS - 1) / WS : 0;  // slices of this set
+    const int iters = (nk + WS - 1) / WS;
+    const int steps = nk_set * NC;
+
+    const rsrc_t rs_src = make_rsrc(src, (uint32_t)(n * CR * 2));
+    const rsrc_t rs_w = make_rsrc(wb, (uint32_t)(9 * NC * ((n_out + 15) / 16)) * 1024u);
+
+    // A slice: the BM gathered rows of one offset, 16-byte chunk e = ltid + q*256
+    u32x4 ra[A_PER];
+    auto load_a = [&](int it) {
+        const bool live = it < nk_set;
+        const int k = klist[live ? it * WS + set : 0];
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = ltid + q * 256;
+            const int m = e < A_CHUNKS ? e / CPR : 0;
+            ra[q] = bload16(rs_src, live && e < A_CHUNKS ? soff[k][m] + (uint32_t)((e - m * CPR) * 16) : kOOB);
+        }
+    };
+    auto store_a = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = ltid + q * 256;
+            if (e < A_CHUNKS) *(u32x4*)&As[set][buf][e / CPR][(e - (e / CPR) * CPR) * 8] = ra[q];
+        }
+    };
+
+    // B fragments come from the fragment-ordered weight wf (k_pack_frag): the
+    // 64 lanes of fragment (k, c-step, column block) are 1 KB contiguous, so a
+    // fragment load is fully coalesced. Per-lane offsets are fixed; a step adds
+    // the wave-uniform slab offset. Steps past the set's end reload its last step.
+    const int ncol = col0 + wave * FN * 16 + (lane & 15);
+    const int kof = (lane >> 4) * 8;
+    const int nf = (n_out + 15) / 16;
+    uint32_t boff[FN];
+#pragma unroll
+    for (int f = 0; f < FN; ++f) {
+        const int blk = (col0 + wave * FN * 16) / 16 + f;
+        boff[f] = blk < nf ? (uint32_t)(blk * 64 + lane) * 16u : kOOB;
+    }
+    u32x4 ring[D][FN];
+    auto load_b = [&](int s, u32x4* rb) {
+        const int sc = s < steps ? s : (steps > 0 ? steps - 1 : 0);
+        const int it = sc / NC;
+        const uint32_t so = (uint32_t)((klist[it * WS + set] * NC + (sc - it * NC)) * nf) * 1024u;
+#pragma unroll
+        for (int f = 0; f < FN; ++f) rb[f] = bload16(rs_w, boff[f] + so);
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load_a(0);
+    store_a(0);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_b(d, ring[d]);
+    __syncthreads();
+
+    const int arow = lane & 15;
+    for (int it = 0; it < iters; ++it) {
+        const int buf = it & 1;
+        const bool live = it < nk_set;  // uniform per wave set
+        load_a(it + 1);
+        if (live) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int d = c % D;
+                u32x4 fa[FM];
+#pragma unroll
+                for (int a = 0; a < FM; ++a) fa[a] = *(const u32x4*)&As[set][buf][a * 16 + arow][c * KS + kof];
+#pragma unroll
+                for (int a = 0; a < FM; ++a)
+#pragma unroll
+                    for (int f = 0; f < FN; ++f) acc[a][f] = MfmaOp<T>::run(fa[a], ring[d][f], acc[a][f]);
+                load_b(it * NC + c + D, ring[d]);
+            }
+        }
+        store_a(buf ^ 1);
+        __syncthreads();
+    }
+
+    if constexpr (WS > 1) {
+        // sets 1.. add their partial sums into set 0's through LDS (fixed order)
+        float* red = (float*)&As[0][0][0][0];
+        for (int h = 1; h < WS; ++h) {
+            if (set == h) {
+#pragma unroll
+                for (int f = 0; f < FN; ++f)
+#pragma unroll
+                    for (int a = 0; a < FM; ++a)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            red[(a * 16 + (lane >> 4) * 4 + j) * BN + wave * FN * 16 + f * 16 + (lane & 15)] = acc[a][f][j];
+            }
+            __syncthreads();
+            if (set == 0) {
+#pragma unroll
+                for (int f = 0; f < FN; ++f)
+#pragma unroll
+                    for (int a = 0; a < FM; ++a)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            acc[a][f][j] += red[(a * 16 + (lane >> 4) * 4 + j) * BN + wave * FN * 16 + f * 16 + (lane & 15)];
+            }
+            __syncthreads();
+        }
+    }
+
+    // epilogue: round (with the bias) into an LDS copy of the output tile, then
+    // write whole 16-byte chunks so each output row goes out as one run
+    constexpr int OP = BN + 8;
+    static_assert((size_t)BM * OP * 2 <= sizeof(u16) * 2 * BM * RP, "output tile must fit in the A buffers");
+    u16* ot = &As[0][0][0][0];
+    if (WS == 1) __syncthreads();  // all waves are done reading the A buffers
+    if (set == 0) {
+#pragma unroll
+        for (int f = 0; f < FN; ++f) {
+            const int lc = wave * FN * 16 + f * 16 + (lane & 15);
+            const int col = col0 + lc;
+            float bv = 0.f;
+            if (col < n_out) {
+                if (bias_mode == SVTAD_BIAS_FP32) bv = ((const float*)bias)[col];
+                else if (bias_mode != SVTAD_BIAS_NONE) bv = (float)((const T*)bias)[col];
+            }
+#pragma unroll
+            for (int a = 0; a < FM; ++a) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float v = acc[a][f][j];
+                    T o;
+                    if (bias_mode == SVTAD_BIAS_PRE || bias_mode == SVTAD_BIAS_FP32) o = (T)(v + bv);
+                    else if (bias_mode == SVTAD_BIAS_AFTER) o = (T)((float)(T)v + bv);
+                    else o = (T)v;
+                    ot[(a * 16 + (lane >> 4) * 4 + j) * OP + lc] = __builtin_bit_cast(u16, o);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    constexpr int CH = BN / 8;
+    for (int e = tid; e < BM * CH; e += 256 * WS) {
+        const int r = e / CH, c8 = e - (e / CH) * CH;
+        const int64_t i = row0 + r;
+        const int col = col0 + c8 * 8;
+        if (i < n && col < n_out) *(u32x4*)(out + i * n_out + col) = *(const u32x4*)&ot[r * OP + c8 * 8];
+    }
+}
+
+// Weight in MFMA fragment order for the gathered GEMMs. For reduction step cs
+// (32 values) and column block nb (16 columns), the 64 lanes' B fragments are
+// stored contiguously: wf[((k*NCS + cs)*NB + nb)*64 + lane][e] =
+//   B(k, c = cs*32 + (lane/16)*8 + e, n = nb*16 + lane%16), 0 past n_out,
+// with B(k,c,n) = w[k][c][n] for the forward (c over c_in, n over c_out) and
+// w[k][n][c] for backward-input (c over c_out, n over c_in). One thread per
+// 16-byte fragment slot; grid cdiv(9*NCS*NB*64, 256).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_pack_frag(const u16* __restrict__ w, u16* __restrict__ wf,
+                                                   int c_red, int n_out) {
+    const int ncs = c_red / KS, nb = (n_out + 15) / 16;
+    const int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (slot >= (int64_t)9 * ncs * nb * 64) return;
+    const int lane = (int)(slot & 63);
+    int64_t q = slot >> 6;
+    const int b = (int)(q % nb);
+    q /= nb;
+    const int cs = (int)(q % ncs);
+    const int k = (int)(q / ncs);
+    const int n = b * 16 + (lane & 15);
+    const int c = cs * KS + (lane >> 4) * 8;
+    const u16* wk = w + (int64_t)k * c_red * n_out;
+    u16 v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        u16 x = 0;
+        if (n < n_out) x = MODE == MODE_FWD ? wk[(int64_t)(c + e) * n_out + n] : wk[(int64_t)n * c_red + c + e];
+        v[e] = x;
+    }
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = (unsigned)v[2 * j] | ((unsigned)v[2 * j + 1] << 16);
+    *(u32x4*)(wf + slot * 8) = o;
+}
+
+// ---------------------------------------------------------------------------
+// Backward-weight partials: ws[s][k][ci][co] = sum over rows i of split s of
+// x[src(i,k), ci] * go[i, co]; ws_bias[s][co] = sum of go[i, co] (written by
+// the k == 4, ci-tile 0 workgroups). Grid: 1-D over (tiles x splits), the
+// tiles of one split consecutive (they read the same rows).
+// Per stage the workgroup takes KR = 64 rows: x rows gathered through the
+// split's source-row list (staged in LDS once) and go rows, both written
+// transposed into LDS ([channel][row], rows contiguous) so each MFMA operand
+// fragment is one 16-byte read. Loads of stage t+1 are in flight while stage
+// t runs; a split holds at most kMaxSplitRows rows.
+// ---------------------------------------------------------------------------
+constexpr int KR = 64;
+constexpr int RPK = KR + 8;  // LDS pitch of a transposed stage: 144 bytes
+
+template <typename T, int FM, int FN>
+__global__ __launch_bounds__(256) void k_bw_mfma(
+    const T* __restrict__ go, const T* __restrict__ x, const int32_t* __restrict__ nbr,
+    float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int c_in, int c_out,
+    int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks) {
+    constexpr int BM = 2 * FM * 16;  // ci
+    constexpr int BN = 2 * FN * 16;  // co
+    constexpr int A_ITEMS = (KR / 2) * (BM / 8);
+    constexpr int B_ITEMS = (KR / 2) * (BN / 8);
+    constexpr int A_PER = (A_ITEMS + 255) / 256;
+    constexpr int B_PER = (B_ITEMS + 255) / 256;
+
+    __shared__ __align__(16) u16 As[2][BM][RPK];
+    __shared__ __align__(16) u16 Bs[2][BN][RPK];
+    __shared__ uint32_t srow[kMaxSplitRows];  // byte offset of x[src(i,k)], kOOB if missing
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int64_t lin = xcd_tile(blockIdx.x, n_blocks);
+    const int tiles = 9 * n_ci_tiles * n_co_tiles;
+    const int s = (int)(lin / tiles);
+    int rem = (int)(lin - (int64_t)s * tiles);
+    const int k = rem / (n_ci_tiles * n_co_tiles);
+    rem -= k * n_ci_tiles * n_co_tiles;
+    const int ci0 = (rem / n_co_tiles) * BM;
+    const int co0 = (rem % n_co_tiles) * BN;
+    const int64_t r_begin = (int64_t)s * rows_per_split;
+    const int rows = (int)max<int64_t>(0, min(n, r_begin + rows_per_split) - r_begin);
+    const int steps = (rows + KR - 1) / KR;
+    const bool do_bias = ws_bias != nullptr && k == 4 && ci0 == 0;
+
+    for (int r = tid; r < steps * KR; r += 256) {
+        const int64_t sr = r < rows ? src_row(nbr, r_begin + r, k, n, tpb) : -1;
+        srow[r] = sr >= 0 ? (uint32_t)sr * (uint32_t)(c_in * 2) : kOOB;
+    }
+    __syncthreads();
+
+    const rsrc_t rs_x = make_rsrc(x, (uint32_t)(n * c_in * 2));
+    const rsrc_t rs_g = make_rsrc(go + r_begin * c_out, (uint32_t)((int64_t)rows * c_out * 2));
+
+    // per-thread constants: channel byte offsets (x) and row-pair byte offsets (go)
+    bool a_ok[A_PER];
+    uint32_t a_c[A_PER];
+    uint32_t b_off[B_PER];
+#pragma unroll
+    for (int q = 0; q < A_PER; ++q) {
+        const int e = tid + q * 256;
+        const int c = ci0 + (e >> 5) * 8;
+        a_ok[q] = e < A_ITEMS && c < c_in;
+        a_c[q] = (uint32_t)c * 2u;
+    }
+#pragma unroll
+    for (int q = 0; q < B_PER; ++q) {
+        const int e = tid + q * 256;
+        const int c = co0 + (e >> 5) * 8;
+        b_off[q] = (e < B_ITEMS && c < c_out) ? (uint32_t)(2 * (e & 31) * c_out + c) * 2u : kOOB;
+    }
+
+    u32x4 ra[A_PER][2], rb[B_PER][2];
+    auto load = [&](int t) {
+        const int r0 = t * KR;
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int rp = (tid + q * 256) & 31;
+            const uint32_t s0 = srow[r0 + 2 * rp], s1 = srow[r0 + 2 * rp + 1];
+            ra[q][0] = bload16(rs_x, a_ok[q] ? s0 + a_c[q] : kOOB);
+            ra[q][1] = bload16(rs_x, a_ok[q] ? s1 + a_c[q] : kOOB);
+        }
+        // rows past the split read out of range -> 0
+        const uint32_t g0 = (uint32_t)(r0 * c_out) * 2u;
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) {
+            rb[q][0] = bload16(rs_g, b_off[q] + g0);
+            rb[q][1] = bload16(rs_g, b_off[q] + g0 + (uint32_t)c_out * 2u);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = tid + q * 256;
+            if (e >= A_ITEMS) continue;
+            const int rp = e & 31, g = e >> 5;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                *(unsigned*)&As[buf][g * 8 + j][2 * rp] =
+                    (unsigned)half_of(ra[q][0], j) | ((unsigned)half_of(ra[q][1], j) << 16);
+        }
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) {
+            const int e = tid + q * 256;
+            if (e >= B_ITEMS) continue;
+            const int rp = e & 31, g = e >> 5;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                *(unsigned*)&Bs[buf][g * 8 + j][2 * rp] =
+                    (unsigned)half_of(rb[q][0], j) | ((unsigned)half_of(rb[q][1], j) << 16);
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float bsum = 0.f;
+
+    const int wm = wave >> 1, wn = wave & 1;
+    const int arow = wm * FM * 16 + (lane & 15);
+    const int brow = wn * FN * 16 + (lane & 15);
+    const int kof = (lane >> 4) * 8;
+
+    if (steps > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < steps; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < steps) load(t + 1);
+#pragma unroll
+        for (int h = 0; h < KR / KS; ++h) {
+            u32x4 fa[FM], fb[FN];
+#pragma unroll
+            for (int a = 0; a < FM; ++a) fa[a] = *(const u32x4*)&As[buf][arow + a * 16][h * KS + kof];
+#pragma unroll
+            for (int b = 0; b < FN; ++b) fb[b] = *(const u32x4*)&Bs[buf][brow + b * 16][h * KS + kof];
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fa[a], fb[b], acc[a][b]);
+        }
+        if (do_bias && tid < BN) {
+#pragma unroll
+            for (int r = 0; r < KR; r += 2) {
+                const unsigned pr = *(const unsigned*)&Bs[buf][tid][r];
+                bsum += (float)__builtin_bit_cast(T, (u16)(pr & 0xffffu));
+                bsum += (float)__builtin_bit_cast(T, (u16)(pr >> 16));
+            }
+        }
+        if (t + 1 < steps) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    float* dst = ws + ((int64_t)s * 9 + k) * c_in * c_out;
+#pragma unroll
+    for (int b = 0; b < FN; ++b) {
+        const int co = co0 + wn * FN * 16 + b * 16 + (lane & 15);
+        if (co >= c_out) continue;
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int ci = ci0 + wm * FM * 16 + a * 16 + (lane >> 4) * 4 + j;
+                if (ci < c_in) dst[(int64_t)ci * c_out + co] = acc[a][b][j];
+            }
+    }
+    if (do_bias && tid < BN && co0 + tid < c_out) ws_bias[(int64_t)s * c_out + co0 + tid] = bsum;
+}
+
+// ---------------------------------------------------------------------------
+// Backward-weight partials, large tiles (the shapes of the adapter convs).
+// A workgroup owns one offset k, a BM x BN (ci x co) tile of gw and one row
+// split. Per 64-row stage it stages the gathered x rows and the go rows in
+// LDS untransposed ([row][channel], 16-byte coalesced loads with the lanes
+// along the channels) and reads the MFMA fragments with the gfx950 LDS
+// transpose load ds_read_b64_tr_b16: within each 16-lane group, lane j points
+// at 4 consecutive channels of row j/4 and lane i receives the value of
+// channel i at 4 consecutive rows, so two such reads give a lane the 8
+// consecutive rows of its fragment. Two register stages keep the loads of
+// stage t+2 in flight while stage t runs. The bias gradient is one extra MFMA
+// per column fragment against a fragment of ones (k == 4, ci-tile 0 only).
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+__device__ __forceinline__ u32x4 tr_frag(const u16* lds_row0, int pitch, int g, int i, int col0) {
+    // rows 8g + 4r + i/4, channels col0 + 4*(i%4) .. +3, r = 0, 1
+    const u16* p0 = lds_row0 + (8 * g + (i >> 2)) * pitch + col0 + 4 * (i & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 4 * pitch));
+    const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
+    return u32x4{a.x, a.y, b.x, b.y};
+}
+
+template <typename T, int FM, int FN>
+__global__ __launch_bounds__(256) void k_bw_big(
+    const T* __restrict__ go, const T* __restrict__ x, const int32_t* __restrict__ nbr,
+    float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int c_in, int c_out,
+    int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks) {
+    constexpr int BM = 2 * FM * 16;  // ci
+    constexpr int BN = 2 * FN * 16;  // co
+    constexpr int PA = BM + 8, PB = BN + 8;  // LDS pitches (elements)
+    constexpr int CA = BM / 8, CB = BN / 8;  // 16-byte chunks per staged row
+    constexpr int A_PER = (KR * CA + 255) / 256;
+    constexpr int B_PER = (KR * CB + 255) / 256;
+
+    __shared__ __align__(16) u16 As[2][KR][PA];
+    __shared__ __align__(16) u16 Bs[2][KR][PB];
+    __shared__ uint32_t srow[kMaxSplitRows];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int64_t lin = xcd_tile(blockIdx.x, n_blocks);
+    const int tiles = 9 * n_ci_tiles * n_co_tiles;
+    const int s = (int)(lin / tiles);
+    int rem = (int)(lin - (int64_t)s * tiles);
+    const int k = rem / (n_ci_tiles * n_co_tiles);
+    rem -= k * n_ci_tiles * n_co_tiles;
+    const int ci0 = (rem / n_co_tiles) * BM;
+    const int co0 = (rem % n_co_tiles) * BN;
+    const int64_t r_begin = (int64_t)s * rows_per_split;
+    const int rows = (int)max<int64_t>(0, min(n, r_begin + rows_per_split) - r_begin);
+    const int steps = (rows + KR - 1) / KR;
+    const bool do_bias = ws_bias != nullptr && k == 4 && ci0 == 0;  // uniform
+
+    for (int r = tid; r < steps * KR; r += 256) {
+        const int64_t sr = r < rows ? src_row(nbr, r_begin + r, k, n, tpb) : -1;
+        srow[r] = sr >= 0 ? (uint32_t)sr * (uint32_t)(c_in * 2) : kOOB;
+    }
+    __syncthreads();
+
+    const rsrc_t rs_x = make_rsrc(x, (uint32_t)(n * c_in * 2));
+    const rsrc_t rs_g = make_rsrc(go + r_begin * c_out, (uint32_t)((int64_t)rows * c_out * 2));
+
+    // staging slot e = tid + q*256 of a stage: row e / CA (or CB), 16-byte chunk e % CA
+    u32x4 ra0[A_PER], rb0[B_PER], ra1[A_PER], rb1[B_PER];
+    // stages at or past `steps` load zeros (out of range) so the loop body is uniform
+    auto load = [&](int t, u32x4* ra, u32x4* rb) {
+        const bool live = t < steps;
+        const int r0 = live ? t * KR : 0;
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = tid + q * 256;
+            const int r = e / CA, c = ci0 + (e - r * CA) * 8;
+            const bool ok = live && r < KR && c < c_in;
+            const uint32_t so = srow[r0 + (ok ? r : 0)];
+            ra[q] = bload16(rs_x, ok && so != kOOB ? so + (uint32_t)c * 2u : kOOB);
+        }
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) {
+            const int e = tid + q * 256;
+            const int r = e / CB, c = co0 + (e - r * CB) * 8;
+            const bool ok = live && r < KR && c < c_out;
+            rb[q] = bload16(rs_g, ok ? (uint32_t)((r0 + r) * c_out + c) * 2u : kOOB);
+        }
+    };
+    auto store = [&](int buf, const u32x4* ra, const u32x4* rb) {
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = tid + q * 256;
+            if (e < KR * CA) *(u32x4*)&As[buf][e / CA][(e % CA) * 8] = ra[q];
+        }
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) {
+            const int e = tid + q * 256;
+            if (e < KR * CB) *(u32x4*)&Bs[buf][e / CB][(e % CB) * 8] = rb[q];
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g = lane >> 4, i16 = lane & 15;
+    float bsum = 0.f;
+    auto compute = [&](int buf) {
+        if (do_bias && tid < BN) {  // column sums of the staged go rows
+#pragma unroll 8
+            for (int r = 0; r < KR; ++r) bsum += (float)__builtin_bit_cast(T, Bs[buf][r][tid]);
+        }
+#pragma unroll
+        for (int h = 0; h < KR / KS; ++h) {
+            u32x4 fb[FN];
+#pragma unroll
+            for (int b = 0; b < FN; ++b) fb[b] = tr_frag(&Bs[buf][h * KS][0], PB, g, i16, wn * FN * 16 + b * 16);
+#pragma unroll
+            for (int a = 0; a < FM; ++a) {
+                const u32x4 fa = tr_frag(&As[buf][h * KS][0], PA, g, i16, wm * FM * 16 + a * 16);
+#pragma unroll
+                for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fa, fb[b], acc[a][b]);
+            }
+        }
+    };
+
+    load(0, ra0, rb0);
+    load(1, ra1, rb1);
+    store(0, ra0, rb0);
+    __syncthreads();
+    for (int t = 0; t < steps; t += 2) {
+        load(t + 2, ra0, rb0);  // registers of set 0 are free again
+        compute(0);             // stage t
+        store(1, ra1, rb1);     // stage t+1 (zeros past the end)
+        __syncthreads();
+        load(t + 3, ra1, rb1);
+        compute(1);             // stage t+1
+        store(0, ra0, rb0);     // stage t+2
+        __syncthreads();
+    }
+
+    float* dst = ws + ((int64_t)s * 9 + k) * c_in * c_out;
+#pragma unroll
+    for (int b = 0; b < FN; ++b) {
+        const int co = co0 + wn * FN * 16 + b * 16 + i16;
+        if (co >= c_out) continue;
+#pragma unroll
+        for (int a = 0; a < FM; ++a)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int ci = ci0 + wm * FM * 16 + a * 16 + g * 4 + j;
+                if (ci < c_in) dst[(int64_t)ci * c_out + co] = acc[a][b][j];
+            }
+    }
+    if (do_bias && tid < BN && co0 + tid < c_out) ws_bias[(int64_t)s * c_out + co0 + tid] = bsum;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool gg_mfma_supported(int dtype, int c_red, int n_out) {
+    return (dtype == SVTAD_F16 || dtype == SVTAD_BF16) && c_red % 8 == 0 && n_out % 8 == 0 &&
+           c_red >= 16 && n_out >= 16;
+}
+
+// Reduction widths with a wide-kernel instantiation and its (FM, FN, D).
+struct WideCfg { int cr, fm, fn, d; };
+static const WideCfg kWide[] = {{64, 8, 1, 2}, {128, 8, 2, 4}, {192, 8, 3, 6},
+                                {256, 8, 4, 4}, {512, 4, 4, 4}};
+
+static const WideCfg* wide_cfg(int c_red, int n_out) {
+    for (const WideCfg& c : kWide)
+        if (c.cr == c_red && n_out >= (4 * c.fn * 16) / 2) return &c;
+    return nullptr;
+}
+
+size_t gg_mfma_workspace(int dtype, int c_red, int n_out) {
+    if (!gg_mfma_supported(dtype, c_red, n_out) || !wide_cfg(c_red, n_out)) return 0;
+    return (size_t)9 * c_red * cdiv(n_out, 16) * 16 * 2;
+}
+
+template <typename T, int MODE, int WGM, int WGN, int FM, int FN>
+static void launch_gg(const void* src, const int32_t* nbr, const void* w, const void* bias,
+                      int bias_mode, void* out, int64_t n, int c_red, int n_out, int64_t tpb,
+                      hipStream_t s) {
+    constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
+    const int n_col = (int)cdiv(n_out, BN);
+    const int64_t tiles = cdiv(n, BM) * n_col;
+    hipLaunchKernelGGL((k_gg_mfma<T, MODE, WGM, WGN, FM, FN>), dim3((unsigned)tiles),
+                       dim3(WGM * WGN * 64), 0, s, (const T*)src, nbr, (const T*)w, bias,
+                       bias_mode, (T*)out, n, c_red, n_out, tpb, n_col, tiles);
+}
+
+// Compute units of the current device (cached per device).
+static int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            c = 256;
+        cached[dev] = c;
+    }
+    return cached[dev];
+}
+
+template <typename T, int MODE, int CR, int FM, int FN, int D>
+static void launch_wide(const void* src, const int32_t* nbr, const void* wb, const void* bias,
+                        int bias_mode, void* out, int64_t n, int n_out, int64_t tpb, hipStream_t s) {
+    constexpr int BN = 4 * FN * 16;
+    // two wave sets when both sets' double-buffered A slices fit in LDS
+    constexpr int WS = (size_t)2 * 2 * FM * 16 * (CR + 8) * 2 <= 150 * 1024 ? 2 : 1;
+    const int n_col = (int)cdiv(n_out, BN);
+    const int64_t tiles = cdiv(n, 16 * FM) * n_col;
+    hipLaunchKernelGGL((k_gg_wide<T, MODE, CR, FM, FN, D, WS>), dim3((unsigned)tiles), dim3(256 * WS),
+                       0, s, (const T*)src, nbr, (const T*)wb, bias, bias_mode, (T*)out, n, n_out,
+                       tpb, n_col, tiles);
+}
+
+// Row fragments per workgroup: the smallest instantiated count that keeps the
+// grid within one workgroup per CU (a second wave of workgroups on a few CUs
+// would double the kernel time).
+static int pick_fm(int64_t n, int n_col, const int* have, int count) {
+    const int64_t need = cdiv(cdiv(n, 16) * n_col, cu_count());
+    for (int q = 0; q < count; ++q)
+        if (have[q] >= need) return have[q];
+    return have[count - 1];
+}
+
+template <typename T, int MODE, int CR, int FN, int D>
+static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, const void* bias,
+                           int bias_mode, void* out, int64_t n, int n_out, int64_t tpb,
+                           hipStream_t s) {
+    const int n_col = (int)cdiv(n_out, 4 * FN * 16);
+    if constexpr (CR == 192 || CR == 256) {
+        static const int have[] = {1, 2, 3, 4, 5, 6, 8};
+        switch (pick_fm(n, n_col, have, 7)) {
+            case 1: launch_wide<T, MODE, CR, 1, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+            case 2: launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+            case 3: launch_wide<T, MODE, CR, 3, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+            case 4: launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+            case 5: launch_wide<T, MODE, CR, 5, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+            case 6: launch_wide<T, MODE, CR, 6, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+            default: launch_wide<T, MODE, CR, 8, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+        }
+    } else {
+        static const int have[] = {2, 4};
+        if (pick_fm(n, n_col, have, 2) == 2)
+            launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s);
+        else
+            launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s);
+    }
+}
+
+template <typename T, int MODE>
+static void gg_dispatch(const void* src, const int32_t* nbr, const void* w, const void* bias,
+                        int bias_mode, void* out, int64_t n, int c_red, int n_out, int64_t tpb,
+                        void* ws, hipStream_t s) {
+    const WideCfg* wc = wide_cfg(c_red, n_out);
+    // buffer loads address operands with 32-bit byte offsets
+    const bool fits = n * c_red * 2 < (int64_t)INT32_MAX && 9LL * c_red * n_out * 2 < (int64_t)INT32_MAX;
+    if (wc && fits && ws) {
+        const int64_t slots = (int64_t)9 * (c_red / KS) * cdiv(n_out, 16) * 64;
+        hipLaunchKernelGGL((k_pack_frag<MODE>), dim3((unsigned)cdiv(slots, 256)), dim3(256), 0, s,
+                           (const u16*)w, (u16*)ws, c_red, n_out);
+        const void* wb = ws;
+#define SVTAD_WIDE_CASE(CR, FM, FN, D)                                                           \
+    if (wc->cr == CR) {                                                                          \
+        launch_wide_fm<T, MODE, CR, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); \
+        return;                                                                                  \
+    }
+        SVTAD_WIDE_CASE(64, 8, 1, 2)
+        SVTAD_WIDE_CASE(128, 8, 2, 4)
+        SVTAD_WIDE_CASE(192, 8, 3, 6)
+        SVTAD_WIDE_CASE(256, 8, 4, 4)
+        SVTAD_WIDE_CASE(512, 4, 4, 4)
+#undef SVTAD_WIDE_CASE
+    }
+    if (n_out % 96 == 0)
+        launch_gg<T, MODE, 2, 2, 2, 3>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s);
+    else if (n_out % 64 == 0)
+        launch_gg<T, MODE, 2, 2, 2, 2>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s);
+    else if (n_out % 48 == 0)
+        launch_gg<T, MODE, 4, 1, 1, 3>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s);
+    else
+        launch_gg<T, MODE, 4, 1, 1, 1>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s);
+}
+
+void gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+             const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
+             int64_t tpb, void* ws, hipStream_t s) {
+    if (dtype == SVTAD_F16) {
+        if (mode == MODE_FWD) gg_dispatch<f16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, s);
+        else gg_dispatch<f16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, s);
+    } else {
+        if (mode == MODE_FWD) gg_dispatch<bf16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, s);
+        else gg_dispatch<bf16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, s);
+    }
+}
+
+bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out) {
+    // buffer loads address x and go with 32-bit byte offsets
+    return (dtype == SVTAD_F16 || dtype == SVTAD_BF16) && c_in % 8 == 0 && c_out % 8 == 0 &&
+           c_in >= 16 && c_out >= 16 && n * std::max(c_in, c_out) * 2 < (int64_t)INT32_MAX;
+}
+
+// Tile edge for a bwd-weight dimension: 96 when it divides, else 64, else 32.
+int bw_mfma_tile(int c) { return c % 96 == 0 ? 96 : (c % 64 == 0 ? 64 : 32); }
+
+template <typename T, int FM, int FN>
+static void launch_bw(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                      float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
+                      hipStream_t s) {
+    constexpr int BM = 2 * FM * 16, BN = 2 * FN * 16;
+    const int nci = (int)cdiv(c_in, BM), nco = (int)cdiv(c_out, BN);
+    const int64_t blocks = (int64_t)9 * nci * nco * p.splits;
+    hipLaunchKernelGGL((k_bw_mfma<T, FM, FN>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
+                       p.rows_per_split, nci, nco, blocks);
+}
+
+// Large-tile backward-weight configurations (wave tile FM x FN fragments):
+// (ci tile, co tile) = (32*FM, 32*FN).
+struct BigCfg { int fm, fn; };
+static bool big_cfg(int c_in, int c_out, BigCfg* out) {
+    static const BigCfg cands[] = {{6, 6}, {4, 8}, {4, 4}, {3, 3}, {2, 2}};
+    for (const BigCfg& c : cands) {
+        const int bm = 32 * c.fm, bn = 32 * c.fn;
+        if (c_in % bm == 0 && c_out % bn == 0) {
+            *out = c;
+            return true;
+        }
+    }
+    return false;
+}
+
+void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn) {
+    BigCfg c;
+    if (big_cfg(c_in, c_out, &c)) {
+        *tm = 32 * c.fm;
+        *tn = 32 * c.fn;
+    } else {
+        *tm = bw_mfma_tile(c_in);
+        *tn = bw_mfma_tile(c_out);
+    }
+}
+
+template <typename T, int FM, int FN>
+static void launch_big(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                       float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
+                       hipStream_t s) {
+    constexpr int BM = 2 * FM * 16, BN = 2 * FN * 16;
+    const int nci = (int)cdiv(c_in, BM), nco = (int)cdiv(c_out, BN);
+    const int64_t blocks = (int64_t)9 * nci * nco * p.splits;
+    hipLaunchKernelGGL((k_bw_big<T, FM, FN>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
+                       p.rows_per_split, nci, nco, blocks);
+}
+
+template <typename T>
+static void bw_dispatch(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                        float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
+                        hipStream_t s) {
+    BigCfg bc;
+    if (big_cfg(c_in, c_out, &bc)) {
+#define SVTAD_BIG_CASE(M, N)                                                                     \
+    if (bc.fm == M && bc.fn == N) {                                                              \
+        launch_big<T, M, N>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);               \
+        return;                                                                                  \
+    }
+        SVTAD_BIG_CASE(6, 6)
+        SVTAD_BIG_CASE(4, 8)
+        SVTAD_BIG_CASE(4, 4)
+        SVTAD_BIG_CASE(3, 3)
+        SVTAD_BIG_CASE(2, 2)
+#undef SVTAD_BIG_CASE
+    }
+    const int tm = bw_mfma_tile(c_in), tn = bw_mfma_tile(c_out);
+#define SVTAD_BW_CASE(M, N)                                                                 \
+    if (tm == M && tn == N) {                                                               \
+        launch_bw<T, M / 32, N / 32>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s); \
+        return;                                                                             \
+    }
+    SVTAD_BW_CASE(96, 96)
+    SVTAD_BW_CASE(96, 64)
+    SVTAD_BW_CASE(64, 96)
+    SVTAD_BW_CASE(64, 64)
+    SVTAD_BW_CASE(96, 32)
+    SVTAD_BW_CASE(32, 96)
+    SVTAD_BW_CASE(64, 32)
+    SVTAD_BW_CASE(32, 64)
+    SVTAD_BW_CASE(32, 32)
+#undef SVTAD_BW_CASE
+}
+
+void bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+             void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
+             hipStream_t s) {
+    float* part = (float*)ws;
+    float* part_b = gb ? part + (int64_t)p.splits * 9 * c_in * c_out : nullptr;
+    if (dtype == SVTAD_F16) bw_dispatch<f16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
+    else bw_dispatch<bf16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
+    split_reduce(dtype, part, 9LL * c_in * c_out, p.splits, gw, s);
+    if (gb) split_reduce(dtype, part_b, (int64_t)c_out, p.splits, gb, s);
+}
 
 }  // namespace svtad

@@ -101,6 +101,8 @@ __global__ __launch_bounds__(256) void k_gg_valu(const T* __restrict__ src,
             T o;
             if (bias_mode == SVTAD_BIAS_FP32) {
                 o = from_acc<T>(v + ((const A*)bias)[col]);
+            } else if (bias_mode == SVTAD_BIAS_PRE) {
+                o = from_acc<T>(v + to_acc<A>(((const T*)bias)[col]));
             } else if (bias_mode == SVTAD_BIAS_AFTER) {
                 o = from_acc<T>(to_acc<A>(from_acc<T>(v)) + to_acc<A>(((const T*)bias)[col]));
             } else {
@@ -334,6 +336,30 @@ __global__ __launch_bounds__(256) void k_dw_bw(const T* __restrict__ go, const T
 // host launchers
 // ---------------------------------------------------------------------------
 
+template <typename T> constexpr int dtype_of();
+template <> constexpr int dtype_of<float>() { return SVTAD_F32; }
+template <> constexpr int dtype_of<f16>() { return SVTAD_F16; }
+template <> constexpr int dtype_of<bf16>() { return SVTAD_BF16; }
+template <> constexpr int dtype_of<double>() { return SVTAD_F64; }
+
+template <typename T>
+static void launch_split_reduce(const void* part, int64_t count, int splits, void* out,
+                                hipStream_t s) {
+    typedef typename Acc<T>::type A;
+    hipLaunchKernelGGL((k_split_reduce<T, A>),
+                       dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(count, 256), 4096))),
+                       dim3(256), 0, s, (const A*)part, count, splits, (T*)out);
+}
+
+void split_reduce(int dtype, const void* part, int64_t count, int splits, void* out, hipStream_t s) {
+    switch (dtype) {
+        case SVTAD_F32: launch_split_reduce<float>(part, count, splits, out, s); break;
+        case SVTAD_F16: launch_split_reduce<f16>(part, count, splits, out, s); break;
+        case SVTAD_BF16: launch_split_reduce<bf16>(part, count, splits, out, s); break;
+        case SVTAD_F64: launch_split_reduce<double>(part, count, splits, out, s); break;
+    }
+}
+
 template <typename T>
 static void launch_gg_valu(int mode, const void* src, const int32_t* nbr, const void* w,
                            const void* bias, int bias_mode, void* out, int64_t n, int c_red,
@@ -391,12 +417,8 @@ static void launch_bw_valu(const BwPlan& p, const void* go, const void* x, const
     dim3 grid((unsigned)cdiv(c_out, 64), (unsigned)(9 * n_ci_tiles), (unsigned)p.splits);
     hipLaunchKernelGGL((k_bw_valu<T>), grid, dim3(256), 0, s, (const T*)go, (const T*)x, nbr, part,
                        part_b, n, c_in, c_out, tpb, p.rows_per_split, n_ci_tiles);
-    const int64_t cnt = 9LL * c_in * c_out;
-    hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::min<int64_t>(cdiv(cnt, 256), 4096)),
-                       dim3(256), 0, s, (const A*)part, cnt, p.splits, (T*)gw);
-    if (gb)
-        hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)cdiv(c_out, 256)), dim3(256), 0, s,
-                           (const A*)part_b, (int64_t)c_out, p.splits, (T*)gb);
+    split_reduce(dtype_of<T>(), part, 9LL * c_in * c_out, p.splits, gw, s);
+    if (gb) split_reduce(dtype_of<T>(), part_b, (int64_t)c_out, p.splits, gb, s);
 }
 
 void bw_valu(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
@@ -442,11 +464,8 @@ static void launch_dw_bw(const BwPlan& p, const void* go, const void* x, const i
     dim3 grid((unsigned)cdiv(c, 64), (unsigned)p.splits);
     hipLaunchKernelGGL((k_dw_bw<T>), grid, dim3(256), 0, s, (const T*)go, (const T*)x, nbr, part,
                        part_b, n, c, tpb, p.rows_per_split);
-    hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)cdiv(9LL * c, 256)), dim3(256), 0, s,
-                       (const A*)part, 9LL * c, p.splits, (T*)gw);
-    if (gb)
-        hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)cdiv(c, 256)), dim3(256), 0, s,
-                           (const A*)part_b, (int64_t)c, p.splits, (T*)gb);
+    split_reduce(dtype_of<T>(), part, 9LL * c, p.splits, gw, s);
+    if (gb) split_reduce(dtype_of<T>(), part_b, (int64_t)c, p.splits, gb, s);
 }
 
 void dw_bw(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, void* gw,

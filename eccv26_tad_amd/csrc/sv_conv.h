@@ -35,13 +35,25 @@ void dw_gather(int dtype, int mode, const void* src, const int32_t* nbr, const v
 void dw_bw(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, void* gw,
            void* gb, void* ws, int64_t n, int c, int64_t tpb, hipStream_t s);
 
+// out[e] = T(sum_s part[s][e]) for e < count; partials in the accumulator type.
+void split_reduce(int dtype, const void* part, int64_t count, int splits, void* out, hipStream_t s);
+
 // MFMA path (f16 / bf16). Returns false when the shape is not handled, so the
 // caller falls back to the VALU kernels.
 bool gg_mfma_supported(int dtype, int c_red, int n_out);
+// Workspace (the weight in MFMA fragment order) a gathered GEMM with
+// reduction width c_red and n_out columns needs; 0 when the shape takes a
+// kernel that reads w directly.
+size_t gg_mfma_workspace(int dtype, int c_red, int n_out);
 void gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
-             int64_t tpb, hipStream_t s);
-bool bw_mfma_supported(int dtype, int c_in, int c_out);
+             int64_t tpb, void* ws, hipStream_t s);
+bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out);
+// Rows per split of the MFMA backward-weight (its row list lives in LDS).
+constexpr int kMaxSplitRows = 2048;
+int bw_mfma_tile(int c);
+// (ci, co) tile edges of the MFMA backward-weight kernel chosen for a shape.
+void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn);
 void bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
              void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
              hipStream_t s);

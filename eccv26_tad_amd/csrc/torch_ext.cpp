@@ -78,17 +78,30 @@ at::Tensor conv_fwd(const at::Tensor& x_in, const at::Tensor& nbr_in, const at::
     at::Tensor bias;
     if (bias_mode != SVTAD_BIAS_NONE && bias_present(bias_in)) {
         TORCH_CHECK(bias_in->numel() == c_out, "bias must have C_out = ", c_out, " elements");
-        const at::ScalarType bt = bias_mode == SVTAD_BIAS_FP32
-                                      ? (x.scalar_type() == at::kDouble ? at::kDouble : at::kFloat)
-                                      : x.scalar_type();
-        bias = bias_in->to(x.device(), bt).contiguous();
+        if (bias_mode == SVTAD_BIAS_FP32 && bias_in->scalar_type() == x.scalar_type()) {
+            // widened exactly inside the kernel: no conversion launch
+            bias_mode = SVTAD_BIAS_PRE;
+            bias = bias_in->contiguous();
+        } else {
+            const at::ScalarType bt =
+                bias_mode == SVTAD_BIAS_FP32
+                    ? (x.scalar_type() == at::kDouble ? at::kDouble : at::kFloat)
+                    : x.scalar_type();
+            bias = bias_in->to(x.device(), bt).contiguous();
+        }
+        TORCH_CHECK(bias.device() == x.device(), "bias must be on x's device");
     } else {
         bias_mode = SVTAD_BIAS_NONE;
     }
     at::Tensor out = at::empty({n, c_out}, x.options());
+    const int dt = dtype_code(x);
+    const size_t ws_bytes = svtad_fwd_workspace_bytes((int)c_in, (int)c_out, dt);
+    at::Tensor ws;
+    if (ws_bytes && n > 0) ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
     const int st = svtad_fwd(x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
                              bias.defined() ? bias.data_ptr() : nullptr, bias_mode, out.data_ptr(),
-                             n, (int)c_in, (int)c_out, tpb, dtype_code(x), stream_of(x));
+                             ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, n, (int)c_in,
+                             (int)c_out, tpb, dt, stream_of(x));
     check_status(st, "fwd");
     return out;
 }
@@ -143,8 +156,13 @@ at::Tensor op_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const at
     at::Tensor nbr = table_i32(nbr_in, n_kept);
     c10::DeviceGuard g(go.device());
     at::Tensor gi = at::empty({n_kept, c_in}, go.options());
+    const int dt = dtype_code(go);
+    const size_t ws_bytes = svtad_bwd_in_workspace_bytes((int)c_in, (int)c_out, dt);
+    at::Tensor ws;
+    if (ws_bytes && n_kept > 0) ws = at::empty({(int64_t)ws_bytes}, go.options().dtype(at::kByte));
     const int st = svtad_bwd_in(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(), gi.data_ptr(),
-                                n_kept, (int)c_in, (int)c_out, tpb, dtype_code(go), stream_of(go));
+                                ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, n_kept, (int)c_in,
+                                (int)c_out, tpb, dt, stream_of(go));
     check_status(st, "bwd_in");
     return gi;
 }

@@ -56,14 +56,24 @@ enum svtad_bias_mode {
     SVTAD_BIAS_FP32 = 1,   /* bias in the accumulator type (float32; float64 for
                               SVTAD_F64) added before rounding
                               (implicit_gemm_v2.cu:153-159, 291-294) */
-    SVTAD_BIAS_AFTER = 2   /* bias in `dtype`, added after rounding the conv to
+    SVTAD_BIAS_AFTER = 2,  /* bias in `dtype`, added after rounding the conv to
                               dtype, then rounded again: `output += bias`
                               (sparse_conv_layer.py:86-87) */
+    SVTAD_BIAS_PRE = 3     /* bias in `dtype`, widened exactly to the accumulator
+                              type and added before rounding: the same result as
+                              SVTAD_BIAS_FP32 given bias.to(float32)
+                              (implicit_gemm_v2.cu:290-297) without the conversion */
 };
 
 /* Message of the last SVTAD_ERR_* returned on this host thread. */
 const char* svtad_last_error(void);
 const char* svtad_version(void);
+
+/* Workspace bytes svtad_fwd / svtad_bwd_in need for this shape (0: none).
+ * For f16/bf16 matrix-core shapes it holds the weight re-laid out in the
+ * order the matrix-core operand fragments are read. */
+size_t svtad_fwd_workspace_bytes(int c_in, int c_out, int dtype);
+size_t svtad_bwd_in_workspace_bytes(int c_in, int c_out, int dtype);
 
 /*
  * Forward SparseConv2D: out[i,co] = sum_k sum_ci x[src(i,k),ci] * w[k,ci,co]
@@ -71,11 +81,13 @@ const char* svtad_version(void);
  * Replaces `fwd` / launch_fwd (2d_sparse_v3_bind.cpp:9, 2d_sparse_v3.cu:751-822)
  * with SVTAD_BIAS_NONE, and `implicit_gemm_fwd_v2` / `implicit_gemm_fwd_v2_chunked`
  * (2d_sparse_v3_bind.cpp:12-13, implicit_gemm_v2.cu:197-300, 306-417) with
- * SVTAD_BIAS_FP32. Requires c_in % 4 == 0 (sparse_conv_layer.py:39-42).
+ * SVTAD_BIAS_FP32 / SVTAD_BIAS_PRE. Requires c_in % 4 == 0
+ * (sparse_conv_layer.py:39-42). `workspace` must hold
+ * svtad_fwd_workspace_bytes() bytes (may be NULL when that is 0).
  */
 int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, const void* bias,
-              int bias_mode, void* out, int64_t n, int c_in, int c_out,
-              int64_t tokens_per_batch, int dtype, void* stream);
+              int bias_mode, void* out, void* workspace, size_t workspace_bytes, int64_t n,
+              int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream);
 
 /*
  * Backward-input: gi[src(i,k),ci] += sum_co go[i,co] * w[k,ci,co], as a
@@ -83,10 +95,12 @@ int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, const void*
  * not in the table are added afterwards with atomics).
  * Replaces `bwd_in` / launch_bwd_in (2d_sparse_v3_bind.cpp:10,
  * 2d_sparse_v3.cu:824-835). gi is fully written (no pre-zeroing needed).
+ * `workspace` must hold svtad_bwd_in_workspace_bytes() bytes (may be NULL
+ * when that is 0).
  */
 int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight, void* grad_in,
-                 int64_t n, int c_in, int c_out, int64_t tokens_per_batch, int dtype,
-                 void* stream);
+                 void* workspace, size_t workspace_bytes, int64_t n, int c_in, int c_out,
+                 int64_t tokens_per_batch, int dtype, void* stream);
 
 /* Workspace bytes needed by svtad_bwd_w for this shape. */
 size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, int dtype);

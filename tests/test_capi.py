@@ -16,6 +16,7 @@ LIB = os.path.join(ROOT, "eccv26_tad_amd", "libsvtad_sparse.so")
 HEADER = os.path.join(ROOT, "include", "svtad_sparse.h")
 
 I64 = ctypes.c_int64
+Z = ctypes.c_size_t(0)
 
 
 def declared_functions():
@@ -48,30 +49,30 @@ def test_version(lib):
 
 
 def test_bad_dtype_rejected_on_host(lib):
-    st = lib.svtad_fwd(None, None, None, None, 0, None, I64(10), 8, 8, I64(0), 9, None)
+    st = lib.svtad_fwd(None, None, None, None, 0, None, None, Z, I64(10), 8, 8, I64(0), 9, None)
     assert st == -1
     assert b"dtype" in lib.svtad_last_error()
 
 
 def test_bad_cin_rejected_on_host(lib):
-    st = lib.svtad_fwd(None, None, None, None, 0, None, I64(10), 6, 8, I64(0), 0, None)
+    st = lib.svtad_fwd(None, None, None, None, 0, None, None, Z, I64(10), 6, 8, I64(0), 0, None)
     assert st == -1
     assert b"divisible by 4" in lib.svtad_last_error()
 
 
 def test_bias_mode_needs_pointer(lib):
-    st = lib.svtad_fwd(None, None, None, None, 1, None, I64(10), 8, 8, I64(0), 0, None)
+    st = lib.svtad_fwd(None, None, None, None, 1, None, None, Z, I64(10), 8, 8, I64(0), 0, None)
     assert st == -1 and b"bias" in lib.svtad_last_error()
 
 
 def test_negative_sizes_rejected(lib):
-    assert lib.svtad_bwd_in(None, None, None, None, I64(-1), 8, 8, I64(0), 0, None) == -1
-    assert lib.svtad_bwd_in(None, None, None, None, I64(4), 8, 8, I64(-3), 0, None) == -1
+    assert lib.svtad_bwd_in(None, None, None, None, None, Z, I64(-1), 8, 8, I64(0), 0, None) == -1
+    assert lib.svtad_bwd_in(None, None, None, None, None, Z, I64(4), 8, 8, I64(-3), 0, None) == -1
 
 
 def test_empty_input_is_a_noop(lib):
-    assert lib.svtad_fwd(None, None, None, None, 0, None, I64(0), 8, 8, I64(0), 1, None) == 0
-    assert lib.svtad_bwd_in(None, None, None, None, I64(0), 8, 8, I64(0), 1, None) == 0
+    assert lib.svtad_fwd(None, None, None, None, 0, None, None, Z, I64(0), 8, 8, I64(0), 0, None) == 0
+    assert lib.svtad_bwd_in(None, None, None, None, None, Z, I64(0), 8, 8, I64(0), 0, None) == 0
 
 
 def test_workspace_sizes(lib):
@@ -81,6 +82,19 @@ def test_workspace_sizes(lib):
         assert b >= (9 * ci * co + co) * acc
         assert b % ((9 * ci * co + co) * acc) == 0
     assert lib.svtad_dw_bwd_w_workspace_bytes(I64(17248), 192, 1) >= 10 * 192 * 4
+
+
+def test_fwd_workspace(lib):
+    lib.svtad_fwd_workspace_bytes.restype = ctypes.c_size_t
+    # f16 / bf16 shapes of the matrix-core forward hold the packed weight
+    lib.svtad_bwd_in_workspace_bytes.restype = ctypes.c_size_t
+    assert lib.svtad_fwd_workspace_bytes(192, 192, 1) == 9 * 192 * 192 * 2
+    assert lib.svtad_bwd_in_workspace_bytes(256, 128, 1) == 9 * 256 * 128 * 2
+    assert lib.svtad_fwd_workspace_bytes(256, 256, 2) == 9 * 256 * 256 * 2
+    assert lib.svtad_fwd_workspace_bytes(192, 192, 0) == 0  # f32: VALU kernel, no workspace
+    assert lib.svtad_fwd_workspace_bytes(20, 36, 1) == 0
+    st = lib.svtad_fwd(None, None, None, None, 0, None, None, Z, I64(10), 192, 192, I64(0), 1, None)
+    assert st == -2 and b"workspace" in lib.svtad_last_error()
 
 
 def test_workspace_too_small_rejected(lib):

@@ -184,6 +184,10 @@ CONV_CASES = [
     ((1, 3, 7, 9), 0.6, 12, 20, "float32"),        # C_in % 8 != 0, odd C_out
     ((1, 3, 7, 9), 0.6, 20, 36, "float16"),
     ((2, 2, 14, 14), 1.0, 128, 96, "float16"),
+    ((2, 16, 14, 14), 0.55, 192, 192, "float16"),  # many row tiles and row splits
+    ((1, 4, 16, 16), 0.4, 256, 128, "bfloat16"),
+    ((1, 8, 14, 14), 0.5, 48, 48, "float16"),      # config-1 channels on the matrix cores
+    ((1, 3, 9, 11), 0.7, 40, 24, "float16"),       # widths that are not tile multiples
 ]
 
 
