@@ -116,7 +116,7 @@ extern "C" int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, 
     if (gg_mfma_supported(dtype, c_in, c_out) && al16(x) && al16(weight) && al16(out) &&
         (!need || al16(workspace)))
         gg_mfma(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
-                tokens_per_batch, need ? workspace : nullptr, s);
+                tokens_per_batch, need ? workspace : nullptr, false, s);
     else
         gg_valu(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
                 tokens_per_batch, s);
@@ -139,10 +139,60 @@ extern "C" int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void
     if (gg_mfma_supported(dtype, c_out, c_in) && al16(grad_out) && al16(weight) && al16(grad_in) &&
         (!need || al16(workspace)))
         gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
-                tokens_per_batch, need ? workspace : nullptr, s);
+                tokens_per_batch, need ? workspace : nullptr, false, s);
     else
         gg_valu(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
                 tokens_per_batch, s);
+    orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, s);
+    return launch_status();
+}
+
+extern "C" int svtad_pack_weight(const void* weight, void* packed_fwd, void* packed_bwd, int c_in,
+                                 int c_out, int dtype, void* stream) {
+    if (!weight || (!packed_fwd && !packed_bwd) || c_in <= 0 || c_out <= 0)
+        return set_error(SVTAD_ERR_INVALID, "pack_weight: bad arguments");
+    if ((packed_fwd && !gg_mfma_workspace(dtype, c_in, c_out)) ||
+        (packed_bwd && !gg_mfma_workspace(dtype, c_out, c_in)))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "pack_weight: shape/dtype has no packed layout");
+    if (!al16(packed_fwd) || !al16(packed_bwd))
+        return set_error(SVTAD_ERR_INVALID, "pack_weight: packed buffers must be 16-byte aligned");
+    pack_weight(weight, packed_fwd, packed_bwd, c_in, c_out, (hipStream_t)stream);
+    return launch_status();
+}
+
+extern "C" int svtad_fwd_packed(const void* x, const int32_t* nbr, const void* packed_fwd,
+                                const void* bias, int bias_mode, void* out, int64_t n, int c_in,
+                                int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
+    int st = check_common("fwd_packed", n, c_in, c_out, tokens_per_batch, dtype);
+    if (st) return st;
+    if (bias_mode < SVTAD_BIAS_NONE || bias_mode > SVTAD_BIAS_PRE || (bias_mode != SVTAD_BIAS_NONE && !bias))
+        return set_error(SVTAD_ERR_INVALID, "fwd_packed: bad bias_mode / bias");
+    if (!gg_mfma_packed_ok(dtype, n, c_in, c_out))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "fwd_packed: shape/dtype has no packed layout");
+    if (n == 0) return SVTAD_OK;
+    if (!x || !nbr || !packed_fwd || !out) return set_error(SVTAD_ERR_INVALID, "fwd_packed: null pointer");
+    if (!al16(x) || !al16(packed_fwd) || !al16(out))
+        return set_error(SVTAD_ERR_INVALID, "fwd_packed: x, packed weight and out must be 16-byte aligned");
+    gg_mfma(dtype, MODE_FWD, x, nbr, packed_fwd, bias, bias_mode, out, n, c_in, c_out,
+            tokens_per_batch, nullptr, true, (hipStream_t)stream);
+    return launch_status();
+}
+
+extern "C" int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* weight,
+                                   const void* packed_bwd, void* grad_in, int64_t n, int c_in,
+                                   int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
+    int st = check_common("bwd_in_packed", n, c_in, c_out, tokens_per_batch, dtype);
+    if (st) return st;
+    if (!gg_mfma_packed_ok(dtype, n, c_out, c_in))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_in_packed: shape/dtype has no packed layout");
+    if (n == 0) return SVTAD_OK;
+    if (!grad_out || !nbr || !weight || !packed_bwd || !grad_in)
+        return set_error(SVTAD_ERR_INVALID, "bwd_in_packed: null pointer");
+    if (!al16(grad_out) || !al16(packed_bwd) || !al16(grad_in))
+        return set_error(SVTAD_ERR_INVALID, "bwd_in_packed: grad_out, packed weight and grad_in must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in, n, c_out, c_in,
+            tokens_per_batch, nullptr, true, s);
     orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, s);
     return launch_status();
 }
@@ -158,7 +208,8 @@ extern "C" int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* n
     int st = check_common("bwd_w", n, c_in, c_out, tokens_per_batch, dtype);
     if (st) return st;
     BwPlan p = plan_bw(n, c_in, c_out, dtype);
-    if (!grad_w || !workspace || (n > 0 && (!grad_out || !x || !nbr)))
+    // grad_w NULL: only the row-split partial sums are written (to workspace)
+    if (!workspace || (n > 0 && (!grad_out || !x || !nbr)))
         return set_error(SVTAD_ERR_INVALID, "bwd_w: null pointer");
     if (p.path == 1 && !(al16(grad_out) && al16(x))) p.path = 0;  // same workspace layout
     if (workspace_bytes < p.ws_bytes)

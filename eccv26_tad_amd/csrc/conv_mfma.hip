@@ -500,6 +500,40 @@ __global__ __launch_bounds__(256) void k_pack_frag(const u16* __restrict__ w, u1
     *(u32x4*)(wf + slot * 8) = o;
 }
 
+// Both fragment-ordered layouts in one launch: slots [0, sf) write the
+// forward layout (if wf_fwd), slots [sf, sf + sb) the backward-input layout
+// (if wf_bwd). Same slot formula as k_pack_frag.
+__global__ __launch_bounds__(256) void k_pack_both(const u16* __restrict__ w, u16* __restrict__ wf_fwd,
+                                                   u16* __restrict__ wf_bwd, int c_in, int c_out,
+                                                   int64_t sf, int64_t sb) {
+    int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool fwd = slot < sf;
+    if (!fwd) slot -= sf;
+    if (slot >= (fwd ? sf : sb)) return;
+    const int c_red = fwd ? c_in : c_out, n_out = fwd ? c_out : c_in;
+    const int ncs = c_red / KS, nb = (n_out + 15) / 16;
+    const int lane = (int)(slot & 63);
+    int64_t q = slot >> 6;
+    const int b = (int)(q % nb);
+    q /= nb;
+    const int cs = (int)(q % ncs);
+    const int k = (int)(q / ncs);
+    const int n = b * 16 + (lane & 15);
+    const int c = cs * KS + (lane >> 4) * 8;
+    const u16* wk = w + (int64_t)k * c_in * c_out;
+    u16 v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        u16 x = 0;
+        if (n < n_out) x = fwd ? wk[(int64_t)(c + e) * c_out + n] : wk[(int64_t)n * c_out + c + e];
+        v[e] = x;
+    }
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = (unsigned)v[2 * j] | ((unsigned)v[2 * j + 1] << 16);
+    *(u32x4*)((fwd ? wf_fwd : wf_bwd) + slot * 8) = o;
+}
+
 // ---------------------------------------------------------------------------
 // Backward-weight partials: ws[s][k][ci][co] = sum over rows i of split s of
 // x[src(i,k), ci] * go[i, co]; ws_bias[s][co] = sum of go[i, co] (written by
@@ -676,43 +710,91 @@ __global__ __launch_bounds__(256) void k_bw_mfma(
 // ---------------------------------------------------------------------------
 // Backward-weight partials, large tiles (the shapes of the adapter convs).
 // A workgroup owns one offset k, a BM x BN (ci x co) tile of gw and one row
-// split. Per 64-row stage it stages the gathered x rows and the go rows in
-// LDS untransposed ([row][channel], 16-byte coalesced loads with the lanes
-// along the channels) and reads the MFMA fragments with the gfx950 LDS
-// transpose load ds_read_b64_tr_b16: within each 16-lane group, lane j points
-// at 4 consecutive channels of row j/4 and lane i receives the value of
-// channel i at 4 consecutive rows, so two such reads give a lane the 8
-// consecutive rows of its fragment. Two register stages keep the loads of
-// stage t+2 in flight while stage t runs. The bias gradient is one extra MFMA
-// per column fragment against a fragment of ones (k == 4, ci-tile 0 only).
+// split. Per 64-row stage each thread loads an 8-row x 8-channel block of the
+// gathered x rows (or of the go rows) with 16-byte coalesced loads (lanes
+// along the channels), transposes it in registers (v_perm_b32) and writes
+// eight 16-byte rows of a [channel][row] LDS tile; the MFMA fragments (8
+// consecutive rows of one channel) are then single 16-byte LDS reads, and
+// with a 144-byte pitch both the writes and the reads are free of bank
+// conflicts. Two register stages keep the loads of stage t+2 in flight while
+// stage t runs. Partials are stored in fragment order (each lane's 4 values
+// contiguous); k_bw_reduce sums the splits in a fixed order. The k == 4,
+// ci-tile 0 workgroups also sum the staged go rows per column (bias).
 // ---------------------------------------------------------------------------
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+constexpr int TP = KR + 8;  // pitch of a transposed stage: 72 elements = 144 bytes
 
-__device__ __forceinline__ u32x4 tr_frag(const u16* lds_row0, int pitch, int g, int i, int col0) {
-    // rows 8g + 4r + i/4, channels col0 + 4*(i%4) .. +3, r = 0, 1
-    const u16* p0 = lds_row0 + (8 * g + (i >> 2)) * pitch + col0 + 4 * (i & 3);
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 4 * pitch));
-    const uint2 a = __builtin_bit_cast(uint2, lo), b = __builtin_bit_cast(uint2, hi);
-    return u32x4{a.x, a.y, b.x, b.y};
+// 8x8 transpose of 16-bit values: in[r] holds channels 0..7 of row r; out[c]
+// gets rows 0..7 of channel c.
+__device__ __forceinline__ void transpose8(const u32x4* in, u32x4* out) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int d = c >> 1;
+        const unsigned sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        u32x4 o;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = __builtin_amdgcn_perm(in[2 * q + 1][d], in[2 * q][d], sel);
+        out[c] = o;
+    }
 }
 
-template <typename T, int FM, int FN>
-__global__ __launch_bounds__(256) void k_bw_big(
+// gw[k][ci][co] = T(sum_s part[s]...) for the fragment-ordered partials of
+// k_bw_big (quadruple e: 4 consecutive floats of one lane), splits summed in
+// order; and gb[co] = T(sum_s part_b[s][co]) for "quadruple" quads + co.
+template <typename T>
+__device__ __forceinline__ void bw_reduce_one(int64_t e, const float* __restrict__ part,
+                                              const float* __restrict__ part_b, int splits,
+                                              int c_in, int c_out, int fm, int fn, int wgm, int wgn,
+                                              int n_ci_tiles, int n_co_tiles, T* __restrict__ gw,
+                                              T* __restrict__ gb) {
+    const int bm = wgm * fm * 16, bn = wgn * fn * 16;
+    const int64_t per_split = (int64_t)9 * c_in * c_out;
+    const int64_t quads = per_split / 4;
+    if (e < quads) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < splits; ++q) acc += *(const f32x4*)(part + q * per_split + e * 4);
+        // decode the fragment-order position
+        int64_t rest = e * 4;
+        const int64_t tile_sz = (int64_t)bm * bn;
+        const int64_t tile = rest / tile_sz;
+        rest -= tile * tile_sz;
+        const int k = (int)(tile / (n_ci_tiles * n_co_tiles));
+        const int tr = (int)(tile - (int64_t)k * n_ci_tiles * n_co_tiles);
+        const int ci0 = (tr / n_co_tiles) * bm, co0 = (tr % n_co_tiles) * bn;
+        const int lane = (int)((rest >> 2) & 63);
+        int fr = (int)(rest >> 8);  // (wave * fm + a) * fn + b
+        const int b = fr % fn;
+        fr /= fn;
+        const int a = fr % fm;
+        const int wave = fr / fm;
+        const int ci = ci0 + (wave / wgn) * fm * 16 + a * 16 + (lane >> 4) * 4;
+        const int co = co0 + (wave % wgn) * fn * 16 + b * 16 + (lane & 15);
+        T* g = gw + ((int64_t)k * c_in + ci) * c_out + co;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) g[(int64_t)j * c_out] = (T)acc[j];
+    } else if (gb && e - quads < c_out) {
+        const int c = (int)(e - quads);
+        float v = 0.f;
+        for (int q = 0; q < splits; ++q) v += part_b[(int64_t)q * c_out + c];
+        gb[c] = (T)v;
+    }
+}
+
+template <typename T, int FM, int FN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
     const T* __restrict__ go, const T* __restrict__ x, const int32_t* __restrict__ nbr,
     float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int c_in, int c_out,
     int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks) {
-    constexpr int BM = 2 * FM * 16;  // ci
-    constexpr int BN = 2 * FN * 16;  // co
-    constexpr int PA = BM + 8, PB = BN + 8;  // LDS pitches (elements)
-    constexpr int CA = BM / 8, CB = BN / 8;  // 16-byte chunks per staged row
-    constexpr int A_PER = (KR * CA + 255) / 256;
-    constexpr int B_PER = (KR * CB + 255) / 256;
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int BM = WGM * FM * 16;  // ci
+    constexpr int BN = WGN * FN * 16;  // co
+    constexpr int A_ITEMS = (KR / 8) * (BM / 8);  // 8x8 blocks per stage
+    constexpr int B_ITEMS = (KR / 8) * (BN / 8);
+    constexpr int ITEMS = A_ITEMS + B_ITEMS;
+    constexpr int PER = (ITEMS + NT - 1) / NT;
 
-    __shared__ __align__(16) u16 As[2][KR][PA];
-    __shared__ __align__(16) u16 Bs[2][KR][PB];
-    __shared__ uint32_t srow[kMaxSplitRows];
+    __shared__ __align__(16) u16 As[2][BM][TP];
+    __shared__ __align__(16) u16 Bs[2][BN][TP];
+    __shared__ __align__(16) uint32_t srow[kMaxSplitRows];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -722,14 +804,14 @@ __global__ __launch_bounds__(256) void k_bw_big(
     int rem = (int)(lin - (int64_t)s * tiles);
     const int k = rem / (n_ci_tiles * n_co_tiles);
     rem -= k * n_ci_tiles * n_co_tiles;
-    const int ci0 = (rem / n_co_tiles) * BM;
-    const int co0 = (rem % n_co_tiles) * BN;
+    const int cit = rem / n_co_tiles, cot = rem % n_co_tiles;
+    const int ci0 = cit * BM, co0 = cot * BN;
     const int64_t r_begin = (int64_t)s * rows_per_split;
     const int rows = (int)max<int64_t>(0, min(n, r_begin + rows_per_split) - r_begin);
     const int steps = (rows + KR - 1) / KR;
     const bool do_bias = ws_bias != nullptr && k == 4 && ci0 == 0;  // uniform
 
-    for (int r = tid; r < steps * KR; r += 256) {
+    for (int r = tid; r < steps * KR; r += NT) {
         const int64_t sr = r < rows ? src_row(nbr, r_begin + r, k, n, tpb) : -1;
         srow[r] = sr >= 0 ? (uint32_t)sr * (uint32_t)(c_in * 2) : kOOB;
     }
@@ -738,38 +820,52 @@ __global__ __launch_bounds__(256) void k_bw_big(
     const rsrc_t rs_x = make_rsrc(x, (uint32_t)(n * c_in * 2));
     const rsrc_t rs_g = make_rsrc(go + r_begin * c_out, (uint32_t)((int64_t)rows * c_out * 2));
 
-    // staging slot e = tid + q*256 of a stage: row e / CA (or CB), 16-byte chunk e % CA
-    u32x4 ra0[A_PER], rb0[B_PER], ra1[A_PER], rb1[B_PER];
-    // stages at or past `steps` load zeros (out of range) so the loop body is uniform
-    auto load = [&](int t, u32x4* ra, u32x4* rb) {
+    // item e < A_ITEMS: rows 8*(e / (BM/8)) .. +7, channels 8*(e % (BM/8)) of x;
+    // else the same for go with BN. Stages at or past `steps` load zeros.
+    u32x4 r0s[PER][8], r1s[PER][8];
+    auto load = [&](int t, u32x4 (*rg)[8]) {
         const bool live = t < steps;
-        const int r0 = live ? t * KR : 0;
+        const int rbase = live ? t * KR : 0;
 #pragma unroll
-        for (int q = 0; q < A_PER; ++q) {
-            const int e = tid + q * 256;
-            const int r = e / CA, c = ci0 + (e - r * CA) * 8;
-            const bool ok = live && r < KR && c < c_in;
-            const uint32_t so = srow[r0 + (ok ? r : 0)];
-            ra[q] = bload16(rs_x, ok && so != kOOB ? so + (uint32_t)c * 2u : kOOB);
-        }
+        for (int q = 0; q < PER; ++q) {
+            const int e = tid + q * NT;
+            if (e < A_ITEMS) {
+                const int rgp = e / (BM / 8), c = ci0 + (e - rgp * (BM / 8)) * 8;
+                const bool ok = live && c < c_in;
+                const u32x4 s0 = *(const u32x4*)&srow[rbase + rgp * 8];
+                const u32x4 s1 = *(const u32x4*)&srow[rbase + rgp * 8 + 4];
 #pragma unroll
-        for (int q = 0; q < B_PER; ++q) {
-            const int e = tid + q * 256;
-            const int r = e / CB, c = co0 + (e - r * CB) * 8;
-            const bool ok = live && r < KR && c < c_out;
-            rb[q] = bload16(rs_g, ok ? (uint32_t)((r0 + r) * c_out + c) * 2u : kOOB);
+                for (int r = 0; r < 8; ++r) {
+                    const uint32_t so = r < 4 ? s0[r] : s1[r - 4];
+                    rg[q][r] = bload16(rs_x, ok && so != kOOB ? so + (uint32_t)c * 2u : kOOB);
+                }
+            } else {
+                const int eb = e - A_ITEMS;
+                const int rgp = eb / (BN / 8), c = co0 + (eb - rgp * (BN / 8)) * 8;
+                const bool ok = live && e < ITEMS && c < c_out;
+#pragma unroll
+                for (int r = 0; r < 8; ++r)
+                    rg[q][r] = bload16(rs_g, ok ? (uint32_t)((rbase + rgp * 8 + r) * c_out + c) * 2u : kOOB);
+            }
         }
     };
-    auto store = [&](int buf, const u32x4* ra, const u32x4* rb) {
+    auto store = [&](int buf, u32x4 (*rg)[8]) {
 #pragma unroll
-        for (int q = 0; q < A_PER; ++q) {
-            const int e = tid + q * 256;
-            if (e < KR * CA) *(u32x4*)&As[buf][e / CA][(e % CA) * 8] = ra[q];
-        }
+        for (int q = 0; q < PER; ++q) {
+            const int e = tid + q * NT;
+            if (e >= ITEMS) continue;
+            u32x4 o[8];
+            transpose8(rg[q], o);
+            if (e < A_ITEMS) {
+                const int rgp = e / (BM / 8), cl = (e - rgp * (BM / 8)) * 8;
 #pragma unroll
-        for (int q = 0; q < B_PER; ++q) {
-            const int e = tid + q * 256;
-            if (e < KR * CB) *(u32x4*)&Bs[buf][e / CB][(e % CB) * 8] = rb[q];
+                for (int c = 0; c < 8; ++c) *(u32x4*)&As[buf][cl + c][rgp * 8] = o[c];
+            } else {
+                const int eb = e - A_ITEMS;
+                const int rgp = eb / (BN / 8), cl = (eb - rgp * (BN / 8)) * 8;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) *(u32x4*)&Bs[buf][cl + c][rgp * 8] = o[c];
+            }
         }
     };
 
@@ -779,57 +875,69 @@ __global__ __launch_bounds__(256) void k_bw_big(
 #pragma unroll
         for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int wm = wave >> 1, wn = wave & 1;
-    const int g = lane >> 4, i16 = lane & 15;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int arow = wm * FM * 16 + (lane & 15), brow = wn * FN * 16 + (lane & 15);
+    const int kof = (lane >> 4) * 8;
     float bsum = 0.f;
     auto compute = [&](int buf) {
         if (do_bias && tid < BN) {  // column sums of the staged go rows
-#pragma unroll 8
-            for (int r = 0; r < KR; ++r) bsum += (float)__builtin_bit_cast(T, Bs[buf][r][tid]);
+#pragma unroll
+            for (int r = 0; r < KR; r += 8) {
+                const u32x4 v = *(const u32x4*)&Bs[buf][tid][r];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    bsum += (float)__builtin_bit_cast(T, (u16)(v[q] & 0xffffu));
+                    bsum += (float)__builtin_bit_cast(T, (u16)(v[q] >> 16));
+                }
+            }
         }
 #pragma unroll
         for (int h = 0; h < KR / KS; ++h) {
             u32x4 fb[FN];
 #pragma unroll
-            for (int b = 0; b < FN; ++b) fb[b] = tr_frag(&Bs[buf][h * KS][0], PB, g, i16, wn * FN * 16 + b * 16);
+            for (int b = 0; b < FN; ++b) fb[b] = *(const u32x4*)&Bs[buf][brow + b * 16][h * KS + kof];
 #pragma unroll
             for (int a = 0; a < FM; ++a) {
-                const u32x4 fa = tr_frag(&As[buf][h * KS][0], PA, g, i16, wm * FM * 16 + a * 16);
+                const u32x4 fa = *(const u32x4*)&As[buf][arow + a * 16][h * KS + kof];
 #pragma unroll
                 for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fa, fb[b], acc[a][b]);
             }
         }
     };
 
-    load(0, ra0, rb0);
-    load(1, ra1, rb1);
-    store(0, ra0, rb0);
+    load(0, r0s);
+    load(1, r1s);
+    store(0, r0s);
     __syncthreads();
     for (int t = 0; t < steps; t += 2) {
-        load(t + 2, ra0, rb0);  // registers of set 0 are free again
-        compute(0);             // stage t
-        store(1, ra1, rb1);     // stage t+1 (zeros past the end)
+        load(t + 2, r0s);  // registers of set 0 are free again
+        compute(0);        // stage t
+        store(1, r1s);     // stage t+1 (zeros past the end)
         __syncthreads();
-        load(t + 3, ra1, rb1);
-        compute(1);             // stage t+1
-        store(0, ra0, rb0);     // stage t+2
+        load(t + 3, r1s);
+        compute(1);        // stage t+1
+        store(0, r0s);     // stage t+2
         __syncthreads();
     }
 
-    float* dst = ws + ((int64_t)s * 9 + k) * c_in * c_out;
+    // partial tile in fragment order: [wave][a][b][lane][4]
+    float* dst = ws + (((int64_t)s * 9 + k) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
 #pragma unroll
-    for (int b = 0; b < FN; ++b) {
-        const int co = co0 + wn * FN * 16 + b * 16 + i16;
-        if (co >= c_out) continue;
+    for (int a = 0; a < FM; ++a)
 #pragma unroll
-        for (int a = 0; a < FM; ++a)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int ci = ci0 + wm * FM * 16 + a * 16 + g * 4 + j;
-                if (ci < c_in) dst[(int64_t)ci * c_out + co] = acc[a][b][j];
-            }
-    }
+        for (int b = 0; b < FN; ++b)
+            *(f32x4*)(dst + (((wave * FM + a) * FN + b) * 64 + lane) * 4) = acc[a][b];
     if (do_bias && tid < BN && co0 + tid < c_out) ws_bias[(int64_t)s * c_out + co0 + tid] = bsum;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ part,
+                                                   const float* __restrict__ part_b, int splits,
+                                                   int c_in, int c_out, int fm, int fn, int wgm,
+                                                   int wgn, int n_ci_tiles, int n_co_tiles,
+                                                   T* __restrict__ gw, T* __restrict__ gb) {
+    bw_reduce_one<T>((int64_t)blockIdx.x * 256 + threadIdx.x, part, part_b, splits, c_in, c_out, fm,
+                     fn, wgm, wgn, n_ci_tiles, n_co_tiles, gw, gb);
 }
 
 // ---------------------------------------------------------------------------
@@ -936,15 +1044,17 @@ static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, 
 template <typename T, int MODE>
 static void gg_dispatch(const void* src, const int32_t* nbr, const void* w, const void* bias,
                         int bias_mode, void* out, int64_t n, int c_red, int n_out, int64_t tpb,
-                        void* ws, hipStream_t s) {
+                        void* ws, bool prepacked, hipStream_t s) {
     const WideCfg* wc = wide_cfg(c_red, n_out);
     // buffer loads address operands with 32-bit byte offsets
     const bool fits = n * c_red * 2 < (int64_t)INT32_MAX && 9LL * c_red * n_out * 2 < (int64_t)INT32_MAX;
-    if (wc && fits && ws) {
-        const int64_t slots = (int64_t)9 * (c_red / KS) * cdiv(n_out, 16) * 64;
-        hipLaunchKernelGGL((k_pack_frag<MODE>), dim3((unsigned)cdiv(slots, 256)), dim3(256), 0, s,
-                           (const u16*)w, (u16*)ws, c_red, n_out);
-        const void* wb = ws;
+    if (wc && fits && (ws || prepacked)) {
+        const void* wb = prepacked ? w : ws;
+        if (!prepacked) {
+            const int64_t slots = (int64_t)9 * (c_red / KS) * cdiv(n_out, 16) * 64;
+            hipLaunchKernelGGL((k_pack_frag<MODE>), dim3((unsigned)cdiv(slots, 256)), dim3(256), 0, s,
+                               (const u16*)w, (u16*)ws, c_red, n_out);
+        }
 #define SVTAD_WIDE_CASE(CR, FM, FN, D)                                                           \
     if (wc->cr == CR) {                                                                          \
         launch_wide_fm<T, MODE, CR, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); \
@@ -969,14 +1079,27 @@ static void gg_dispatch(const void* src, const int32_t* nbr, const void* w, cons
 
 void gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
-             int64_t tpb, void* ws, hipStream_t s) {
+             int64_t tpb, void* ws, bool prepacked, hipStream_t s) {
     if (dtype == SVTAD_F16) {
-        if (mode == MODE_FWD) gg_dispatch<f16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, s);
-        else gg_dispatch<f16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, s);
+        if (mode == MODE_FWD) gg_dispatch<f16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, s);
+        else gg_dispatch<f16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, s);
     } else {
-        if (mode == MODE_FWD) gg_dispatch<bf16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, s);
-        else gg_dispatch<bf16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, s);
+        if (mode == MODE_FWD) gg_dispatch<bf16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, s);
+        else gg_dispatch<bf16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, s);
     }
+}
+
+bool gg_mfma_packed_ok(int dtype, int64_t n, int c_red, int n_out) {
+    return gg_mfma_workspace(dtype, c_red, n_out) > 0 && n * c_red * 2 < (int64_t)INT32_MAX &&
+           9LL * c_red * n_out * 2 < (int64_t)INT32_MAX;
+}
+
+void pack_weight(const void* w, void* wf_fwd, void* wf_bwd, int c_in, int c_out, hipStream_t s) {
+    const int64_t sf = wf_fwd ? (int64_t)9 * (c_in / KS) * cdiv(c_out, 16) * 64 : 0;
+    const int64_t sb = wf_bwd ? (int64_t)9 * (c_out / KS) * cdiv(c_in, 16) * 64 : 0;
+    if (sf + sb == 0) return;
+    hipLaunchKernelGGL(k_pack_both, dim3((unsigned)cdiv(sf + sb, 256)), dim3(256), 0, s, (const u16*)w,
+                       (u16*)wf_fwd, (u16*)wf_bwd, c_in, c_out, sf, sb);
 }
 
 bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out) {
@@ -1000,13 +1123,15 @@ static void launch_bw(const BwPlan& p, const void* go, const void* x, const int3
                        p.rows_per_split, nci, nco, blocks);
 }
 
-// Large-tile backward-weight configurations (wave tile FM x FN fragments):
-// (ci tile, co tile) = (32*FM, 32*FN).
-struct BigCfg { int fm, fn; };
+// Large-tile backward-weight configurations: WGM x WGN waves, each with
+// FM x FN fragments, so (ci tile, co tile) = (16*WGM*FM, 16*WGN*FN). Eight
+// waves put two on every SIMD (one wave alone cannot keep the matrix core
+// busy).
+struct BigCfg { int fm, fn, wgm, wgn; };
 static bool big_cfg(int c_in, int c_out, BigCfg* out) {
-    static const BigCfg cands[] = {{6, 6}, {4, 8}, {4, 4}, {3, 3}, {2, 2}};
+    static const BigCfg cands[] = {{6, 3, 2, 4}, {4, 4, 2, 4}, {4, 2, 2, 4}, {3, 3, 2, 2}, {2, 2, 2, 2}};
     for (const BigCfg& c : cands) {
-        const int bm = 32 * c.fm, bn = 32 * c.fn;
+        const int bm = 16 * c.wgm * c.fm, bn = 16 * c.wgn * c.fn;
         if (c_in % bm == 0 && c_out % bn == 0) {
             *out = c;
             return true;
@@ -1018,23 +1143,23 @@ static bool big_cfg(int c_in, int c_out, BigCfg* out) {
 void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn) {
     BigCfg c;
     if (big_cfg(c_in, c_out, &c)) {
-        *tm = 32 * c.fm;
-        *tn = 32 * c.fn;
+        *tm = 16 * c.wgm * c.fm;
+        *tn = 16 * c.wgn * c.fn;
     } else {
         *tm = bw_mfma_tile(c_in);
         *tn = bw_mfma_tile(c_out);
     }
 }
 
-template <typename T, int FM, int FN>
+template <typename T, int FM, int FN, int WGM, int WGN>
 static void launch_big(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
                        float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
                        hipStream_t s) {
-    constexpr int BM = 2 * FM * 16, BN = 2 * FN * 16;
+    constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
     const int nci = (int)cdiv(c_in, BM), nco = (int)cdiv(c_out, BN);
     const int64_t blocks = (int64_t)9 * nci * nco * p.splits;
-    hipLaunchKernelGGL((k_bw_big<T, FM, FN>), dim3((unsigned)blocks), dim3(256), 0, s,
-                       (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
+    hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks), dim3(64 * WGM * WGN),
+                       0, s, (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
                        p.rows_per_split, nci, nco, blocks);
 }
 
@@ -1044,16 +1169,16 @@ static void bw_dispatch(const BwPlan& p, const void* go, const void* x, const in
                         hipStream_t s) {
     BigCfg bc;
     if (big_cfg(c_in, c_out, &bc)) {
-#define SVTAD_BIG_CASE(M, N)                                                                     \
-    if (bc.fm == M && bc.fn == N) {                                                              \
-        launch_big<T, M, N>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);               \
-        return;                                                                                  \
+#define SVTAD_BIG_CASE(M, N, WM, WN)                                                          \
+    if (bc.fm == M && bc.fn == N && bc.wgm == WM && bc.wgn == WN) {                           \
+        launch_big<T, M, N, WM, WN>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);    \
+        return;                                                                               \
     }
-        SVTAD_BIG_CASE(6, 6)
-        SVTAD_BIG_CASE(4, 8)
-        SVTAD_BIG_CASE(4, 4)
-        SVTAD_BIG_CASE(3, 3)
-        SVTAD_BIG_CASE(2, 2)
+        SVTAD_BIG_CASE(6, 3, 2, 4)
+        SVTAD_BIG_CASE(4, 4, 2, 4)
+        SVTAD_BIG_CASE(4, 2, 2, 4)
+        SVTAD_BIG_CASE(3, 3, 2, 2)
+        SVTAD_BIG_CASE(2, 2, 2, 2)
 #undef SVTAD_BIG_CASE
     }
     const int tm = bw_mfma_tile(c_in), tn = bw_mfma_tile(c_out);
@@ -1081,6 +1206,22 @@ void bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const in
     float* part_b = gb ? part + (int64_t)p.splits * 9 * c_in * c_out : nullptr;
     if (dtype == SVTAD_F16) bw_dispatch<f16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
     else bw_dispatch<bf16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
+    if (!gw) return;  // partials only
+    BigCfg bc;
+    if (big_cfg(c_in, c_out, &bc)) {
+        const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
+        const int64_t threads = (int64_t)9 * c_in * c_out / 4 + (gb ? c_out : 0);
+        const dim3 grid((unsigned)cdiv(threads, 256));
+        if (dtype == SVTAD_F16)
+            hipLaunchKernelGGL((k_bw_reduce<f16>), grid, dim3(256), 0, s, (const float*)part,
+                               (const float*)part_b, p.splits, c_in, c_out, bc.fm, bc.fn, bc.wgm,
+                               bc.wgn, nci, nco, (f16*)gw, (f16*)gb);
+        else
+            hipLaunchKernelGGL((k_bw_reduce<bf16>), grid, dim3(256), 0, s, (const float*)part,
+                               (const float*)part_b, p.splits, c_in, c_out, bc.fm, bc.fn, bc.wgm,
+                               bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb);
+        return;
+    }
     split_reduce(dtype, part, 9LL * c_in * c_out, p.splits, gw, s);
     if (gb) split_reduce(dtype, part_b, (int64_t)c_out, p.splits, gb, s);
 }

@@ -417,6 +417,7 @@ static void launch_bw_valu(const BwPlan& p, const void* go, const void* x, const
     dim3 grid((unsigned)cdiv(c_out, 64), (unsigned)(9 * n_ci_tiles), (unsigned)p.splits);
     hipLaunchKernelGGL((k_bw_valu<T>), grid, dim3(256), 0, s, (const T*)go, (const T*)x, nbr, part,
                        part_b, n, c_in, c_out, tpb, p.rows_per_split, n_ci_tiles);
+    if (!gw) return;  // partials only
     split_reduce(dtype_of<T>(), part, 9LL * c_in * c_out, p.splits, gw, s);
     if (gb) split_reduce(dtype_of<T>(), part_b, (int64_t)c_out, p.splits, gb, s);
 }

@@ -45,9 +45,16 @@ bool gg_mfma_supported(int dtype, int c_red, int n_out);
 // reduction width c_red and n_out columns needs; 0 when the shape takes a
 // kernel that reads w directly.
 size_t gg_mfma_workspace(int dtype, int c_red, int n_out);
+// w is the raw weight (ws holds room for its packed form, packed here) or,
+// with prepacked, the fragment-ordered weight itself.
 void gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
-             int64_t tpb, void* ws, hipStream_t s);
+             int64_t tpb, void* ws, bool prepacked, hipStream_t s);
+// Whether the fragment-ordered (prepacked) entry points handle this shape.
+bool gg_mfma_packed_ok(int dtype, int64_t n, int c_red, int n_out);
+// Fragment-ordered weights for the forward (wf_fwd) and backward-input
+// (wf_bwd) gathered GEMMs, one launch; either may be NULL.
+void pack_weight(const void* w, void* wf_fwd, void* wf_bwd, int c_in, int c_out, hipStream_t s);
 bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out);
 // Rows per split of the MFMA backward-weight (its row list lives in LDS).
 constexpr int kMaxSplitRows = 2048;

@@ -140,6 +140,68 @@ at::Tensor op_fwd_bias(const at::Tensor& x, const at::Tensor& nbr, const at::Ten
     return conv_fwd(x, nbr, w, bias, tpb, (int)bias_mode, -1);
 }
 
+// pack_weight(weight, fwd, bwd) -> (packed_fwd, packed_bwd): the weight in the
+// fragment order of the matrix-core kernels; an empty tensor for a layout not
+// requested or not available for this shape / dtype.
+std::tuple<at::Tensor, at::Tensor> op_pack_weight(const at::Tensor& w_in, bool fwd, bool bwd) {
+    check_gpu(w_in, "weight");
+    TORCH_CHECK(w_in.dim() == 3 && w_in.size(0) == 9, "weight must be (9, C_in, C_out)");
+    at::Tensor w = w_in.contiguous();
+    const int c_in = (int)w.size(1), c_out = (int)w.size(2);
+    const int dt = dtype_code(w);
+    const size_t bf = fwd ? svtad_fwd_workspace_bytes(c_in, c_out, dt) : 0;
+    const size_t bb = bwd ? svtad_bwd_in_workspace_bytes(c_in, c_out, dt) : 0;
+    c10::DeviceGuard g(w.device());
+    at::Tensor pf = at::empty({(int64_t)bf}, w.options().dtype(at::kByte));
+    at::Tensor pb = at::empty({(int64_t)bb}, w.options().dtype(at::kByte));
+    if (bf || bb)
+        check_status(svtad_pack_weight(w.data_ptr(), bf ? pf.data_ptr() : nullptr,
+                                       bb ? pb.data_ptr() : nullptr, c_in, c_out, dt, stream_of(w)),
+                     "pack_weight");
+    return {pf, pb};
+}
+
+// fwd_packed(x, neighbor_indices, weight, packed_fwd, bias, tokens_per_batch,
+// bias_mode): fwd_bias with a weight packed by pack_weight (falls back to
+// fwd_bias when packed_fwd is empty or the shape has no packed path).
+at::Tensor op_fwd_packed(const at::Tensor& x_in, const at::Tensor& nbr_in, const at::Tensor& w,
+                         const at::Tensor& packed, const c10::optional<at::Tensor>& bias_in,
+                         int64_t tpb, int64_t bias_mode) {
+    TORCH_CHECK(bias_mode >= 0 && bias_mode <= 2, "bias_mode must be 0, 1 or 2");
+    if (packed.numel() == 0) return conv_fwd(x_in, nbr_in, w, bias_in, tpb, (int)bias_mode, -1);
+    check_gpu(x_in, "x");
+    at::Tensor x = rows_view(x_in);
+    const int64_t c_in = x.size(-1), n = n_rows(x);
+    TORCH_CHECK(w.dim() == 3 && w.size(0) == 9 && w.size(1) == c_in, "weight must be (9, C_in, C_out)");
+    TORCH_CHECK(w.scalar_type() == x.scalar_type(), "x and weight dtypes differ");
+    const int64_t c_out = w.size(2);
+    const int dt = dtype_code(x);
+    TORCH_CHECK((size_t)packed.numel() == svtad_fwd_workspace_bytes((int)c_in, (int)c_out, dt),
+                "packed_fwd does not match the weight");
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    int mode = (int)bias_mode;
+    at::Tensor bias;
+    if (mode != SVTAD_BIAS_NONE && bias_present(bias_in)) {
+        TORCH_CHECK(bias_in->numel() == c_out, "bias must have C_out = ", c_out, " elements");
+        if (mode == SVTAD_BIAS_FP32 && bias_in->scalar_type() == x.scalar_type()) {
+            mode = SVTAD_BIAS_PRE;
+            bias = bias_in->contiguous();
+        } else {
+            bias = bias_in->to(x.device(), mode == SVTAD_BIAS_FP32 ? at::kFloat : x.scalar_type()).contiguous();
+        }
+    } else {
+        mode = SVTAD_BIAS_NONE;
+    }
+    at::Tensor out = at::empty({n, c_out}, x.options());
+    const int st = svtad_fwd_packed(x.data_ptr(), nbr.data_ptr<int32_t>(), packed.data_ptr(),
+                                    bias.defined() ? bias.data_ptr() : nullptr, mode, out.data_ptr(),
+                                    n, (int)c_in, (int)c_out, tpb, dt, stream_of(x));
+    if (st == SVTAD_ERR_UNSUPPORTED) return conv_fwd(x_in, nbr_in, w, bias_in, tpb, (int)bias_mode, -1);
+    check_status(st, "fwd_packed");
+    return out;
+}
+
 // bwd_in(grad_output, neighbor_indices, weight, n_kept, C_in, tokens_per_batch)
 // -> [n_kept, C_in] in grad_output's dtype (2d_sparse_v3.cu:824-835)
 at::Tensor op_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
@@ -164,6 +226,34 @@ at::Tensor op_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const at
                                 ws.defined() ? ws.data_ptr() : nullptr, ws_bytes, n_kept, (int)c_in,
                                 (int)c_out, tpb, dt, stream_of(go));
     check_status(st, "bwd_in");
+    return gi;
+}
+
+// bwd_in_packed(grad_output, neighbor_indices, weight, packed_bwd, n_kept, C_in,
+// tokens_per_batch): bwd_in with a weight packed by pack_weight (falls back to
+// bwd_in when packed_bwd is empty or the shape has no packed path).
+at::Tensor op_bwd_in_packed(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
+                            const at::Tensor& packed, int64_t n_kept, int64_t c_in, int64_t tpb) {
+    if (packed.numel() == 0) return op_bwd_in(go_in, nbr_in, w_in, n_kept, c_in, tpb);
+    check_gpu(go_in, "grad_output");
+    at::Tensor go = rows_view(go_in);
+    const int64_t c_out = go.size(-1);
+    TORCH_CHECK(n_rows(go) == n_kept, "grad_output has ", n_rows(go), " rows, n_kept = ", n_kept);
+    TORCH_CHECK(w_in.dim() == 3 && w_in.size(0) == 9 && w_in.size(1) == c_in && w_in.size(2) == c_out,
+                "weight must be (9, ", c_in, ", ", c_out, ")");
+    TORCH_CHECK(w_in.scalar_type() == go.scalar_type(), "grad_output and weight dtypes differ");
+    const int dt = dtype_code(go);
+    TORCH_CHECK((size_t)packed.numel() == svtad_bwd_in_workspace_bytes((int)c_in, (int)c_out, dt),
+                "packed_bwd does not match the weight");
+    at::Tensor w = w_in.contiguous();
+    at::Tensor nbr = table_i32(nbr_in, n_kept);
+    c10::DeviceGuard g(go.device());
+    at::Tensor gi = at::empty({n_kept, c_in}, go.options());
+    const int st = svtad_bwd_in_packed(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                                       packed.data_ptr(), gi.data_ptr(), n_kept, (int)c_in,
+                                       (int)c_out, tpb, dt, stream_of(go));
+    if (st == SVTAD_ERR_UNSUPPORTED) return op_bwd_in(go_in, nbr_in, w_in, n_kept, c_in, tpb);
+    check_status(st, "bwd_in_packed");
     return gi;
 }
 
@@ -194,6 +284,32 @@ std::tuple<at::Tensor, at::Tensor> op_bwd_w_bias(const at::Tensor& go_in, const 
                                (int)c_in, (int)c_out, tpb, dt, stream_of(x));
     check_status(st, "bwd_w");
     return {gw, with_bias ? gb : at::empty({0}, x.options())};
+}
+
+// bwd_w_partials(grad_output, x, neighbor_indices, C_in, tokens_per_batch, with_bias)
+// -> workspace bytes holding the row-split partial sums only (no reduction).
+// For timing the partial-sum kernel of backward-weight on its own.
+at::Tensor op_bwd_w_partials(const at::Tensor& go_in, const at::Tensor& x_in, const at::Tensor& nbr_in,
+                             int64_t c_in, int64_t tpb, bool with_bias) {
+    check_gpu(go_in, "grad_output");
+    check_gpu(x_in, "x");
+    at::Tensor go = rows_view(go_in);
+    at::Tensor x = rows_view(x_in);
+    TORCH_CHECK(x.size(-1) == c_in, "x has ", x.size(-1), " channels, C_in = ", c_in);
+    const int64_t n = n_rows(x), c_out = go.size(-1);
+    TORCH_CHECK(n_rows(go) == n && go.scalar_type() == x.scalar_type(), "grad_output must match x");
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    const int dt = dtype_code(x);
+    const size_t ws_bytes = svtad_bwd_w_workspace_bytes(n, (int)c_in, (int)c_out, dt);
+    TORCH_CHECK(ws_bytes > 0, "bwd_w_partials: ", svtad_last_error());
+    at::Tensor ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
+    at::Tensor gb = with_bias ? at::empty({c_out}, x.options()) : at::Tensor();
+    check_status(svtad_bwd_w(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), nullptr,
+                             with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
+                             (int)c_in, (int)c_out, tpb, dt, stream_of(x)),
+                 "bwd_w_partials");
+    return ws;
 }
 
 // bwd_w(grad_output, x, neighbor_indices, C_in, tokens_per_batch) -> [9, C_in, C_out]
@@ -368,6 +484,17 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.def("fwd_bias", &op_fwd_bias, "Forward with bias_mode 0 none / 1 fp32 / 2 after rounding",
           py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"), py::arg("bias"),
           py::arg("tokens_per_batch"), py::arg("bias_mode"));
+    m.def("pack_weight", &op_pack_weight, "Weight in the matrix-core fragment order (fwd, bwd_in)",
+          py::arg("weight"), py::arg("fwd") = true, py::arg("bwd") = true);
+    m.def("fwd_packed", &op_fwd_packed, "fwd_bias with a packed weight", py::arg("x"),
+          py::arg("neighbor_indices"), py::arg("weight"), py::arg("packed_fwd"), py::arg("bias"),
+          py::arg("tokens_per_batch"), py::arg("bias_mode"));
+    m.def("bwd_in_packed", &op_bwd_in_packed, "bwd_in with a packed weight", py::arg("grad_output"),
+          py::arg("neighbor_indices"), py::arg("weight"), py::arg("packed_bwd"), py::arg("n_kept"),
+          py::arg("C_in"), py::arg("tokens_per_batch"));
+    m.def("bwd_w_partials", &op_bwd_w_partials, "Backward-weight partial sums only (timing)",
+          py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("C_in"),
+          py::arg("tokens_per_batch"), py::arg("with_bias"));
     m.def("bwd_w_bias", &op_bwd_w_bias, "Backward weight and bias", py::arg("grad_output"),
           py::arg("x"), py::arg("neighbor_indices"), py::arg("C_in"), py::arg("tokens_per_batch"),
           py::arg("with_bias"));

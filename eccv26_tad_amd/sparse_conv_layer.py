@@ -42,7 +42,6 @@ class SparseConv2dFunction(Function):
         _, C_in, C_out = weight.shape
         if C_in % 4 != 0:
             raise ValueError(f"C_in ({C_in}) must be divisible by 4 for optimized kernel.")
-        ctx.save_for_backward(x, neighbor_indices, weight, bias)
         ctx.C_in = C_in
         ctx.tokens_per_batch = tokens_per_batch
         if bias is None:
@@ -51,18 +50,23 @@ class SparseConv2dFunction(Function):
             mode = BIAS_FP32
         else:
             mode = BIAS_AFTER
-        return _ops.fwd_bias(x, neighbor_indices, weight, bias, tokens_per_batch, mode)
+        # Both matrix-core weight layouts in one launch; the backward-input one
+        # is kept for backward (empty tensors where the shape has none).
+        packed_fwd, packed_bwd = _ops.pack_weight(weight, True, bool(ctx.needs_input_grad[0]))
+        ctx.save_for_backward(x, neighbor_indices, weight, bias, packed_bwd)
+        return _ops.fwd_packed(x, neighbor_indices, weight, packed_fwd, bias, tokens_per_batch, mode)
 
     @staticmethod
     @custom_bwd
     def backward(ctx, grad_output):
-        x, neighbor_indices, weight, bias = ctx.saved_tensors
+        x, neighbor_indices, weight, bias, packed_bwd = ctx.saved_tensors
         C_in = ctx.C_in
         tpb = ctx.tokens_per_batch
         go = grad_output.contiguous()
         grad_input = grad_weight = grad_bias = None
         if ctx.needs_input_grad[0]:
-            grad_input = _ops.bwd_in(go, neighbor_indices, weight, x.numel() // x.shape[-1], C_in, tpb)
+            grad_input = _ops.bwd_in_packed(go, neighbor_indices, weight, packed_bwd,
+                                            x.numel() // x.shape[-1], C_in, tpb)
             if x.dim() == 3:
                 grad_input = grad_input.view(x.shape)
         need_b = bias is not None and ctx.needs_input_grad[3]

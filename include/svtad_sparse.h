@@ -102,6 +102,27 @@ int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight, v
                  void* workspace, size_t workspace_bytes, int64_t n, int c_in, int c_out,
                  int64_t tokens_per_batch, int dtype, void* stream);
 
+/*
+ * Pre-packed weights (no counterpart in the reference; the autograd wrapper
+ * packs once per forward and reuses the backward layout, where the entry
+ * points above repack per call). svtad_pack_weight writes the weight
+ * [9, c_in, c_out] in the order the matrix-core kernels read it: packed_fwd
+ * holds svtad_fwd_workspace_bytes() bytes, packed_bwd
+ * svtad_bwd_in_workspace_bytes(); either may be NULL. The packed entry points
+ * compute exactly what svtad_fwd / svtad_bwd_in compute and return
+ * SVTAD_ERR_UNSUPPORTED for shapes without a packed layout (both workspace
+ * sizes 0). svtad_bwd_in_packed also takes the raw weight for table entries
+ * whose transpose is absent.
+ */
+int svtad_pack_weight(const void* weight, void* packed_fwd, void* packed_bwd, int c_in, int c_out,
+                      int dtype, void* stream);
+int svtad_fwd_packed(const void* x, const int32_t* nbr, const void* packed_fwd, const void* bias,
+                     int bias_mode, void* out, int64_t n, int c_in, int c_out,
+                     int64_t tokens_per_batch, int dtype, void* stream);
+int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* weight,
+                        const void* packed_bwd, void* grad_in, int64_t n, int c_in, int c_out,
+                        int64_t tokens_per_batch, int dtype, void* stream);
+
 /* Workspace bytes needed by svtad_bwd_w for this shape. */
 size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, int dtype);
 
@@ -110,6 +131,8 @@ size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, int dtype);
  * deterministic per-offset reduction (row-split fp32 partials in `workspace`,
  * then an ordered sum). If grad_bias is not NULL it also writes
  * grad_bias[co] = sum_i go[i,co] (sparse_conv_layer.py:120-121).
+ * With grad_w == NULL only the row-split partial sums are written to the
+ * workspace (for timing the partial-sum kernel alone; layout internal).
  * Replaces `bwd_w` / launch_bwd_w (2d_sparse_v3_bind.cpp:11, 2d_sparse_v3.cu:837-850).
  */
 int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,

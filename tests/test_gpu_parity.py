@@ -188,6 +188,7 @@ CONV_CASES = [
     ((1, 4, 16, 16), 0.4, 256, 128, "bfloat16"),
     ((1, 8, 14, 14), 0.5, 48, 48, "float16"),      # config-1 channels on the matrix cores
     ((1, 3, 9, 11), 0.7, 40, 24, "float16"),       # widths that are not tile multiples
+    ((1, 8, 16, 16), 0.5, 512, 512, "bfloat16"),   # backward-weight wider than one co-resident grid
 ]
 
 
@@ -436,3 +437,31 @@ def test_backward_is_deterministic(dev, oracle):
     w1 = ops.bwd_w(G, X, T, 192, 0)
     w2 = ops.bwd_w(G, X, T, 192, 0)
     assert torch.equal(a1, a2) and torch.equal(w1, w2)
+
+
+@pytest.mark.parametrize("ci,co,dname", [(192, 192, "float16"), (256, 256, "bfloat16"), (128, 96, "float16")])
+def test_packed_entry_points_match(dev, oracle, ci, co, dname):
+    """pack_weight + fwd_packed / bwd_in_packed (the autograd path) give exactly
+    what fwd_bias / bwd_in give (same kernels, same order)."""
+    import opentad_sparse_ops as ops
+    import torch
+
+    _say("packed", ci, co, dname)
+    dt = _dt(dname)
+    mask, x, w, b, go = _conv_case(11, (2, 6, 14, 14), 0.55, ci, co, dname)
+    t = oracle.build_table(mask)
+    X, W, Bb, G = (_t(a, dev, dt) for a in (x, w, b, go))
+    T = _t(t, dev, _dt("int32"))
+    pf, pb = ops.pack_weight(W, True, True)
+    # a layout exists for reduction widths 64/128/192/256/512; C_out = 96 has
+    # none for backward-input (empty tensor -> the per-call path)
+    assert pf.numel() > 0 and (pb.numel() > 0) == (co in (64, 128, 192, 256, 512))
+    for mode in (0, 1, 2):
+        assert torch.equal(ops.fwd_packed(X, T, W, pf, Bb, 0, mode), ops.fwd_bias(X, T, W, Bb, 0, mode))
+    assert torch.equal(ops.bwd_in_packed(G, T, W, pb, x.shape[0], ci, 0), ops.bwd_in(G, T, W, x.shape[0], ci, 0))
+    # empty packed tensors fall back to the per-call path
+    empty = torch.empty(0, dtype=torch.uint8, device=dev)
+    assert torch.equal(ops.fwd_packed(X, T, W, empty, Bb, 0, 1), ops.fwd_bias(X, T, W, Bb, 0, 1))
+    f32 = W.float()
+    pf32, pb32 = ops.pack_weight(f32, True, True)
+    assert pf32.numel() == 0 and pb32.numel() == 0
