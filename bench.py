@@ -69,6 +69,24 @@ def op_bytes(n, ci, co, s):
     return {"fwd": fwd, "bwd_in": bwd_in, "bwd_w": bwd_w}
 
 
+TRAFFIC_PROFILE = os.path.join("profiles", "sparseconv2d_c2_keep055_hbm_traffic.md")
+
+
+def pmc_traffic(kernel_key):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, KiB per dispatch) of the
+    kernel whose name contains kernel_key, from the committed rocprofv3 --pmc
+    summary of this workload at keep 0.55; None if absent."""
+    try:
+        with open(os.path.join(ROOT, TRAFFIC_PROFILE)) as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 4 and kernel_key in cells[0]:
+                    return int((float(cells[2]) + float(cells[3])) * 1024)
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def time_events(fn, reps, warm=3):
     """Average ms per call of fn() from HIP events on torch's current stream,
     the stream the extension launches on."""
@@ -317,7 +335,10 @@ def main():
         roof = {"bound": "hbm", "achieved": round(by_dom / t_dom / 1e9, 3),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 5)
-    roof["traffic"] = None
+    key = "k_gg_wideIDF16_Li0" if dom == "fwd" else "k_bw_big"
+    roof["traffic"] = pmc_traffic(key) if abs(args.keep - 0.55) < 1e-9 else None
+    if roof["traffic"] is not None:
+        roof["traffic_source"] = TRAFFIC_PROFILE
     roof["kernel"] = {"fwd": "k_gg_wide (forward gathered GEMM)",
                       "bwd_w_partials": "k_bw_big (backward-weight partial sums)"}[dom]
     roof["kernel_us"] = round(phases[dom] * 1e3, 2)
