@@ -711,12 +711,13 @@ __global__ __launch_bounds__(256) void k_bw_mfma(
 // Backward-weight partials, large tiles (the shapes of the adapter convs).
 // A workgroup owns one offset k, a BM x BN (ci x co) tile of gw and one row
 // split. Per 64-row stage each thread loads an 8-row x 8-channel block of the
-// gathered x rows (or of the go rows) with 16-byte coalesced loads (lanes
-// along the channels), transposes it in registers (v_perm_b32) and writes
-// eight 16-byte rows of a [channel][row] LDS tile; the MFMA fragments (8
-// consecutive rows of one channel) are then single 16-byte LDS reads, and
-// with a 144-byte pitch both the writes and the reads are free of bank
-// conflicts. Two register stages keep the loads of stage t+2 in flight while
+// gathered x rows (or of the go rows) with 16-byte loads (8 lanes take the 8
+// row groups of one channel chunk, so each row is read 128 contiguous bytes
+// at a time), transposes it in registers (v_perm_b32) and writes eight
+// 16-byte rows of a [channel][row] LDS tile; the MFMA fragments (8
+// consecutive rows of one channel) are then single 16-byte LDS reads. With a
+// 144-byte pitch the reads are free of bank conflicts, and so are the writes:
+// the 8 lanes of a group write one 128-byte span of a transposed row. Two register stages keep the loads of stage t+2 in flight while
 // stage t runs. Partials are stored in fragment order (each lane's 4 values
 // contiguous); k_bw_reduce sums the splits in a fixed order. The k == 4,
 // ci-tile 0 workgroups also sum the staged go rows per column (bias).
@@ -791,6 +792,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
     constexpr int B_ITEMS = (KR / 8) * (BN / 8);
     constexpr int ITEMS = A_ITEMS + B_ITEMS;
     constexpr int PER = (ITEMS + NT - 1) / NT;
+    // Row groups per stage. Consecutive items take consecutive row groups of
+    // one 8-channel chunk, so each 8 lanes store 8 adjacent 16-byte slots of
+    // one transposed row (128 bytes over all banks); items that walked the
+    // channel chunks instead stored 8 rows (1152 bytes) apart, all on the
+    // same four banks.
+    constexpr int RG = KR / 8;
 
     __shared__ __align__(16) u16 As[2][BM][TP];
     __shared__ __align__(16) u16 Bs[2][BN][TP];
@@ -820,7 +827,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
     const rsrc_t rs_x = make_rsrc(x, (uint32_t)(n * c_in * 2));
     const rsrc_t rs_g = make_rsrc(go + r_begin * c_out, (uint32_t)((int64_t)rows * c_out * 2));
 
-    // item e < A_ITEMS: rows 8*(e / (BM/8)) .. +7, channels 8*(e % (BM/8)) of x;
+    // item e < A_ITEMS: rows 8*(e % RG) .. +7, channels 8*(e / RG) of x;
     // else the same for go with BN. Stages at or past `steps` load zeros.
     u32x4 r0s[PER][8], r1s[PER][8];
     auto load = [&](int t, u32x4 (*rg)[8]) {
@@ -830,7 +837,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
         for (int q = 0; q < PER; ++q) {
             const int e = tid + q * NT;
             if (e < A_ITEMS) {
-                const int rgp = e / (BM / 8), c = ci0 + (e - rgp * (BM / 8)) * 8;
+                const int rgp = e % RG, c = ci0 + (e / RG) * 8;
                 const bool ok = live && c < c_in;
                 const u32x4 s0 = *(const u32x4*)&srow[rbase + rgp * 8];
                 const u32x4 s1 = *(const u32x4*)&srow[rbase + rgp * 8 + 4];
@@ -841,7 +848,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
                 }
             } else {
                 const int eb = e - A_ITEMS;
-                const int rgp = eb / (BN / 8), c = co0 + (eb - rgp * (BN / 8)) * 8;
+                const int rgp = eb % RG, c = co0 + (eb / RG) * 8;
                 const bool ok = live && e < ITEMS && c < c_out;
 #pragma unroll
                 for (int r = 0; r < 8; ++r)
@@ -857,12 +864,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
             u32x4 o[8];
             transpose8(rg[q], o);
             if (e < A_ITEMS) {
-                const int rgp = e / (BM / 8), cl = (e - rgp * (BM / 8)) * 8;
+                const int rgp = e % RG, cl = (e / RG) * 8;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) *(u32x4*)&As[buf][cl + c][rgp * 8] = o[c];
             } else {
                 const int eb = e - A_ITEMS;
-                const int rgp = eb / (BN / 8), cl = (eb - rgp * (BN / 8)) * 8;
+                const int rgp = eb % RG, cl = (eb / RG) * 8;
 #pragma unroll
                 for (int c = 0; c < 8; ++c) *(u32x4*)&Bs[buf][cl + c][rgp * 8] = o[c];
             }
