@@ -273,15 +273,23 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     constexpr int BM = FM * 16;
     constexpr int BN = 4 * FN * 16;
     constexpr int NC = CR / KS;
-    constexpr int RP = CR + 8;  // LDS row pitch (elements): odd multiple of 16 bytes
+    // A slice rows are CR elements with no padding; 16-byte chunk q of row m is
+    // stored at position q ^ (m & 7) (CR / 8 is a multiple of 8, so the swizzle
+    // stays inside the row). Fragment reads (16 rows x 4 chunks) and the row
+    // stores then both run at the full LDS rate; a 16-byte pad does not.
+    constexpr int RP = CR;
     constexpr int CPR = CR / 8;  // 16-byte chunks per row
+    static_assert(CPR % 8 == 0, "the chunk swizzle needs a multiple of 8 chunks per row");
     constexpr int A_CHUNKS = BM * CPR;
     constexpr int A_PER = (A_CHUNKS + 255) / 256;
+    // rows past BM take the stores of threads without a chunk in the last
+    // round, so every thread stores unconditionally
+    constexpr int APAD = (A_PER * 256 - A_CHUNKS + CPR - 1) / CPR;
     static_assert(NC % D == 0, "ring depth must divide the steps of a slice");
     static_assert(WS == 1 || (size_t)BM * BN * 4 <= sizeof(u16) * 2 * BM * RP,
                   "the partial accumulators of a set must fit in its A buffers");
 
-    __shared__ __align__(16) u16 As[WS][2][BM][RP];
+    __shared__ __align__(16) u16 As[WS][2][BM + APAD][RP];
     __shared__ uint32_t soff[9][BM];  // byte offset of the gathered row, kOOB if missing
     __shared__ int kvalid[9];
     __shared__ int klist[10];
@@ -309,7 +317,7 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
         int c = 0;
         for (int k = 0; k < 9; ++k)
             if (kvalid[k]) klist[c++] = k;
-        for (int q = c; q < 10; ++q) klist[q] = klist[c > 0 ? c - 1 : 0];
+        for (int q = c; q < 10; ++q) klist[q] = c > 0 ? klist[c - 1] : 0;  // always a valid offset
         nk_s = c;
     }
     __syncthreads();
@@ -321,7 +329,11 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const rsrc_t rs_src = make_rsrc(src, (uint32_t)(n * CR * 2));
     const rsrc_t rs_w = make_rsrc(wb, (uint32_t)(9 * NC * ((n_out + 15) / 16)) * 1024u);
 
-    // A slice: the BM gathered rows of one offset, 16-byte chunk e = ltid + q*256
+    // A slice: the BM gathered rows of one offset, 16-byte chunk e = ltid + q*256.
+    // Loads and stores are straight-line (no branch around a load or around
+    // the store that consumes it): a path on which a load is not consumed
+    // makes the compiler wait for every younger load too, including the
+    // weight-ring prefetch.
     u32x4 ra[A_PER];
     auto load_a = [&](int it) {
         const bool live = it < nk_set;
@@ -329,15 +341,17 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
 #pragma unroll
         for (int q = 0; q < A_PER; ++q) {
             const int e = ltid + q * 256;
-            const int m = e < A_CHUNKS ? e / CPR : 0;
-            ra[q] = bload16(rs_src, live && e < A_CHUNKS ? soff[k][m] + (uint32_t)((e - m * CPR) * 16) : kOOB);
+            const int m = min(e / CPR, BM - 1);
+            const uint32_t so = soff[k][m];
+            ra[q] = bload16(rs_src, live && e < A_CHUNKS && so != kOOB ? so + (uint32_t)((e - m * CPR) * 16) : kOOB);
         }
     };
     auto store_a = [&](int buf) {
 #pragma unroll
         for (int q = 0; q < A_PER; ++q) {
             const int e = ltid + q * 256;
-            if (e < A_CHUNKS) *(u32x4*)&As[set][buf][e / CPR][(e - (e / CPR) * CPR) * 8] = ra[q];
+            const int m = e / CPR;
+            *(u32x4*)&As[set][buf][m][((e - m * CPR) ^ (m & 7)) * 8] = ra[q];
         }
     };
 
@@ -345,8 +359,6 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     // 64 lanes of fragment (k, c-step, column block) are 1 KB contiguous, so a
     // fragment load is fully coalesced. Per-lane offsets are fixed; a step adds
     // the wave-uniform slab offset. Steps past the set's end reload its last step.
-    const int ncol = col0 + wave * FN * 16 + (lane & 15);
-    const int kof = (lane >> 4) * 8;
     const int nf = (n_out + 15) / 16;
     uint32_t boff[FN];
 #pragma unroll
@@ -376,23 +388,28 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     __syncthreads();
 
     const int arow = lane & 15;
+    // chunk of step c is 4c + lane/16, stored at (4c + lane/16) ^ (lane & 7):
+    // 4c + t for even c and 4(c-1) + (t ^ 4) for odd c, t = lane/16 ^ lane&7
+    const int sw = ((lane >> 4) ^ (lane & 7)) * 8;
+    const int swz[2] = {sw, sw ^ 32};
+    // With two wave sets, a set with fewer slices than `iters` skips its
+    // last iteration's MFMAs (the other set's waves share its SIMDs); with
+    // one set every iteration is live and the loop has no branch.
     for (int it = 0; it < iters; ++it) {
         const int buf = it & 1;
-        const bool live = it < nk_set;  // uniform per wave set
         load_a(it + 1);
-        if (live) {
+        if (WS == 1 || it < nk_set)
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const int d = c % D;
-                u32x4 fa[FM];
+        for (int c = 0; c < NC; ++c) {
+            const int d = c % D;
+            u32x4 fa[FM];
 #pragma unroll
-                for (int a = 0; a < FM; ++a) fa[a] = *(const u32x4*)&As[set][buf][a * 16 + arow][c * KS + kof];
+            for (int a = 0; a < FM; ++a) fa[a] = *(const u32x4*)&As[set][buf][a * 16 + arow][(c & ~1) * KS + swz[c & 1]];
 #pragma unroll
-                for (int a = 0; a < FM; ++a)
+            for (int a = 0; a < FM; ++a)
 #pragma unroll
-                    for (int f = 0; f < FN; ++f) acc[a][f] = MfmaOp<T>::run(fa[a], ring[d][f], acc[a][f]);
-                load_b(it * NC + c + D, ring[d]);
-            }
+                for (int f = 0; f < FN; ++f) acc[a][f] = MfmaOp<T>::run(fa[a], ring[d][f], acc[a][f]);
+            load_b(it * NC + c + D, ring[d]);
         }
         store_a(buf ^ 1);
         __syncthreads();
@@ -711,18 +728,26 @@ __global__ __launch_bounds__(256) void k_bw_mfma(
 // Backward-weight partials, large tiles (the shapes of the adapter convs).
 // A workgroup owns one offset k, a BM x BN (ci x co) tile of gw and one row
 // split. Per 64-row stage each thread loads an 8-row x 8-channel block of the
-// gathered x rows (or of the go rows) with 16-byte loads (8 lanes take the 8
-// row groups of one channel chunk, so each row is read 128 contiguous bytes
-// at a time), transposes it in registers (v_perm_b32) and writes eight
-// 16-byte rows of a [channel][row] LDS tile; the MFMA fragments (8
-// consecutive rows of one channel) are then single 16-byte LDS reads. With a
-// 144-byte pitch the reads are free of bank conflicts, and so are the writes:
-// the 8 lanes of a group write one 128-byte span of a transposed row. Two register stages keep the loads of stage t+2 in flight while
+// gathered x rows (or of the go rows) with 16-byte loads (consecutive lanes
+// on consecutive channel chunks of a row), transposes it in registers
+// (v_perm_b32) and writes eight 16-byte rows of a [channel][row] LDS tile
+// (swizzled by bw_swz); the MFMA fragments (8 consecutive rows of one
+// channel) are then single 16-byte LDS reads. Each wave stages only x or only
+// go rows. Two register stages keep the loads of stage t+2 in flight while
 // stage t runs. Partials are stored in fragment order (each lane's 4 values
 // contiguous); k_bw_reduce sums the splits in a fixed order. The k == 4,
 // ci-tile 0 workgroups also sum the staged go rows per column (bias).
 // ---------------------------------------------------------------------------
-constexpr int TP = KR + 8;  // pitch of a transposed stage: 72 elements = 144 bytes
+// A transposed stage row (one channel, KR = 64 source rows) is 128 bytes with
+// no padding; its eight 16-byte chunks (8 rows each) are stored at position
+// chunk ^ (channel & 7) ^ ((channel >> 3) & 7). The MFMA fragment reads (16
+// consecutive channels x 4 chunks per instruction) and the transposed stores
+// (8 lanes on 8 consecutive channel chunks, i.e. channels 8 apart) then both
+// run at the full LDS rate on gfx950; a padded 144-byte pitch halves the
+// fragment-read rate. Returns the element offset in the row.
+__device__ __forceinline__ int bw_swz(int channel, int chunk) {
+    return (chunk ^ (channel & 7) ^ ((channel >> 3) & 7)) * 8;
+}
 
 // 8x8 transpose of 16-bit values: in[r] holds channels 0..7 of row r; out[c]
 // gets rows 0..7 of channel c.
@@ -790,17 +815,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
     constexpr int BN = WGN * FN * 16;  // co
     constexpr int A_ITEMS = (KR / 8) * (BM / 8);  // 8x8 blocks per stage
     constexpr int B_ITEMS = (KR / 8) * (BN / 8);
-    constexpr int ITEMS = A_ITEMS + B_ITEMS;
-    constexpr int PER = (ITEMS + NT - 1) / NT;
-    // Row groups per stage. Consecutive items take consecutive row groups of
-    // one 8-channel chunk, so each 8 lanes store 8 adjacent 16-byte slots of
-    // one transposed row (128 bytes over all banks); items that walked the
-    // channel chunks instead stored 8 rows (1152 bytes) apart, all on the
-    // same four banks.
-    constexpr int RG = KR / 8;
+    // Consecutive items walk the 8-channel chunks of one row group, so four
+    // consecutive lanes load 64 contiguous bytes of a row (lanes walking the
+    // row groups instead load 16 bytes from each of 8 rows per 8 lanes, which
+    // costs more address-unit cycles than the LDS conflicts it avoids; the
+    // bw_swz swizzle keeps the chunk-major stores conflict-free).
+    constexpr int CPT_A = BM / 8, CPT_B = BN / 8;  // channel chunks per row group
+    // Each wave stages one operand: waves [0, WA) the gathered x rows (A
+    // items), waves [WA, WA + WB) the go rows (B items), any others nothing.
+    // With a wave-uniform role the loads are one straight-line path writing
+    // one register set; two load paths writing the same registers (even if
+    // a wave only ever takes one) make the compiler wait for every load in
+    // flight before issuing the next stage's, which serialises the prefetch.
+    constexpr int WA = (A_ITEMS + 63) / 64, WB = (B_ITEMS + 63) / 64;
+    static_assert(WA + WB <= NT / 64, "one staging item per thread");
 
-    __shared__ __align__(16) u16 As[2][BM][TP];
-    __shared__ __align__(16) u16 Bs[2][BN][TP];
+    __shared__ __align__(16) u16 As[2][BM][KR];
+    __shared__ __align__(16) u16 Bs[2][BN][KR];
     __shared__ __align__(16) uint32_t srow[kMaxSplitRows];
 
     const int tid = threadIdx.x;
@@ -824,55 +855,44 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
     }
     __syncthreads();
 
-    const rsrc_t rs_x = make_rsrc(x, (uint32_t)(n * c_in * 2));
-    const rsrc_t rs_g = make_rsrc(go + r_begin * c_out, (uint32_t)((int64_t)rows * c_out * 2));
+    // item e of the wave's operand: rows 8*(e / cpt) .. +7 of the stage,
+    // channels 8*(e % cpt) .. +7 of the tile. Stages at or past `steps`, and
+    // threads without an item, load zeros (out-of-range buffer offsets).
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const bool role_a = wv < WA;
+    const int e = role_a ? tid : tid - WA * 64;
+    const int n_items = role_a ? A_ITEMS : (wv < WA + WB ? B_ITEMS : 0);
+    const bool has_item = e < n_items;
+    const int cpt = role_a ? CPT_A : CPT_B;
+    const int rgp = has_item ? e / cpt : 0, cl = has_item ? (e % cpt) * 8 : 0;
+    const int chan = (role_a ? ci0 : co0) + cl;
+    const bool chan_ok = has_item && chan < (role_a ? c_in : c_out);
+    const rsrc_t rs = make_rsrc(role_a ? (const void*)x : (const void*)(go + r_begin * c_out),
+                                role_a ? (uint32_t)(n * c_in * 2) : (uint32_t)((int64_t)rows * c_out * 2));
+    const uint32_t chan_b = (uint32_t)chan * 2u, row_b = (uint32_t)c_out * 2u;
 
-    // item e < A_ITEMS: rows 8*(e % RG) .. +7, channels 8*(e / RG) of x;
-    // else the same for go with BN. Stages at or past `steps` load zeros.
-    u32x4 r0s[PER][8], r1s[PER][8];
-    auto load = [&](int t, u32x4 (*rg)[8]) {
+    u32x4 r0s[8], r1s[8];
+    auto load = [&](int t, u32x4* rg) {
         const bool live = t < steps;
         const int rbase = live ? t * KR : 0;
+        const bool ok = live && chan_ok;
+        const u32x4 s0 = *(const u32x4*)&srow[rbase + rgp * 8];
+        const u32x4 s1 = *(const u32x4*)&srow[rbase + rgp * 8 + 4];
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int e = tid + q * NT;
-            if (e < A_ITEMS) {
-                const int rgp = e % RG, c = ci0 + (e / RG) * 8;
-                const bool ok = live && c < c_in;
-                const u32x4 s0 = *(const u32x4*)&srow[rbase + rgp * 8];
-                const u32x4 s1 = *(const u32x4*)&srow[rbase + rgp * 8 + 4];
-#pragma unroll
-                for (int r = 0; r < 8; ++r) {
-                    const uint32_t so = r < 4 ? s0[r] : s1[r - 4];
-                    rg[q][r] = bload16(rs_x, ok && so != kOOB ? so + (uint32_t)c * 2u : kOOB);
-                }
-            } else {
-                const int eb = e - A_ITEMS;
-                const int rgp = eb % RG, c = co0 + (eb / RG) * 8;
-                const bool ok = live && e < ITEMS && c < c_out;
-#pragma unroll
-                for (int r = 0; r < 8; ++r)
-                    rg[q][r] = bload16(rs_g, ok ? (uint32_t)((rbase + rgp * 8 + r) * c_out + c) * 2u : kOOB);
-            }
+        for (int r = 0; r < 8; ++r) {
+            const uint32_t so = r < 4 ? s0[r] : s1[r - 4];
+            const uint32_t off = role_a ? (so != kOOB ? so + chan_b : kOOB)
+                                        : (uint32_t)(rbase + rgp * 8 + r) * row_b + chan_b;
+            rg[r] = bload16(rs, ok ? off : kOOB);
         }
     };
-    auto store = [&](int buf, u32x4 (*rg)[8]) {
+    auto store = [&](int buf, const u32x4* rg) {
+        u32x4 o[8];
+        transpose8(rg, o);
+        if (has_item) {
+            u16(*dst)[KR] = role_a ? As[buf] : Bs[buf];
 #pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            const int e = tid + q * NT;
-            if (e >= ITEMS) continue;
-            u32x4 o[8];
-            transpose8(rg[q], o);
-            if (e < A_ITEMS) {
-                const int rgp = e % RG, cl = (e / RG) * 8;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) *(u32x4*)&As[buf][cl + c][rgp * 8] = o[c];
-            } else {
-                const int eb = e - A_ITEMS;
-                const int rgp = eb % RG, cl = (eb / RG) * 8;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) *(u32x4*)&Bs[buf][cl + c][rgp * 8] = o[c];
-            }
+            for (int c = 0; c < 8; ++c) *(u32x4*)&dst[cl + c][bw_swz(cl + c, rgp)] = o[c];
         }
     };
 
@@ -884,13 +904,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
 
     const int wm = wave / WGN, wn = wave % WGN;
     const int arow = wm * FM * 16 + (lane & 15), brow = wn * FN * 16 + (lane & 15);
-    const int kof = (lane >> 4) * 8;
+    // fragment chunk of k-step h is h*4 + lane/16 (bw_swz gives its position)
+    const int kq = lane >> 4;
     float bsum = 0.f;
     auto compute = [&](int buf) {
         if (do_bias && tid < BN) {  // column sums of the staged go rows
 #pragma unroll
-            for (int r = 0; r < KR; r += 8) {
-                const u32x4 v = *(const u32x4*)&Bs[buf][tid][r];
+            for (int r = 0; r < KR / 8; ++r) {
+                const u32x4 v = *(const u32x4*)&Bs[buf][tid][bw_swz(tid, r)];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     bsum += (float)__builtin_bit_cast(T, (u16)(v[q] & 0xffffu));
@@ -902,10 +923,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
         for (int h = 0; h < KR / KS; ++h) {
             u32x4 fb[FN];
 #pragma unroll
-            for (int b = 0; b < FN; ++b) fb[b] = *(const u32x4*)&Bs[buf][brow + b * 16][h * KS + kof];
+            for (int b = 0; b < FN; ++b) fb[b] = *(const u32x4*)&Bs[buf][brow + b * 16][bw_swz(brow + b * 16, h * 4 + kq)];
 #pragma unroll
             for (int a = 0; a < FM; ++a) {
-                const u32x4 fa = *(const u32x4*)&As[buf][arow + a * 16][h * KS + kof];
+                const u32x4 fa = *(const u32x4*)&As[buf][arow + a * 16][bw_swz(arow + a * 16, h * 4 + kq)];
 #pragma unroll
                 for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fa, fb[b], acc[a][b]);
             }
@@ -1004,8 +1025,11 @@ template <typename T, int MODE, int CR, int FM, int FN, int D>
 static void launch_wide(const void* src, const int32_t* nbr, const void* wb, const void* bias,
                         int bias_mode, void* out, int64_t n, int n_out, int64_t tpb, hipStream_t s) {
     constexpr int BN = 4 * FN * 16;
-    // two wave sets when both sets' double-buffered A slices fit in LDS
-    constexpr int WS = (size_t)2 * 2 * FM * 16 * (CR + 8) * 2 <= 150 * 1024 ? 2 : 1;
+    // two wave sets when both sets' double-buffered A slices (with the pad
+    // rows k_gg_wide adds) fit in LDS
+    constexpr int CPR = CR / 8, A_CHUNKS = FM * 16 * CPR, A_PER = (A_CHUNKS + 255) / 256;
+    constexpr int APAD = (A_PER * 256 - A_CHUNKS + CPR - 1) / CPR;
+    constexpr int WS = (size_t)2 * 2 * (FM * 16 + APAD) * CR * 2 <= 150 * 1024 ? 2 : 1;
     const int n_col = (int)cdiv(n_out, BN);
     const int64_t tiles = cdiv(n, 16 * FM) * n_col;
     hipLaunchKernelGGL((k_gg_wide<T, MODE, CR, FM, FN, D, WS>), dim3((unsigned)tiles), dim3(256 * WS),
