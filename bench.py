@@ -141,11 +141,13 @@ class Problem:
     def bwd_w_partials(self):  # the partial-sum kernel of bwd_w alone
         return self.ops.bwd_w_partials(self.go, self.x, self.table, C, 0, True)
 
+    def bwd(self):  # the autograd backward: bwd_in + bwd_w in one call
+        return self.ops.bwd_packed(self.go, self.x, self.table, self.w, self.pb, C, 0, True)
+
     def step(self):
         pf, pb = self.ops.pack_weight(self.w, True, True)
         y = self.ops.fwd_packed(self.x, self.table, self.w, pf, self.b, 0, 1)
-        gi = self.ops.bwd_in_packed(self.go, self.table, self.w, pb, self.n, C, 0)
-        gw, gb = self.ops.bwd_w_bias(self.go, self.x, self.table, C, 0, True)
+        gi, gw, gb = self.ops.bwd_packed(self.go, self.x, self.table, self.w, pb, C, 0, True)
         return y, gi, gw, gb
 
 
@@ -318,10 +320,11 @@ def main():
 
     # per-pass timing. fwd is one kernel (gathered GEMM); bwd_in adds the
     # orphan pass; bwd_w is the partial-sum kernel (timed alone through
-    # bwd_w_partials) plus the split reduction. The roofline names the longer
-    # of the two single-kernel timings.
+    # bwd_w_partials) plus the split reduction; bwd is the step's backward
+    # (bwd_in + bwd_w in one call, the orphan pass inside the reduction). The
+    # roofline names the longer of the two single-kernel timings.
     phases = {p: time_events(getattr(prob, p), max(args.steps, 20))
-              for p in ("pack", "fwd", "bwd_in", "bwd_w", "bwd_w_partials")}
+              for p in ("pack", "fwd", "bwd_in", "bwd_w", "bwd_w_partials", "bwd")}
     dom = max(("fwd", "bwd_w_partials"), key=phases.get)
     f_pass = 2 * 9 * n * C * C
     t_dom = phases[dom] * 1e-3

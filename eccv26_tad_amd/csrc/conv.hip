@@ -91,9 +91,15 @@ extern "C" size_t svtad_fwd_workspace_bytes(int c_in, int c_out, int dtype) {
     return gg_mfma_workspace(dtype, c_in, c_out);
 }
 
+// The packed backward-input weight is followed by the orphan flag word.
+static size_t bwd_in_ws(int dtype, int c_in, int c_out) {
+    const size_t w = gg_mfma_workspace(dtype, c_out, c_in);
+    return w ? w + kOrphanFlagBytes : 0;
+}
+
 extern "C" size_t svtad_bwd_in_workspace_bytes(int c_in, int c_out, int dtype) {
     if (!dtype_ok(dtype) || c_in <= 0 || c_out <= 0) return 0;
-    return gg_mfma_workspace(dtype, c_out, c_in);
+    return bwd_in_ws(dtype, c_in, c_out);
 }
 
 extern "C" int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, const void* bias,
@@ -116,7 +122,7 @@ extern "C" int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, 
     if (gg_mfma_supported(dtype, c_in, c_out) && al16(x) && al16(weight) && al16(out) &&
         (!need || al16(workspace)))
         gg_mfma(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
-                tokens_per_batch, need ? workspace : nullptr, false, s);
+                tokens_per_batch, need ? workspace : nullptr, false, nullptr, s);
     else
         gg_valu(dtype, MODE_FWD, x, nbr, weight, bias, bias_mode, out, n, c_in, c_out,
                 tokens_per_batch, s);
@@ -128,7 +134,7 @@ extern "C" int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void
                             int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
     int st = check_common("bwd_in", n, c_in, c_out, tokens_per_batch, dtype);
     if (st) return st;
-    const size_t need = gg_mfma_workspace(dtype, c_out, c_in);
+    const size_t need = bwd_in_ws(dtype, c_in, c_out);
     if (need && (!workspace || workspace_bytes < need))
         return set_error(SVTAD_ERR_WORKSPACE, "bwd_in: workspace smaller than svtad_bwd_in_workspace_bytes()");
     if (n == 0) return SVTAD_OK;
@@ -136,14 +142,17 @@ extern "C" int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void
         return set_error(SVTAD_ERR_INVALID, "bwd_in: null pointer");
     hipStream_t s = (hipStream_t)stream;
     // gi[j, ci] = sum_k sum_co go[src_t(j,k), co] * w[k][ci][co]
+    uint32_t* flag = need ? (uint32_t*)((char*)workspace + need - kOrphanFlagBytes) : nullptr;
+    bool flagged = false;
     if (gg_mfma_supported(dtype, c_out, c_in) && al16(grad_out) && al16(weight) && al16(grad_in) &&
         (!need || al16(workspace)))
-        gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
-                tokens_per_batch, need ? workspace : nullptr, false, s);
+        flagged = gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
+                          tokens_per_batch, need ? workspace : nullptr, false, flag, s);
     else
         gg_valu(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, 0, grad_in, n, c_out, c_in,
                 tokens_per_batch, s);
-    orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, s);
+    orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch,
+            flagged ? flag : nullptr, s);
     return launch_status();
 }
 
@@ -174,12 +183,12 @@ extern "C" int svtad_fwd_packed(const void* x, const int32_t* nbr, const void* p
     if (!al16(x) || !al16(packed_fwd) || !al16(out))
         return set_error(SVTAD_ERR_INVALID, "fwd_packed: x, packed weight and out must be 16-byte aligned");
     gg_mfma(dtype, MODE_FWD, x, nbr, packed_fwd, bias, bias_mode, out, n, c_in, c_out,
-            tokens_per_batch, nullptr, true, (hipStream_t)stream);
+            tokens_per_batch, nullptr, true, nullptr, (hipStream_t)stream);
     return launch_status();
 }
 
 extern "C" int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* weight,
-                                   const void* packed_bwd, void* grad_in, int64_t n, int c_in,
+                                   void* packed_bwd, void* grad_in, int64_t n, int c_in,
                                    int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
     int st = check_common("bwd_in_packed", n, c_in, c_out, tokens_per_batch, dtype);
     if (st) return st;
@@ -191,9 +200,12 @@ extern "C" int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, con
     if (!al16(grad_out) || !al16(packed_bwd) || !al16(grad_in))
         return set_error(SVTAD_ERR_INVALID, "bwd_in_packed: grad_out, packed weight and grad_in must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
-    gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in, n, c_out, c_in,
-            tokens_per_batch, nullptr, true, s);
-    orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, s);
+    // the orphan flag follows the packed layout (cleared by svtad_pack_weight)
+    uint32_t* flag = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
+    const bool flagged = gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in,
+                                 n, c_out, c_in, tokens_per_batch, nullptr, true, flag, s);
+    orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch,
+            flagged ? flag : nullptr, s);
     return launch_status();
 }
 
@@ -217,10 +229,51 @@ extern "C" int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* n
     hipStream_t s = (hipStream_t)stream;
     if (p.path == 1)
         bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
-                tokens_per_batch, s);
+                tokens_per_batch, nullptr, s);
     else
         bw_valu(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
                 tokens_per_batch, s);
+    return launch_status();
+}
+
+extern "C" int svtad_bwd_packed(const void* grad_out, const void* x, const int32_t* nbr,
+                                const void* weight, void* packed_bwd, void* grad_in, void* grad_w,
+                                void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n,
+                                int c_in, int c_out, int64_t tokens_per_batch, int dtype,
+                                void* stream) {
+    int st = check_common("bwd_packed", n, c_in, c_out, tokens_per_batch, dtype);
+    if (st) return st;
+    if (!gg_mfma_packed_ok(dtype, n, c_out, c_in))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_packed: shape/dtype has no packed layout");
+    BwPlan p = plan_bw(n, c_in, c_out, dtype);
+    if (!workspace || !grad_w || !weight || !packed_bwd ||
+        (n > 0 && (!grad_out || !x || !nbr || !grad_in)))
+        return set_error(SVTAD_ERR_INVALID, "bwd_packed: null pointer");
+    if (n > 0 && !(al16(grad_out) && al16(packed_bwd) && al16(grad_in)))
+        return set_error(SVTAD_ERR_INVALID, "bwd_packed: grad_out, packed weight and grad_in must be 16-byte aligned");
+    if (p.path == 1 && !(al16(grad_out) && al16(x))) p.path = 0;
+    if (workspace_bytes < p.ws_bytes)
+        return set_error(SVTAD_ERR_WORKSPACE, "bwd_packed: workspace smaller than svtad_bwd_w_workspace_bytes()");
+    hipStream_t s = (hipStream_t)stream;
+    // 1. grad_in (keeps the orphan flag after the packed layout)
+    const uint32_t* flag = nullptr;
+    if (n > 0) {
+        uint32_t* f = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
+        if (gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in, n, c_out,
+                    c_in, tokens_per_batch, nullptr, true, f, s))
+            flag = f;
+    }
+    // 2. grad_w / grad_bias; the reduction also runs the orphan pass of step 1
+    const OrphanJob job{grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, flag};
+    bool taken = false;
+    if (p.path == 1)
+        taken = bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
+                        tokens_per_batch, n > 0 ? &job : nullptr, s);
+    else
+        bw_valu(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
+                tokens_per_batch, s);
+    if (n > 0 && !taken)
+        orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, flag, s);
     return launch_status();
 }
 
@@ -245,7 +298,7 @@ extern "C" int svtad_dw_bwd_in(const void* grad_out, const int32_t* nbr, const v
         return set_error(SVTAD_ERR_INVALID, "dw_bwd_in: null pointer");
     hipStream_t s = (hipStream_t)stream;
     dw_gather(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, grad_in, n, c, tokens_per_batch, s);
-    orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, s);
+    orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, nullptr, s);
     return launch_status();
 }
 

@@ -266,7 +266,7 @@ template <typename T, int MODE, int CR, int FM, int FN, int D, int WS>
 __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const T* __restrict__ src, const int32_t* __restrict__ nbr, const T* __restrict__ wb,
     const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n, int n_out,
-    int64_t tpb, int n_col_tiles, int64_t n_tiles) {
+    int64_t tpb, int n_col_tiles, int64_t n_tiles, uint32_t* __restrict__ orphan_flag) {
     // WS wave sets of 4 waves share the tile; set h takes the offsets
     // klist[h], klist[h + WS], ... so WS independent load streams are in
     // flight per workgroup. The sets' accumulators are summed through LDS.
@@ -308,7 +308,20 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
         const int k = e / BM, m = e - k * BM;
         const int64_t i = row0 + m;
         int64_t r = -1;
-        if (i < n) r = MODE == MODE_FWD ? src_row(nbr, i, k, n, tpb) : src_row_t(nbr, i, k, n, tpb);
+        if (i < n) {
+            if (MODE == MODE_FWD) {
+                r = src_row(nbr, i, k, n, tpb);
+            } else {
+                // transposed source (see src_row_t); an entry (i, 8-k) -> p
+                // whose partner (p, k) -> i is absent is left to the orphan
+                // pass, which the flag arms
+                const int64_t p = src_row(nbr, i, 8 - k, n, tpb);
+                if (p >= 0) {
+                    if (src_row(nbr, p, k, n, tpb) == i) r = p;
+                    else if (orphan_flag) *orphan_flag = 1u;
+                }
+            }
+        }
         soff[k][m] = r >= 0 ? (uint32_t)r * (uint32_t)(CR * 2) : kOOB;
         if (r >= 0) kvalid[k] = 1;
     }
@@ -491,9 +504,10 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
 // 16-byte fragment slot; grid cdiv(9*NCS*NB*64, 256).
 template <int MODE>
 __global__ __launch_bounds__(256) void k_pack_frag(const u16* __restrict__ w, u16* __restrict__ wf,
-                                                   int c_red, int n_out) {
+                                                   int c_red, int n_out, uint32_t* __restrict__ flag) {
     const int ncs = c_red / KS, nb = (n_out + 15) / 16;
     const int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (flag && slot == 0) *flag = 0u;  // orphan flag after a backward-input layout
     if (slot >= (int64_t)9 * ncs * nb * 64) return;
     const int lane = (int)(slot & 63);
     int64_t q = slot >> 6;
@@ -524,6 +538,7 @@ __global__ __launch_bounds__(256) void k_pack_both(const u16* __restrict__ w, u1
                                                    u16* __restrict__ wf_bwd, int c_in, int c_out,
                                                    int64_t sf, int64_t sb) {
     int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (wf_bwd && slot == 0) *(uint32_t*)(wf_bwd + sb * 8) = 0u;  // orphan flag after the layout
     const bool fwd = slot < sf;
     if (!fwd) slot -= sf;
     if (slot >= (fwd ? sf : sb)) return;
@@ -958,14 +973,22 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
     if (do_bias && tid < BN && co0 + tid < c_out) ws_bias[(int64_t)s * c_out + co0 + tid] = bsum;
 }
 
+// The reduction of the partials; with a job (oj.gi != NULL) its workgroups
+// also run the orphan pass of a backward-input computed before it (flag-gated
+// as in k_orphans), which saves that pass a launch of its own.
 template <typename T>
 __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ part,
                                                    const float* __restrict__ part_b, int splits,
                                                    int c_in, int c_out, int fm, int fn, int wgm,
                                                    int wgn, int n_ci_tiles, int n_co_tiles,
-                                                   T* __restrict__ gw, T* __restrict__ gb) {
+                                                   T* __restrict__ gw, T* __restrict__ gb,
+                                                   OrphanJob oj) {
     bw_reduce_one<T>((int64_t)blockIdx.x * 256 + threadIdx.x, part, part_b, splits, c_in, c_out, fm,
                      fn, wgm, wgn, n_ci_tiles, n_co_tiles, gw, gb);
+    if (!oj.gi || (oj.flag && *oj.flag == 0u)) return;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < oj.n * 9; e += (int64_t)gridDim.x * 256)
+        orphan_entry<T, false>(e, (const T*)oj.go, oj.nbr, (const T*)oj.w, (T*)oj.gi, oj.n, oj.c_in,
+                               oj.c_out, oj.tpb);
 }
 
 // ---------------------------------------------------------------------------
@@ -1023,7 +1046,8 @@ static int cu_count() {
 
 template <typename T, int MODE, int CR, int FM, int FN, int D>
 static void launch_wide(const void* src, const int32_t* nbr, const void* wb, const void* bias,
-                        int bias_mode, void* out, int64_t n, int n_out, int64_t tpb, hipStream_t s) {
+                        int bias_mode, void* out, int64_t n, int n_out, int64_t tpb, uint32_t* flag,
+                        hipStream_t s) {
     constexpr int BN = 4 * FN * 16;
     // two wave sets when both sets' double-buffered A slices (with the pad
     // rows k_gg_wide adds) fit in LDS
@@ -1034,7 +1058,7 @@ static void launch_wide(const void* src, const int32_t* nbr, const void* wb, con
     const int64_t tiles = cdiv(n, 16 * FM) * n_col;
     hipLaunchKernelGGL((k_gg_wide<T, MODE, CR, FM, FN, D, WS>), dim3((unsigned)tiles), dim3(256 * WS),
                        0, s, (const T*)src, nbr, (const T*)wb, bias, bias_mode, (T*)out, n, n_out,
-                       tpb, n_col, tiles);
+                       tpb, n_col, tiles, flag);
 }
 
 // Row fragments per workgroup: the smallest instantiated count that keeps the
@@ -1050,46 +1074,48 @@ static int pick_fm(int64_t n, int n_col, const int* have, int count) {
 template <typename T, int MODE, int CR, int FN, int D>
 static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, const void* bias,
                            int bias_mode, void* out, int64_t n, int n_out, int64_t tpb,
-                           hipStream_t s) {
+                           uint32_t* flag, hipStream_t s) {
     const int n_col = (int)cdiv(n_out, 4 * FN * 16);
     if constexpr (CR == 192 || CR == 256) {
         static const int have[] = {1, 2, 3, 4, 5, 6, 8};
         switch (pick_fm(n, n_col, have, 7)) {
-            case 1: launch_wide<T, MODE, CR, 1, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
-            case 2: launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
-            case 3: launch_wide<T, MODE, CR, 3, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
-            case 4: launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
-            case 5: launch_wide<T, MODE, CR, 5, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
-            case 6: launch_wide<T, MODE, CR, 6, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
-            default: launch_wide<T, MODE, CR, 8, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); return;
+            case 1: launch_wide<T, MODE, CR, 1, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
+            case 2: launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
+            case 3: launch_wide<T, MODE, CR, 3, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
+            case 4: launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
+            case 5: launch_wide<T, MODE, CR, 5, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
+            case 6: launch_wide<T, MODE, CR, 6, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
+            default: launch_wide<T, MODE, CR, 8, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
         }
     } else {
         static const int have[] = {2, 4};
         if (pick_fm(n, n_col, have, 2) == 2)
-            launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s);
+            launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
         else
-            launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s);
+            launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
     }
 }
 
+// Returns whether the orphan flag is maintained (the wide kernel ran with it).
 template <typename T, int MODE>
-static void gg_dispatch(const void* src, const int32_t* nbr, const void* w, const void* bias,
+static bool gg_dispatch(const void* src, const int32_t* nbr, const void* w, const void* bias,
                         int bias_mode, void* out, int64_t n, int c_red, int n_out, int64_t tpb,
-                        void* ws, bool prepacked, hipStream_t s) {
+                        void* ws, bool prepacked, uint32_t* flag, hipStream_t s) {
     const WideCfg* wc = wide_cfg(c_red, n_out);
     // buffer loads address operands with 32-bit byte offsets
     const bool fits = n * c_red * 2 < (int64_t)INT32_MAX && 9LL * c_red * n_out * 2 < (int64_t)INT32_MAX;
+    if (MODE == MODE_FWD) flag = nullptr;
     if (wc && fits && (ws || prepacked)) {
         const void* wb = prepacked ? w : ws;
         if (!prepacked) {
             const int64_t slots = (int64_t)9 * (c_red / KS) * cdiv(n_out, 16) * 64;
             hipLaunchKernelGGL((k_pack_frag<MODE>), dim3((unsigned)cdiv(slots, 256)), dim3(256), 0, s,
-                               (const u16*)w, (u16*)ws, c_red, n_out);
+                               (const u16*)w, (u16*)ws, c_red, n_out, flag);
         }
 #define SVTAD_WIDE_CASE(CR, FM, FN, D)                                                           \
     if (wc->cr == CR) {                                                                          \
-        launch_wide_fm<T, MODE, CR, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, s); \
-        return;                                                                                  \
+        launch_wide_fm<T, MODE, CR, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); \
+        return flag != nullptr;                                                                  \
     }
         SVTAD_WIDE_CASE(64, 8, 1, 2)
         SVTAD_WIDE_CASE(128, 8, 2, 4)
@@ -1106,18 +1132,18 @@ static void gg_dispatch(const void* src, const int32_t* nbr, const void* w, cons
         launch_gg<T, MODE, 4, 1, 1, 3>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s);
     else
         launch_gg<T, MODE, 4, 1, 1, 1>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, s);
+    return false;
 }
 
-void gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+bool gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
-             int64_t tpb, void* ws, bool prepacked, hipStream_t s) {
+             int64_t tpb, void* ws, bool prepacked, uint32_t* orphan_flag, hipStream_t s) {
     if (dtype == SVTAD_F16) {
-        if (mode == MODE_FWD) gg_dispatch<f16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, s);
-        else gg_dispatch<f16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, s);
-    } else {
-        if (mode == MODE_FWD) gg_dispatch<bf16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, s);
-        else gg_dispatch<bf16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, s);
+        if (mode == MODE_FWD) return gg_dispatch<f16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, nullptr, s);
+        return gg_dispatch<f16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, orphan_flag, s);
     }
+    if (mode == MODE_FWD) return gg_dispatch<bf16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, nullptr, s);
+    return gg_dispatch<bf16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, orphan_flag, s);
 }
 
 bool gg_mfma_packed_ok(int dtype, int64_t n, int c_red, int n_out) {
@@ -1230,31 +1256,33 @@ static void bw_dispatch(const BwPlan& p, const void* go, const void* x, const in
 #undef SVTAD_BW_CASE
 }
 
-void bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
              void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
-             hipStream_t s) {
+             const OrphanJob* oj, hipStream_t s) {
     float* part = (float*)ws;
     float* part_b = gb ? part + (int64_t)p.splits * 9 * c_in * c_out : nullptr;
     if (dtype == SVTAD_F16) bw_dispatch<f16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
     else bw_dispatch<bf16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
-    if (!gw) return;  // partials only
+    if (!gw) return false;  // partials only
     BigCfg bc;
     if (big_cfg(c_in, c_out, &bc)) {
         const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
         const int64_t threads = (int64_t)9 * c_in * c_out / 4 + (gb ? c_out : 0);
         const dim3 grid((unsigned)cdiv(threads, 256));
+        const OrphanJob job = oj ? *oj : OrphanJob{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
         if (dtype == SVTAD_F16)
             hipLaunchKernelGGL((k_bw_reduce<f16>), grid, dim3(256), 0, s, (const float*)part,
                                (const float*)part_b, p.splits, c_in, c_out, bc.fm, bc.fn, bc.wgm,
-                               bc.wgn, nci, nco, (f16*)gw, (f16*)gb);
+                               bc.wgn, nci, nco, (f16*)gw, (f16*)gb, job);
         else
             hipLaunchKernelGGL((k_bw_reduce<bf16>), grid, dim3(256), 0, s, (const float*)part,
                                (const float*)part_b, p.splits, c_in, c_out, bc.fm, bc.fn, bc.wgm,
-                               bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb);
-        return;
+                               bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb, job);
+        return oj != nullptr;
     }
     split_reduce(dtype, part, 9LL * c_in * c_out, p.splits, gw, s);
     if (gb) split_reduce(dtype, part_b, (int64_t)c_out, p.splits, gb, s);
+    return false;
 }
 
 }  // namespace svtad

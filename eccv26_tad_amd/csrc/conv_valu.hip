@@ -119,54 +119,15 @@ __global__ __launch_bounds__(256) void k_gg_valu(const T* __restrict__ src,
 // (after the gather kernel has stored gi) with atomics. Tables built from a
 // keep mask have none, so the pass only reads the table.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void atomic_add_out(float* p, float v) { atomicAdd(p, v); }
-__device__ __forceinline__ void atomic_add_out(double* p, double v) { atomicAdd(p, v); }
-
-template <typename H>
-__device__ __forceinline__ void atomic_add_half(H* p, float v) {
-    // CAS on the aligned 32-bit word that holds the 16-bit value.
-    uintptr_t addr = (uintptr_t)p;
-    unsigned int* word = (unsigned int*)(addr & ~(uintptr_t)3);
-    const int shift = (addr & 2) ? 16 : 0;
-    unsigned int old = *word, assumed;
-    do {
-        assumed = old;
-        unsigned short bits = (unsigned short)((assumed >> shift) & 0xffffu);
-        H h = __builtin_bit_cast(H, bits);
-        H nh = (H)((float)h + v);
-        unsigned int nb = (unsigned int)__builtin_bit_cast(unsigned short, nh);
-        unsigned int nw = (assumed & ~(0xffffu << shift)) | (nb << shift);
-        old = atomicCAS(word, assumed, nw);
-    } while (old != assumed);
-}
-__device__ __forceinline__ void atomic_add_out(f16* p, float v) { atomic_add_half(p, v); }
-__device__ __forceinline__ void atomic_add_out(bf16* p, float v) { atomic_add_half(p, v); }
-
 template <typename T, bool DEPTHWISE>
 __global__ __launch_bounds__(256) void k_orphans(const T* __restrict__ go,
                                                  const int32_t* __restrict__ nbr,
                                                  const T* __restrict__ w, T* __restrict__ gi,
-                                                 int64_t n, int c_in, int c_out, int64_t tpb) {
-    typedef typename Acc<T>::type A;
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (e >= n * 9) return;
-    const int64_t i = e / 9;
-    const int k = (int)(e - i * 9);
-    const int64_t j = src_row(nbr, i, k, n, tpb);
-    if (j < 0 || src_row(nbr, j, 8 - k, n, tpb) == i) return;
-    if (DEPTHWISE) {
-        for (int c = 0; c < c_in; ++c)
-            atomic_add_out(gi + j * c_in + c,
-                           to_acc<A>(go[i * c_in + c]) * to_acc<A>(w[(int64_t)k * c_in + c]));
-    } else {
-        const T* wk = w + (int64_t)k * c_in * c_out;
-        for (int ci = 0; ci < c_in; ++ci) {
-            A s = 0;
-            for (int co = 0; co < c_out; ++co)
-                s += to_acc<A>(go[i * c_out + co]) * to_acc<A>(wk[(int64_t)ci * c_out + co]);
-            atomic_add_out(gi + j * c_in + ci, s);
-        }
-    }
+                                                 int64_t n, int c_in, int c_out, int64_t tpb,
+                                                 const uint32_t* __restrict__ flag) {
+    if (flag && *flag == 0u) return;  // no entry without a symmetric partner
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n * 9; e += (int64_t)gridDim.x * 256)
+        orphan_entry<T, DEPTHWISE>(e, go, nbr, w, gi, n, c_in, c_out, tpb);
 }
 
 // ---------------------------------------------------------------------------
@@ -386,23 +347,26 @@ void gg_valu(int dtype, int mode, const void* src, const int32_t* nbr, const voi
 
 template <typename T>
 static void launch_orphans(bool dw, const void* go, const int32_t* nbr, const void* w, void* gi,
-                           int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
-    dim3 grid((unsigned)cdiv(n * 9, 256));
+                           int64_t n, int c_in, int c_out, int64_t tpb, const uint32_t* flag,
+                           hipStream_t s) {
+    // with a flag the pass is almost always a no-op: a small grid-stride grid
+    const int64_t blocks = cdiv(n * 9, 256);
+    dim3 grid((unsigned)(flag ? std::min<int64_t>(blocks, 256) : blocks));
     if (dw)
         hipLaunchKernelGGL((k_orphans<T, true>), grid, dim3(256), 0, s, (const T*)go, nbr,
-                           (const T*)w, (T*)gi, n, c_in, c_out, tpb);
+                           (const T*)w, (T*)gi, n, c_in, c_out, tpb, flag);
     else
         hipLaunchKernelGGL((k_orphans<T, false>), grid, dim3(256), 0, s, (const T*)go, nbr,
-                           (const T*)w, (T*)gi, n, c_in, c_out, tpb);
+                           (const T*)w, (T*)gi, n, c_in, c_out, tpb, flag);
 }
 
 void orphans(int dtype, bool dw, const void* go, const int32_t* nbr, const void* w, void* gi,
-             int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
+             int64_t n, int c_in, int c_out, int64_t tpb, const uint32_t* flag, hipStream_t s) {
     switch (dtype) {
-        case SVTAD_F32: launch_orphans<float>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
-        case SVTAD_F16: launch_orphans<f16>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
-        case SVTAD_BF16: launch_orphans<bf16>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
-        case SVTAD_F64: launch_orphans<double>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, s); break;
+        case SVTAD_F32: launch_orphans<float>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, flag, s); break;
+        case SVTAD_F16: launch_orphans<f16>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, flag, s); break;
+        case SVTAD_BF16: launch_orphans<bf16>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, flag, s); break;
+        case SVTAD_F64: launch_orphans<double>(dw, go, nbr, w, gi, n, c_in, c_out, tpb, flag, s); break;
     }
 }
 

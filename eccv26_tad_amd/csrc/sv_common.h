@@ -44,4 +44,55 @@ __device__ __forceinline__ int64_t src_row_t(const int32_t* __restrict__ nbr, in
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+__device__ __forceinline__ void atomic_add_out(float* p, float v) { atomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add_out(double* p, double v) { atomicAdd(p, v); }
+
+template <typename H>
+__device__ __forceinline__ void atomic_add_half(H* p, float v) {
+    // CAS on the aligned 32-bit word that holds the 16-bit value.
+    uintptr_t addr = (uintptr_t)p;
+    unsigned int* word = (unsigned int*)(addr & ~(uintptr_t)3);
+    const int shift = (addr & 2) ? 16 : 0;
+    unsigned int old = *word, assumed;
+    do {
+        assumed = old;
+        unsigned short bits = (unsigned short)((assumed >> shift) & 0xffffu);
+        H h = __builtin_bit_cast(H, bits);
+        H nh = (H)((float)h + v);
+        unsigned int nb = (unsigned int)__builtin_bit_cast(unsigned short, nh);
+        unsigned int nw = (assumed & ~(0xffffu << shift)) | (nb << shift);
+        old = atomicCAS(word, assumed, nw);
+    } while (old != assumed);
+}
+__device__ __forceinline__ void atomic_add_out(f16* p, float v) { atomic_add_half(p, v); }
+__device__ __forceinline__ void atomic_add_out(bf16* p, float v) { atomic_add_half(p, v); }
+
+// Backward-input contribution of table entry e = i*9 + k when (i, k) -> j has
+// no symmetric partner (j, 8-k) -> i, which the transposed gathers cannot see:
+// gi[j] += go[i] . W[k]^T (depthwise: go[i] * w[k]), added with atomics.
+template <typename T, bool DEPTHWISE>
+__device__ __forceinline__ void orphan_entry(int64_t e, const T* __restrict__ go,
+                                             const int32_t* __restrict__ nbr,
+                                             const T* __restrict__ w, T* __restrict__ gi, int64_t n,
+                                             int c_in, int c_out, int64_t tpb) {
+    typedef typename Acc<T>::type A;
+    const int64_t i = e / 9;
+    const int k = (int)(e - i * 9);
+    const int64_t j = src_row(nbr, i, k, n, tpb);
+    if (j < 0 || src_row(nbr, j, 8 - k, n, tpb) == i) return;
+    if (DEPTHWISE) {
+        for (int c = 0; c < c_in; ++c)
+            atomic_add_out(gi + j * c_in + c,
+                           to_acc<A>(go[i * c_in + c]) * to_acc<A>(w[(int64_t)k * c_in + c]));
+    } else {
+        const T* wk = w + (int64_t)k * c_in * c_out;
+        for (int ci = 0; ci < c_in; ++ci) {
+            A s = 0;
+            for (int co = 0; co < c_out; ++co)
+                s += to_acc<A>(go[i * c_out + co]) * to_acc<A>(wk[(int64_t)ci * c_out + co]);
+            atomic_add_out(gi + j * c_in + ci, s);
+        }
+    }
+}
+
 }  // namespace svtad

@@ -25,8 +25,13 @@ struct BwPlan {
 void gg_valu(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
              int64_t tpb, hipStream_t s);
+// Backward-input contributions of table entries (i, k) -> j whose symmetric
+// partner (j, 8-k) -> i is absent (the gathered kernels cannot see them),
+// added with atomics. With a non-NULL flag the pass returns at once when the
+// flag is 0 (the wide backward-input kernel sets it when it meets such an
+// entry; the pack kernels clear it).
 void orphans(int dtype, bool dw, const void* go, const int32_t* nbr, const void* w, void* gi,
-             int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s);
+             int64_t n, int c_in, int c_out, int64_t tpb, const uint32_t* flag, hipStream_t s);
 void bw_valu(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
              void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
              hipStream_t s);
@@ -45,15 +50,22 @@ bool gg_mfma_supported(int dtype, int c_red, int n_out);
 // reduction width c_red and n_out columns needs; 0 when the shape takes a
 // kernel that reads w directly.
 size_t gg_mfma_workspace(int dtype, int c_red, int n_out);
+// The backward-input packed weight is followed by this many bytes holding the
+// 32-bit orphan flag (see orphans).
+constexpr size_t kOrphanFlagBytes = 256;
 // w is the raw weight (ws holds room for its packed form, packed here) or,
-// with prepacked, the fragment-ordered weight itself.
-void gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
+// with prepacked, the fragment-ordered weight itself. For the backward-input
+// mode, orphan_flag (may be NULL) is the flag word after the packed weight;
+// the return value says whether the kernel that ran maintains it (if not,
+// the orphan pass must run without the flag).
+bool gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
-             int64_t tpb, void* ws, bool prepacked, hipStream_t s);
+             int64_t tpb, void* ws, bool prepacked, uint32_t* orphan_flag, hipStream_t s);
 // Whether the fragment-ordered (prepacked) entry points handle this shape.
 bool gg_mfma_packed_ok(int dtype, int64_t n, int c_red, int n_out);
 // Fragment-ordered weights for the forward (wf_fwd) and backward-input
-// (wf_bwd) gathered GEMMs, one launch; either may be NULL.
+// (wf_bwd) gathered GEMMs, one launch; either may be NULL. Clears the orphan
+// flag after wf_bwd.
 void pack_weight(const void* w, void* wf_fwd, void* wf_bwd, int c_in, int c_out, hipStream_t s);
 bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out);
 // Rows per split of the MFMA backward-weight (its row list lives in LDS).
@@ -61,8 +73,23 @@ constexpr int kMaxSplitRows = 2048;
 int bw_mfma_tile(int c);
 // (ci, co) tile edges of the MFMA backward-weight kernel chosen for a shape.
 void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn);
-void bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+// Orphan pass handed to the backward-weight reduction (one launch less when
+// the backward-input and backward-weight run together): flag as for orphans
+// (NULL: always run).
+struct OrphanJob {
+    const void* go;
+    const int32_t* nbr;
+    const void* w;
+    void* gi;
+    int64_t n;
+    int c_in, c_out;
+    int64_t tpb;
+    const uint32_t* flag;
+};
+// Returns true when oj (may be NULL) was run by the reduction; false leaves
+// it to the caller (gw NULL or a shape without the large-tile reduction).
+bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
              void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
-             hipStream_t s);
+             const OrphanJob* oj, hipStream_t s);
 
 }  // namespace svtad

@@ -286,6 +286,53 @@ std::tuple<at::Tensor, at::Tensor> op_bwd_w_bias(const at::Tensor& go_in, const 
     return {gw, with_bias ? gb : at::empty({0}, x.options())};
 }
 
+// bwd_packed(grad_output, x, neighbor_indices, weight, packed_bwd, C_in,
+// tokens_per_batch, with_bias) -> (grad_input [n, C_in], grad_weight, grad_bias
+// or empty): the autograd backward in one call (what bwd_in_packed and
+// bwd_w_bias give, with one launch less); falls back to those two when
+// packed_bwd is empty or the shape has no packed path.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> op_bwd_packed(const at::Tensor& go_in, const at::Tensor& x_in,
+                                                             const at::Tensor& nbr_in, const at::Tensor& w_in,
+                                                             const at::Tensor& packed, int64_t c_in,
+                                                             int64_t tpb, bool with_bias) {
+    check_gpu(go_in, "grad_output");
+    check_gpu(x_in, "x");
+    at::Tensor go = rows_view(go_in);
+    at::Tensor x = rows_view(x_in);
+    TORCH_CHECK(x.size(-1) == c_in, "x has ", x.size(-1), " channels, C_in = ", c_in);
+    const int64_t n = n_rows(x), c_out = go.size(-1);
+    auto separate = [&]() {
+        at::Tensor gi = op_bwd_in_packed(go_in, nbr_in, w_in, packed, n, c_in, tpb);
+        auto gwb = op_bwd_w_bias(go_in, x_in, nbr_in, c_in, tpb, with_bias);
+        return std::make_tuple(gi, std::get<0>(gwb), std::get<1>(gwb));
+    };
+    if (packed.numel() == 0) return separate();
+    TORCH_CHECK(n_rows(go) == n, "grad_output has ", n_rows(go), " rows, x has ", n);
+    TORCH_CHECK(go.scalar_type() == x.scalar_type() && w_in.scalar_type() == x.scalar_type(),
+                "grad_output, x and weight dtypes differ");
+    TORCH_CHECK(w_in.dim() == 3 && w_in.size(0) == 9 && w_in.size(1) == c_in && w_in.size(2) == c_out,
+                "weight must be (9, ", c_in, ", ", c_out, ")");
+    const int dt = dtype_code(x);
+    TORCH_CHECK((size_t)packed.numel() == svtad_bwd_in_workspace_bytes((int)c_in, (int)c_out, dt),
+                "packed_bwd does not match the weight");
+    at::Tensor w = w_in.contiguous();
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    const size_t ws_bytes = svtad_bwd_w_workspace_bytes(n, (int)c_in, (int)c_out, dt);
+    TORCH_CHECK(ws_bytes > 0, "bwd_packed: ", svtad_last_error());
+    at::Tensor ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
+    at::Tensor gi = at::empty({n, c_in}, x.options());
+    at::Tensor gw = at::empty({9, c_in, c_out}, x.options());
+    at::Tensor gb = with_bias ? at::empty({c_out}, x.options()) : at::Tensor();
+    const int st = svtad_bwd_packed(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                                    packed.data_ptr(), gi.data_ptr(), gw.data_ptr(),
+                                    with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
+                                    (int)c_in, (int)c_out, tpb, dt, stream_of(x));
+    if (st == SVTAD_ERR_UNSUPPORTED) return separate();
+    check_status(st, "bwd_packed");
+    return {gi, gw, with_bias ? gb : at::empty({0}, x.options())};
+}
+
 // bwd_w_partials(grad_output, x, neighbor_indices, C_in, tokens_per_batch, with_bias)
 // -> workspace bytes holding the row-split partial sums only (no reduction).
 // For timing the partial-sum kernel of backward-weight on its own.
@@ -492,6 +539,9 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.def("bwd_in_packed", &op_bwd_in_packed, "bwd_in with a packed weight", py::arg("grad_output"),
           py::arg("neighbor_indices"), py::arg("weight"), py::arg("packed_bwd"), py::arg("n_kept"),
           py::arg("C_in"), py::arg("tokens_per_batch"));
+    m.def("bwd_packed", &op_bwd_packed, "bwd_in_packed + bwd_w_bias in one call",
+          py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
+          py::arg("packed_bwd"), py::arg("C_in"), py::arg("tokens_per_batch"), py::arg("with_bias"));
     m.def("bwd_w_partials", &op_bwd_w_partials, "Backward-weight partial sums only (timing)",
           py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("C_in"),
           py::arg("tokens_per_batch"), py::arg("with_bias"));

@@ -64,12 +64,20 @@ class SparseConv2dFunction(Function):
         tpb = ctx.tokens_per_batch
         go = grad_output.contiguous()
         grad_input = grad_weight = grad_bias = None
+        need_b = bias is not None and ctx.needs_input_grad[3]
+        if ctx.needs_input_grad[0] and ctx.needs_input_grad[2]:
+            # both gradients in one call (the same kernels as the two calls
+            # below, with one launch less)
+            gi, gw, gb = _ops.bwd_packed(go, x, neighbor_indices, weight, packed_bwd, C_in, tpb, need_b)
+            grad_input = gi.view(x.shape) if x.dim() == 3 else gi
+            grad_weight = gw
+            grad_bias = gb if need_b else None
+            return grad_input, None, grad_weight, grad_bias, None, None
         if ctx.needs_input_grad[0]:
             grad_input = _ops.bwd_in_packed(go, neighbor_indices, weight, packed_bwd,
                                             x.numel() // x.shape[-1], C_in, tpb)
             if x.dim() == 3:
                 grad_input = grad_input.view(x.shape)
-        need_b = bias is not None and ctx.needs_input_grad[3]
         if ctx.needs_input_grad[2] or need_b:
             gw, gb = _ops.bwd_w_bias(go, x, neighbor_indices, C_in, tpb, need_b)
             if ctx.needs_input_grad[2]:

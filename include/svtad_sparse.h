@@ -113,6 +113,14 @@ int svtad_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight, v
  * SVTAD_ERR_UNSUPPORTED for shapes without a packed layout (both workspace
  * sizes 0). svtad_bwd_in_packed also takes the raw weight for table entries
  * whose transpose is absent.
+ * The backward-input buffer (packed_bwd, and the svtad_bwd_in workspace) ends
+ * with a 32-bit flag that the kernels maintain: svtad_pack_weight clears it,
+ * the backward-input kernel sets it when the table holds an entry (i, k) -> j
+ * without its partner (j, 8-k) -> i, and only then does the pass for such
+ * entries do any work. packed_bwd is therefore written by
+ * svtad_bwd_in_packed; calls that share one packed_bwd on one stream stay
+ * correct (a set flag only costs the full pass), calls on different streams
+ * must not share it.
  */
 int svtad_pack_weight(const void* weight, void* packed_fwd, void* packed_bwd, int c_in, int c_out,
                       int dtype, void* stream);
@@ -120,8 +128,24 @@ int svtad_fwd_packed(const void* x, const int32_t* nbr, const void* packed_fwd, 
                      int bias_mode, void* out, int64_t n, int c_in, int c_out,
                      int64_t tokens_per_batch, int dtype, void* stream);
 int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* weight,
-                        const void* packed_bwd, void* grad_in, int64_t n, int c_in, int c_out,
+                        void* packed_bwd, void* grad_in, int64_t n, int c_in, int c_out,
                         int64_t tokens_per_batch, int dtype, void* stream);
+
+/*
+ * The whole backward in one call: grad_in as svtad_bwd_in_packed computes it
+ * and grad_w / grad_bias as svtad_bwd_w computes them (same kernels, same
+ * results), with the pass for table entries without a symmetric partner run
+ * inside the backward-weight reduction instead of a launch of its own.
+ * Replaces the bwd_in + bwd_w pair the reference's autograd backward calls
+ * (sparse_conv_layer.py:93-123, 2d_sparse_v3_bind.cpp:10-11). packed_bwd as for
+ * svtad_bwd_in_packed; workspace holds svtad_bwd_w_workspace_bytes(); grad_w
+ * must not be NULL (grad_bias may be). Returns SVTAD_ERR_UNSUPPORTED for shapes
+ * without a packed backward-input layout.
+ */
+int svtad_bwd_packed(const void* grad_out, const void* x, const int32_t* nbr, const void* weight,
+                     void* packed_bwd, void* grad_in, void* grad_w, void* grad_bias,
+                     void* workspace, size_t workspace_bytes, int64_t n, int c_in, int c_out,
+                     int64_t tokens_per_batch, int dtype, void* stream);
 
 /* Workspace bytes needed by svtad_bwd_w for this shape. */
 size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, int dtype);

@@ -89,7 +89,8 @@ def test_fwd_workspace(lib):
     # f16 / bf16 shapes of the matrix-core forward hold the packed weight
     lib.svtad_bwd_in_workspace_bytes.restype = ctypes.c_size_t
     assert lib.svtad_fwd_workspace_bytes(192, 192, 1) == 9 * 192 * 192 * 2
-    assert lib.svtad_bwd_in_workspace_bytes(256, 128, 1) == 9 * 256 * 128 * 2
+    # backward-input: the packed weight plus the 256-byte orphan flag block
+    assert lib.svtad_bwd_in_workspace_bytes(256, 128, 1) == 9 * 256 * 128 * 2 + 256
     assert lib.svtad_fwd_workspace_bytes(256, 256, 2) == 9 * 256 * 256 * 2
     assert lib.svtad_fwd_workspace_bytes(192, 192, 0) == 0  # f32: VALU kernel, no workspace
     assert lib.svtad_fwd_workspace_bytes(20, 36, 1) == 0

@@ -273,6 +273,82 @@ def test_asymmetric_table_orphans(dev, oracle, dname):
     assert oracle.rel_err(_np32(ops.bwd_w(G, X, T, ci, 0)), oracle.bwd_w(go, x, t)) <= tol
 
 
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("c", [64, 192])
+def test_orphan_flag_wide_path(dev, oracle, c, dname):
+    """On the matrix-core path the orphan pass only works when the
+    backward-input kernel flags an entry without its symmetric partner. One
+    packed weight is reused across symmetric, asymmetric and symmetric tables
+    (a set flag may only cost time), then repacked (clears the flag); the
+    per-call op keeps the flag in its workspace. Every result is checked
+    against the oracle."""
+    import opentad_sparse_ops as ops
+
+    _say("orphan-flag", c, dname)
+    dt = _dt(dname)
+    rng = np.random.default_rng(29)
+    mask, x, w, b, go = _conv_case(31, (1, 4, 12, 12), 0.6, c, c, dname)
+    sym = oracle.build_table(mask)
+    n = sym.shape[0]
+    asym = sym.copy()
+    # one-way links: entries whose partner (j, 8-k) -> i is absent
+    rows = rng.choice(n, size=12, replace=False)
+    for q, i in enumerate(rows):
+        asym[i, q % 9] = int(rng.integers(0, n))
+    X, W, G = (_t(a, dev, dt) for a in (x, w, go))
+    Ts, Ta = _t(sym, dev, _dt("int32")), _t(asym, dev, _dt("int32"))
+    tol = 2 * TOL[dname]
+    ref_s, ref_a = oracle.bwd_in(go, sym, w), oracle.bwd_in(go, asym, w)
+    assert oracle.rel_err(ref_a, ref_s) > 10 * tol  # the one-way links matter
+    _, pb = ops.pack_weight(W, False, True)
+    assert pb.numel() > 0
+    for T, ref in ((Ts, ref_s), (Ta, ref_a), (Ts, ref_s), (Ta, ref_a)):
+        assert oracle.rel_err(_np32(ops.bwd_in_packed(G, T, W, pb, n, c, 0)), ref) <= tol
+    _, pb2 = ops.pack_weight(W, False, True)
+    for T, ref in ((Ta, ref_a), (Ts, ref_s)):
+        assert oracle.rel_err(_np32(ops.bwd_in_packed(G, T, W, pb2, n, c, 0)), ref) <= tol
+        assert oracle.rel_err(_np32(ops.bwd_in(G, T, W, n, c, 0)), ref) <= tol
+
+
+@pytest.mark.parametrize("ci,co,dname", [(192, 192, "float16"), (64, 64, "bfloat16"),
+                                         (48, 64, "float16"), (128, 96, "bfloat16")])
+def test_bwd_packed_matches(dev, oracle, ci, co, dname):
+    """bwd_packed (the autograd backward in one call) gives what bwd_in_packed +
+    bwd_w_bias give: bit-identical on symmetric tables (same kernels, no
+    atomics), within tolerance of the oracle when one-way links send work to
+    the orphan pass (inside the reduction for the large-tile shapes, a pass of
+    its own for 48 -> 64; 128 -> 96 has no packed backward-input layout and
+    falls back to the two calls)."""
+    import opentad_sparse_ops as ops
+    import torch
+
+    _say("bwd_packed", ci, co, dname)
+    dt = _dt(dname)
+    mask, x, w, b, go = _conv_case(37, (1, 6, 14, 14), 0.5, ci, co, dname)
+    sym = oracle.build_table(mask)
+    n = sym.shape[0]
+    X, W, G = (_t(a, dev, dt) for a in (x, w, go))
+    Ts = _t(sym, dev, _dt("int32"))
+    _, pb = ops.pack_weight(W, False, True)
+    assert (pb.numel() > 0) == (co in (64, 128, 192, 256, 512))
+    gi, gw, gb = ops.bwd_packed(G, X, Ts, W, pb, ci, 0, True)
+    gi2 = ops.bwd_in_packed(G, Ts, W, pb, n, ci, 0)
+    gw2, gb2 = ops.bwd_w_bias(G, X, Ts, ci, 0, True)
+    assert torch.equal(gi, gi2) and torch.equal(gw, gw2) and torch.equal(gb, gb2)
+    _, gw3, gb3 = ops.bwd_packed(G, X, Ts, W, pb, ci, 0, False)
+    assert torch.equal(gw3, gw2) and gb3.numel() == 0
+    rng = np.random.default_rng(41)
+    asym = sym.copy()
+    for q, i in enumerate(rng.choice(n, size=10, replace=False)):
+        asym[i, q % 9] = int(rng.integers(0, n))
+    Ta = _t(asym, dev, _dt("int32"))
+    tol = 2 * TOL[dname]
+    gi, gw, gb = ops.bwd_packed(G, X, Ta, W, pb, ci, 0, True)
+    assert oracle.rel_err(_np32(gi), oracle.bwd_in(go, asym, w)) <= tol
+    assert oracle.rel_err(_np32(gw), oracle.bwd_w(go, x, asym)) <= tol
+    assert oracle.rel_err(_np32(gb), go.astype(np.float64).sum(0)) <= tol
+
+
 def test_empty_and_isolated(dev, oracle):
     import opentad_sparse_ops as ops
     import torch
