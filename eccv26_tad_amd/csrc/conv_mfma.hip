@@ -256,24 +256,45 @@ __global__ __launch_bounds__(WGM* WGN * 64) void k_gg_mfma(
 // Wide gathered GEMM (forward / backward-input) for reduction widths CR in
 // {64, 128, 192, 256, 512}: a workgroup owns BM = FM*16 rows and BN = 4*FN*16
 // output columns; each of its 4 waves owns FN*16 of the columns and all BM
-// rows. Per neighbor offset k, the BM gathered source rows (all CR values)
-// are staged once in LDS (two slices alternate, the next slice's loads are in
-// flight while the current one is consumed); B fragments come straight from
-// global memory (L2-resident weights), D steps ahead in a register ring.
-//   B operand for both modes: the weight in MFMA fragment order (k_pack_frag).
+// rows; WS wave sets of 4 waves split the neighbor offsets (set h takes
+// klist[h], klist[h + WS], ...) and sum their accumulators through LDS.
+//
+// The gathered rows come from LDS in one of two modes, chosen per tile:
+//  * window: the rows a tile gathers lie in a short range [lo, hi] of
+//    source rows (for the tables built from masks, neighbors stay within a
+//    frame, about BM + 30 rows). That range is loaded once, contiguously,
+//    with a zero row for missing neighbors; every offset's fragments are then
+//    read through the table from LDS, and the main loop has no A loads and no
+//    barriers.
+//  * slices (any table): per offset, the BM gathered rows are staged in LDS
+//    (two slices alternate; the next slice's loads are in flight while the
+//    current one is consumed).
+// Weight fragments come straight from global memory (L2-resident), D steps
+// ahead in a register ring (the fragment-ordered layout of k_pack_frag).
+// The MFMA takes the weight fragment as its A operand and the gathered rows
+// as B, so each lane accumulates 4 consecutive output columns of one row
+// (acc[a][f][j] = out[a*16 + lane%16][f*16 + (lane/16)*4 + j] in the wave's
+// columns), which the epilogue packs into 8-byte stores.
 // ---------------------------------------------------------------------------
+// LDS rows (of CR 16-bit elements) of k_gg_wide: the per-set slices, a
+// window of at least BM + 64 rows, and the set reduction / output tile that
+// reuse them at the end.
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
+constexpr int gg_lds_rows(int CR, int FM, int FN, int WS) {
+    return cmax(cmax(WS * FM * 16, FM * 16 + 64),
+                cmax(WS > 1 ? (FM * 16 * (4 * FN * 16 + 4) * 4 + CR * 2 - 1) / (CR * 2) : 0,
+                     (FM * 16 * (4 * FN * 16 + 8) * 2 + CR * 2 - 1) / (CR * 2)));
+}
+
 template <typename T, int MODE, int CR, int FM, int FN, int D, int WS>
 __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const T* __restrict__ src, const int32_t* __restrict__ nbr, const T* __restrict__ wb,
     const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n, int n_out,
     int64_t tpb, int n_col_tiles, int64_t n_tiles, uint32_t* __restrict__ orphan_flag) {
-    // WS wave sets of 4 waves share the tile; set h takes the offsets
-    // klist[h], klist[h + WS], ... so WS independent load streams are in
-    // flight per workgroup. The sets' accumulators are summed through LDS.
     constexpr int BM = FM * 16;
     constexpr int BN = 4 * FN * 16;
     constexpr int NC = CR / KS;
-    // A slice rows are CR elements with no padding; 16-byte chunk q of row m is
+    // LDS rows are CR elements with no padding; 16-byte chunk q of row m is
     // stored at position q ^ (m & 7) (CR / 8 is a multiple of 8, so the swizzle
     // stays inside the row). Fragment reads (16 rows x 4 chunks) and the row
     // stores then both run at the full LDS rate; a 16-byte pad does not.
@@ -281,19 +302,14 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     constexpr int CPR = CR / 8;  // 16-byte chunks per row
     static_assert(CPR % 8 == 0, "the chunk swizzle needs a multiple of 8 chunks per row");
     constexpr int A_CHUNKS = BM * CPR;
-    constexpr int A_PER = (A_CHUNKS + 255) / 256;
-    // rows past BM take the stores of threads without a chunk in the last
-    // round, so every thread stores unconditionally
-    constexpr int APAD = (A_PER * 256 - A_CHUNKS + CPR - 1) / CPR;
+    constexpr int LROWS = gg_lds_rows(CR, FM, FN, WS);
     static_assert(NC % D == 0, "ring depth must divide the steps of a slice");
-    static_assert(WS == 1 || (size_t)BM * BN * 4 <= sizeof(u16) * 2 * BM * RP,
-                  "the partial accumulators of a set must fit in its A buffers");
 
-    __shared__ __align__(16) u16 As[WS][2][BM + APAD][RP];
-    __shared__ uint32_t soff[9][BM];  // byte offset of the gathered row, kOOB if missing
+    __shared__ __align__(16) u16 Ab[LROWS][RP];
+    __shared__ int srow[9][BM];  // gathered source row, -1 if missing
     __shared__ int kvalid[9];
     __shared__ int klist[10];
-    __shared__ int nk_s;
+    __shared__ int nk_s, lo_s, hi_s;
 
     const int tid = threadIdx.x;
     const int set = tid >> 8, ltid = tid & 255;
@@ -303,27 +319,49 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const int col0 = (int)(tile % n_col_tiles) * BN;
 
     if (tid < 9) kvalid[tid] = 0;
+    if (tid == 0) {
+        lo_s = INT32_MAX;
+        hi_s = -1;
+    }
     __syncthreads();
+    // the tile's table rows are contiguous: entry e = m*9 + kk is read in order
+    int lo = INT32_MAX, hi = -1;
     for (int e = tid; e < 9 * BM; e += 256 * WS) {
-        const int k = e / BM, m = e - k * BM;
+        const int m = e / 9, kk = e - m * 9;
         const int64_t i = row0 + m;
+        const int k = MODE == MODE_FWD ? kk : 8 - kk;
         int64_t r = -1;
         if (i < n) {
             if (MODE == MODE_FWD) {
-                r = src_row(nbr, i, k, n, tpb);
+                r = src_row(nbr, i, kk, n, tpb);
             } else {
-                // transposed source (see src_row_t); an entry (i, 8-k) -> p
-                // whose partner (p, k) -> i is absent is left to the orphan
-                // pass, which the flag arms
-                const int64_t p = src_row(nbr, i, 8 - k, n, tpb);
+                // transposed source of offset k (see src_row_t): entry
+                // (i, 8-k) -> p, accepted when its partner (p, k) -> i exists;
+                // one without a partner is left to the orphan pass, which the
+                // flag arms
+                const int64_t p = src_row(nbr, i, kk, n, tpb);
                 if (p >= 0) {
                     if (src_row(nbr, p, k, n, tpb) == i) r = p;
                     else if (orphan_flag) *orphan_flag = 1u;
                 }
             }
         }
-        soff[k][m] = r >= 0 ? (uint32_t)r * (uint32_t)(CR * 2) : kOOB;
-        if (r >= 0) kvalid[k] = 1;
+        srow[k][m] = (int)r;
+        if (r >= 0) {
+            kvalid[k] = 1;
+            lo = min(lo, (int)r);
+            hi = max(hi, (int)r);
+        }
+    }
+    // window bounds: reduce within the wave, then one LDS atomic pair per wave
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        lo = min(lo, __shfl_xor(lo, o));
+        hi = max(hi, __shfl_xor(hi, o));
+    }
+    if (lane == 0 && hi >= 0) {
+        atomicMin(&lo_s, lo);
+        atomicMax(&hi_s, hi);
     }
     __syncthreads();
     if (tid == 0) {
@@ -337,55 +375,37 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const int nk = nk_s;
     const int nk_set = nk > set ? (nk - set + WS - 1) / WS : 0;  // slices of this set
     const int iters = (nk + WS - 1) / WS;
-    const int steps = nk_set * NC;
+    const int wlo = lo_s;
+    const int wrows = hi_s >= 0 ? hi_s - wlo + 1 : 0;
+    const bool window = wrows + 1 <= LROWS;  // + the zero row; uniform
 
     const rsrc_t rs_src = make_rsrc(src, (uint32_t)(n * CR * 2));
-    const rsrc_t rs_w = make_rsrc(wb, (uint32_t)(9 * NC * ((n_out + 15) / 16)) * 1024u);
-
-    // A slice: the BM gathered rows of one offset, 16-byte chunk e = ltid + q*256.
-    // Loads and stores are straight-line (no branch around a load or around
-    // the store that consumes it): a path on which a load is not consumed
-    // makes the compiler wait for every younger load too, including the
-    // weight-ring prefetch.
-    u32x4 ra[A_PER];
-    auto load_a = [&](int it) {
-        const bool live = it < nk_set;
-        const int k = klist[live ? it * WS + set : 0];
-#pragma unroll
-        for (int q = 0; q < A_PER; ++q) {
-            const int e = ltid + q * 256;
-            const int m = min(e / CPR, BM - 1);
-            const uint32_t so = soff[k][m];
-            ra[q] = bload16(rs_src, live && e < A_CHUNKS && so != kOOB ? so + (uint32_t)((e - m * CPR) * 16) : kOOB);
-        }
-    };
-    auto store_a = [&](int buf) {
-#pragma unroll
-        for (int q = 0; q < A_PER; ++q) {
-            const int e = ltid + q * 256;
-            const int m = e / CPR;
-            *(u32x4*)&As[set][buf][m][((e - m * CPR) ^ (m & 7)) * 8] = ra[q];
-        }
-    };
-
-    // B fragments come from the fragment-ordered weight wf (k_pack_frag): the
-    // 64 lanes of fragment (k, c-step, column block) are 1 KB contiguous, so a
-    // fragment load is fully coalesced. Per-lane offsets are fixed; a step adds
-    // the wave-uniform slab offset. Steps past the set's end reload its last step.
     const int nf = (n_out + 15) / 16;
+    const uint32_t step_bytes = (uint32_t)nf * 1024u;  // one reduction step, all column blocks
+    const rsrc_t rs_w = make_rsrc(wb, 9u * NC * step_bytes);
+
+    // Weight fragments (k_pack_frag layout): the 64 lanes of fragment (k,
+    // step, column block) are 1 KB contiguous, so a fragment load is fully
+    // coalesced. The per-lane part of the offset is fixed (kOOB for column
+    // blocks past n_out, which then load zeros); the wave-uniform part (the
+    // slab of the iteration's offset plus the step) goes in the scalar offset,
+    // computed once per slice. Past the set's end the slab is offset 0's
+    // (valid data, never used).
     uint32_t boff[FN];
 #pragma unroll
     for (int f = 0; f < FN; ++f) {
         const int blk = (col0 + wave * FN * 16) / 16 + f;
         boff[f] = blk < nf ? (uint32_t)(blk * 64 + lane) * 16u : kOOB;
     }
+    auto slab_of = [&](int it) -> uint32_t {
+        const int k = it < nk_set ? klist[min(it * WS + set, 9)] : 0;
+        return __builtin_amdgcn_readfirstlane((uint32_t)k * (uint32_t)NC * step_bytes);
+    };
     u32x4 ring[D][FN];
-    auto load_b = [&](int s, u32x4* rb) {
-        const int sc = s < steps ? s : (steps > 0 ? steps - 1 : 0);
-        const int it = sc / NC;
-        const uint32_t so = (uint32_t)((klist[it * WS + set] * NC + (sc - it * NC)) * nf) * 1024u;
+    auto load_b = [&](uint32_t so, u32x4* rb) {
 #pragma unroll
-        for (int f = 0; f < FN; ++f) rb[f] = bload16(rs_w, boff[f] + so);
+        for (int f = 0; f < FN; ++f)
+            rb[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_w, boff[f], so, 0));
     };
 
     f32x4 acc[FM][FN];
@@ -394,52 +414,116 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
 #pragma unroll
         for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load_a(0);
-    store_a(0);
-#pragma unroll
-    for (int d = 0; d < D; ++d) load_b(d, ring[d]);
-    __syncthreads();
-
     const int arow = lane & 15;
-    // chunk of step c is 4c + lane/16, stored at (4c + lane/16) ^ (lane & 7):
-    // 4c + t for even c and 4(c-1) + (t ^ 4) for odd c, t = lane/16 ^ lane&7
-    const int sw = ((lane >> 4) ^ (lane & 7)) * 8;
-    const int swz[2] = {sw, sw ^ 32};
-    // With two wave sets, a set with fewer slices than `iters` skips its
-    // last iteration's MFMAs (the other set's waves share its SIMDs); with
-    // one set every iteration is live and the loop has no branch.
-    for (int it = 0; it < iters; ++it) {
-        const int buf = it & 1;
-        load_a(it + 1);
-        if (WS == 1 || it < nk_set)
+    const int g = lane >> 4;  // reduction chunk of the lane within a step
+    u16* const lds = &Ab[0][0];
+
+    // the bias of this lane's output columns, loaded now so the epilogue does
+    // not wait for it
+    float bv[FN][4];
+#pragma unroll
+    for (int f = 0; f < FN; ++f)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int col = col0 + wave * FN * 16 + f * 16 + g * 4 + j;
+            bv[f][j] = 0.f;
+            if (MODE == MODE_FWD && set == 0 && col < n_out) {
+                if (bias_mode == SVTAD_BIAS_FP32) bv[f][j] = ((const float*)bias)[col];
+                else if (bias_mode != SVTAD_BIAS_NONE) bv[f][j] = (float)((const T*)bias)[col];
+            }
+        }
+
+    // One offset's slice: this lane's fragment rows start at element offsets
+    // off0[a] (even steps) / off1[a] (odd steps) of the LDS rows; the ring
+    // holds the slice's first D steps and is refilled D steps ahead, into the
+    // next slice (slab_next) at the end.
+    auto compute = [&](const int* off0, const int* off1, uint32_t slab, uint32_t slab_next) {
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int d = c % D;
             u32x4 fa[FM];
 #pragma unroll
-            for (int a = 0; a < FM; ++a) fa[a] = *(const u32x4*)&As[set][buf][a * 16 + arow][(c & ~1) * KS + swz[c & 1]];
+            for (int a = 0; a < FM; ++a)
+                fa[a] = *(const u32x4*)&lds[((c & 1) ? off1[a] : off0[a]) + (c & ~1) * KS];
 #pragma unroll
             for (int a = 0; a < FM; ++a)
 #pragma unroll
-                for (int f = 0; f < FN; ++f) acc[a][f] = MfmaOp<T>::run(fa[a], ring[d][f], acc[a][f]);
-            load_b(it * NC + c + D, ring[d]);
+                for (int f = 0; f < FN; ++f) acc[a][f] = MfmaOp<T>::run(ring[d][f], fa[a], acc[a][f]);
+            const int cn = c + D;
+            load_b(cn < NC ? slab + (uint32_t)cn * step_bytes : slab_next + (uint32_t)(cn - NC) * step_bytes, ring[d]);
         }
-        store_a(buf ^ 1);
+    };
+    // LDS row r, chunk position for reduction chunk q: (q ^ (r & 7)); the
+    // element offsets of a lane's even / odd steps in row r:
+    auto row_offs = [&](int r, int& o0, int& o1) {
+        const int sw = (g ^ (r & 7)) * 8;
+        o0 = r * RP + sw;
+        o1 = r * RP + (sw ^ 32);
+    };
+
+    uint32_t slab = slab_of(0);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_b(slab + (uint32_t)d * step_bytes, ring[d]);
+
+    if (window) {
+        // rows wlo .. wlo + wrows - 1 into LDS rows 0 .., zeros in row wrows
+        for (int e = tid; e < (wrows + 1) * CPR; e += 256 * WS) {
+            const int r = e / CPR, q = e - r * CPR;
+            const u32x4 v = bload16(rs_src, r < wrows ? (uint32_t)(wlo + r) * (uint32_t)(CR * 2) + (uint32_t)q * 16u : kOOB);
+            *(u32x4*)&lds[r * RP + ((q ^ (r & 7)) * 8)] = v;
+        }
         __syncthreads();
+        // no barrier from here on: the sets walk their slices independently
+        for (int it = 0; it < nk_set; ++it) {
+            const int k = klist[it * WS + set];
+            const uint32_t slab_next = slab_of(it + 1);
+            int off0[FM], off1[FM];
+#pragma unroll
+            for (int a = 0; a < FM; ++a) {
+                const int r = srow[k][a * 16 + arow];
+                row_offs(r >= 0 ? r - wlo : wrows, off0[a], off1[a]);
+            }
+            compute(off0, off1, slab, slab_next);
+            slab = slab_next;
+        }
+    } else {
+        // any table: per iteration each set stages its offset's BM gathered
+        // rows in its rows [set * BM, +BM) of LDS
+        int off0[FM], off1[FM];
+#pragma unroll
+        for (int a = 0; a < FM; ++a) row_offs(set * BM + a * 16 + arow, off0[a], off1[a]);
+        for (int it = 0; it < iters; ++it) {
+            const bool live = it < nk_set;
+            const int k = klist[live ? it * WS + set : 0];
+            for (int e = ltid; e < A_CHUNKS; e += 256) {
+                const int m = e / CPR, q = e - m * CPR;
+                const int r = live ? srow[k][m] : -1;
+                const u32x4 v = bload16(rs_src, r >= 0 ? (uint32_t)r * (uint32_t)(CR * 2) + (uint32_t)q * 16u : kOOB);
+                *(u32x4*)&lds[(set * BM + m) * RP + ((q ^ (m & 7)) * 8)] = v;
+            }
+            __syncthreads();
+            const uint32_t slab_next = slab_of(it + 1);
+            if (live) compute(off0, off1, slab, slab_next);
+            slab = slab_next;
+            __syncthreads();
+        }
     }
+    __syncthreads();  // all waves are done reading the LDS rows
 
     if constexpr (WS > 1) {
-        // sets 1.. add their partial sums into set 0's through LDS (fixed order)
-        float* red = (float*)&As[0][0][0][0];
+        // sets 1.. add their partial sums into set 0's through LDS (fixed
+        // order); 16-byte rows of 4 columns, the pitch padded by 4 floats so
+        // the 16 rows of an instruction fall on different banks
+        constexpr int RED = BN + 4;
+        static_assert((size_t)BM * RED * 4 <= sizeof(Ab), "the partial accumulators must fit in LDS");
+        float* red = (float*)&Ab[0][0];
         for (int h = 1; h < WS; ++h) {
             if (set == h) {
 #pragma unroll
                 for (int f = 0; f < FN; ++f)
 #pragma unroll
                     for (int a = 0; a < FM; ++a)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            red[(a * 16 + (lane >> 4) * 4 + j) * BN + wave * FN * 16 + f * 16 + (lane & 15)] = acc[a][f][j];
+                        *(f32x4*)&red[(a * 16 + arow) * RED + wave * FN * 16 + f * 16 + g * 4] = acc[a][f];
             }
             __syncthreads();
             if (set == 0) {
@@ -447,41 +531,36 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
                 for (int f = 0; f < FN; ++f)
 #pragma unroll
                     for (int a = 0; a < FM; ++a)
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            acc[a][f][j] += red[(a * 16 + (lane >> 4) * 4 + j) * BN + wave * FN * 16 + f * 16 + (lane & 15)];
+                        acc[a][f] += *(const f32x4*)&red[(a * 16 + arow) * RED + wave * FN * 16 + f * 16 + g * 4];
             }
             __syncthreads();
         }
     }
 
-    // epilogue: round (with the bias) into an LDS copy of the output tile, then
-    // write whole 16-byte chunks so each output row goes out as one run
+    // epilogue: round (with the bias) into an LDS copy of the output tile, 4
+    // columns per 8-byte store, then write whole 16-byte chunks so each
+    // output row goes out as one run
     constexpr int OP = BN + 8;
-    static_assert((size_t)BM * OP * 2 <= sizeof(u16) * 2 * BM * RP, "output tile must fit in the A buffers");
-    u16* ot = &As[0][0][0][0];
-    if (WS == 1) __syncthreads();  // all waves are done reading the A buffers
+    static_assert((size_t)BM * OP * 2 <= sizeof(Ab), "output tile must fit in LDS");
+    u16* ot = &Ab[0][0];
     if (set == 0) {
 #pragma unroll
         for (int f = 0; f < FN; ++f) {
-            const int lc = wave * FN * 16 + f * 16 + (lane & 15);
-            const int col = col0 + lc;
-            float bv = 0.f;
-            if (col < n_out) {
-                if (bias_mode == SVTAD_BIAS_FP32) bv = ((const float*)bias)[col];
-                else if (bias_mode != SVTAD_BIAS_NONE) bv = (float)((const T*)bias)[col];
-            }
+            const int lc = wave * FN * 16 + f * 16 + g * 4;
 #pragma unroll
             for (int a = 0; a < FM; ++a) {
+                unsigned h[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float v = acc[a][f][j];
                     T o;
-                    if (bias_mode == SVTAD_BIAS_PRE || bias_mode == SVTAD_BIAS_FP32) o = (T)(v + bv);
-                    else if (bias_mode == SVTAD_BIAS_AFTER) o = (T)((float)(T)v + bv);
+                    if (bias_mode == SVTAD_BIAS_PRE || bias_mode == SVTAD_BIAS_FP32) o = (T)(v + bv[f][j]);
+                    else if (bias_mode == SVTAD_BIAS_AFTER) o = (T)((float)(T)v + bv[f][j]);
                     else o = (T)v;
-                    ot[(a * 16 + (lane >> 4) * 4 + j) * OP + lc] = __builtin_bit_cast(u16, o);
+                    h[j] = (unsigned)__builtin_bit_cast(u16, o);
                 }
+                typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+                *(u32x2*)&ot[(a * 16 + arow) * OP + lc] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
             }
         }
     }
@@ -1049,11 +1128,13 @@ static void launch_wide(const void* src, const int32_t* nbr, const void* wb, con
                         int bias_mode, void* out, int64_t n, int n_out, int64_t tpb, uint32_t* flag,
                         hipStream_t s) {
     constexpr int BN = 4 * FN * 16;
-    // two wave sets when both sets' double-buffered A slices (with the pad
-    // rows k_gg_wide adds) fit in LDS
-    constexpr int CPR = CR / 8, A_CHUNKS = FM * 16 * CPR, A_PER = (A_CHUNKS + 255) / 256;
-    constexpr int APAD = (A_PER * 256 - A_CHUNKS + CPR - 1) / CPR;
-    constexpr int WS = (size_t)2 * 2 * (FM * 16 + APAD) * CR * 2 <= 150 * 1024 ? 2 : 1;
+    // two wave sets (two waves per SIMD, at most 256 registers each) when
+    // their LDS fits and the accumulators, weight ring and row fragments
+    // leave room for the rest; else one set
+    constexpr int WS = (size_t)gg_lds_rows(CR, FM, FN, 2) * CR * 2 <= 150 * 1024 &&
+                               4 * (FM * FN + D * FN + FM + (MODE == MODE_FWD ? FN : 0)) <= 176
+                           ? 2
+                           : 1;
     const int n_col = (int)cdiv(n_out, BN);
     const int64_t tiles = cdiv(n, 16 * FM) * n_col;
     hipLaunchKernelGGL((k_gg_wide<T, MODE, CR, FM, FN, D, WS>), dim3((unsigned)tiles), dim3(256 * WS),
