@@ -349,6 +349,43 @@ def test_bwd_packed_matches(dev, oracle, ci, co, dname):
     assert oracle.rel_err(_np32(gb), go.astype(np.float64).sum(0)) <= tol
 
 
+@pytest.mark.parametrize("c,dname", [(192, "float16"), (64, "bfloat16")])
+def test_far_symmetric_table_slice_fallback(dev, oracle, c, dname):
+    """A symmetric table whose neighbors are random rows anywhere in [0, n):
+    the row windows of the tiles do not fit in LDS, so the gathered GEMMs take
+    their per-offset slice path (a table from a mask takes the window path).
+    fwd, bwd_in (no orphans: every link has its partner) and bwd_w against the
+    oracle."""
+    import opentad_sparse_ops as ops
+
+    _say("far-table", c, dname)
+    dt = _dt(dname)
+    rng = np.random.default_rng(53)
+    n = 3000
+    t = np.full((n, 9), -1, np.int32)
+    t[:, 4] = np.arange(n)
+    for k in range(4):  # offset k pairs with 8 - k
+        perm = rng.permutation(n)
+        a, b = perm[: n // 2], perm[n // 2: 2 * (n // 2)]
+        keep = rng.random(a.shape[0]) < 0.8
+        t[a[keep], k] = b[keep]
+        t[b[keep], 8 - k] = a[keep]
+    assert all((t[t[:, k][t[:, k] >= 0], 8 - k] == np.nonzero(t[:, k] >= 0)[0]).all() for k in range(9))
+    x = _rounded(rng.standard_normal((n, c)).astype(np.float32), dt)
+    w = _rounded(kaiming_weight(rng, c, c), dt)
+    go = _rounded(rng.standard_normal((n, c)).astype(np.float32), dt)
+    X, W, G = (_t(a_, dev, dt) for a_ in (x, w, go))
+    T = _t(t, dev, _dt("int32"))
+    tol = 2 * TOL[dname]
+    assert oracle.rel_err(_np32(ops.fwd(X, T, W, c, 0)), oracle.fwd(x, t, w)) <= tol
+    assert oracle.rel_err(_np32(ops.bwd_in(G, T, W, n, c, 0)), oracle.bwd_in(go, t, w)) <= tol
+    pf, pb = ops.pack_weight(W, True, True)
+    gi, gw, gb = ops.bwd_packed(G, X, T, W, pb, c, 0, True)
+    assert oracle.rel_err(_np32(gi), oracle.bwd_in(go, t, w)) <= tol
+    assert oracle.rel_err(_np32(gw), oracle.bwd_w(go, x, t)) <= tol
+    assert oracle.rel_err(_np32(ops.fwd_packed(X, T, W, pf, None, 0, 0)), oracle.fwd(x, t, w)) <= tol
+
+
 def test_empty_and_isolated(dev, oracle):
     import opentad_sparse_ops as ops
     import torch
