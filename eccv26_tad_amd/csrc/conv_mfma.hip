@@ -317,6 +317,54 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const int64_t tile = xcd_tile(blockIdx.x, n_tiles);
     const int64_t row0 = (tile / n_col_tiles) * BM;
     const int col0 = (int)(tile % n_col_tiles) * BN;
+    const rsrc_t rs_src = make_rsrc(src, (uint32_t)(n * CR * 2));
+
+    constexpr int NT = 256 * WS;
+    // The tile's table rows are contiguous (entry e = m*9 + kk). All table
+    // loads are issued before the speculative window's (below), so waiting for
+    // them leaves the window loads in flight: load waits count loads in issue
+    // order. Backward-input also gathers each entry's partner first.
+    constexpr int TPER = (9 * BM + NT - 1) / NT;
+    const int64_t tile_ents = min<int64_t>(BM, n - row0) * 9;
+    const rsrc_t rs_tab = make_rsrc(nbr, (uint32_t)(n * 9 * 4));
+    auto src_of = [&](int v, int64_t i) -> int64_t {  // table value of row i -> source row or -1
+        if (v < 0) return -1;
+        const int64_t r = (int64_t)v + (tpb > 0 ? (i / tpb) * tpb : 0);
+        return r < n ? r : -1;
+    };
+    int tv[TPER], pv[TPER];
+#pragma unroll
+    for (int q = 0; q < TPER; ++q) {
+        const int e = tid + q * NT;
+        tv[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_tab, e < tile_ents ? (uint32_t)(row0 * 9 + e) * 4u : kOOB, 0, 0);
+    }
+    if (MODE != MODE_FWD) {
+#pragma unroll
+        for (int q = 0; q < TPER; ++q) {
+            const int e = tid + q * NT;
+            const int m = e / 9, kk = e - m * 9;
+            const int64_t p = e < tile_ents ? src_of(tv[q], row0 + m) : -1;
+            pv[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_tab, p >= 0 ? (uint32_t)(p * 9 + (8 - kk)) * 4u : kOOB, 0, 0);
+        }
+    }
+
+    // Speculative window: the rows a table built from a mask gathers lie within
+    // a few dozen rows of the tile, so rows [spec_lo, spec_lo + SPEC) are loaded
+    // now, while the table is processed; LDS row SPEC is the zero row.
+    constexpr int SPEC = LROWS - 1;
+    constexpr int SPEC_CHUNKS = SPEC * CPR;
+    constexpr int SPEC_PER = (SPEC_CHUNKS + NT - 1) / NT;
+    const int64_t spec_lo = row0 - (SPEC - BM) / 2;
+    u32x4 sp[SPEC_PER];
+#pragma unroll
+    for (int q = 0; q < SPEC_PER; ++q) {
+        const int e = tid + q * NT;
+        const int r = e / CPR;
+        const int64_t gr = spec_lo + r;
+        sp[q] = bload16(rs_src, e < SPEC_CHUNKS && gr >= 0 && gr < n
+                                    ? (uint32_t)gr * (uint32_t)(CR * 2) + (uint32_t)(e - r * CPR) * 16u
+                                    : kOOB);
+    }
 
     if (tid < 9) kvalid[tid] = 0;
     if (tid == 0) {
@@ -324,33 +372,34 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
         hi_s = -1;
     }
     __syncthreads();
-    // the tile's table rows are contiguous: entry e = m*9 + kk is read in order
     int lo = INT32_MAX, hi = -1;
-    for (int e = tid; e < 9 * BM; e += 256 * WS) {
-        const int m = e / 9, kk = e - m * 9;
-        const int64_t i = row0 + m;
-        const int k = MODE == MODE_FWD ? kk : 8 - kk;
-        int64_t r = -1;
-        if (i < n) {
-            if (MODE == MODE_FWD) {
-                r = src_row(nbr, i, kk, n, tpb);
-            } else {
-                // transposed source of offset k (see src_row_t): entry
-                // (i, 8-k) -> p, accepted when its partner (p, k) -> i exists;
-                // one without a partner is left to the orphan pass, which the
-                // flag arms
-                const int64_t p = src_row(nbr, i, kk, n, tpb);
-                if (p >= 0) {
-                    if (src_row(nbr, p, k, n, tpb) == i) r = p;
+#pragma unroll
+    for (int q = 0; q < TPER; ++q) {
+        const int e = tid + q * NT;
+        if (e < 9 * BM) {
+            const int m = e / 9, kk = e - m * 9;
+            const int64_t i = row0 + m;
+            const int k = MODE == MODE_FWD ? kk : 8 - kk;
+            int64_t r = -1;
+            if (e < tile_ents) {
+                const int64_t p = src_of(tv[q], i);
+                if (MODE == MODE_FWD) {
+                    r = p;
+                } else if (p >= 0) {
+                    // transposed source of offset k (see src_row_t): entry
+                    // (i, 8-k) -> p, accepted when its partner (p, k) -> i
+                    // exists; one without a partner is left to the orphan
+                    // pass, which the flag arms
+                    if (src_of(pv[q], p) == i) r = p;
                     else if (orphan_flag) *orphan_flag = 1u;
                 }
             }
-        }
-        srow[k][m] = (int)r;
-        if (r >= 0) {
-            kvalid[k] = 1;
-            lo = min(lo, (int)r);
-            hi = max(hi, (int)r);
+            srow[k][m] = (int)r;
+            if (r >= 0) {
+                kvalid[k] = 1;
+                lo = min(lo, (int)r);
+                hi = max(hi, (int)r);
+            }
         }
     }
     // window bounds: reduce within the wave, then one LDS atomic pair per wave
@@ -375,11 +424,24 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const int nk = nk_s;
     const int nk_set = nk > set ? (nk - set + WS - 1) / WS : 0;  // slices of this set
     const int iters = (nk + WS - 1) / WS;
-    const int wlo = lo_s;
-    const int wrows = hi_s >= 0 ? hi_s - wlo + 1 : 0;
-    const bool window = wrows + 1 <= LROWS;  // + the zero row; uniform
+    const int lo_t = lo_s, hi_t = hi_s;
+    const int wrows = hi_t >= 0 ? hi_t - lo_t + 1 : 0;
+    // uniform: the speculative rows hold the window / the exact window fits
+    const bool spec_ok = hi_t < 0 || (lo_t >= spec_lo && hi_t < spec_lo + SPEC);
+    const bool window = spec_ok || wrows + 1 <= LROWS;
+    const int64_t wlo = spec_ok ? spec_lo : lo_t;  // LDS row r holds source row wlo + r
+    const int zrow = spec_ok ? SPEC : wrows;       // the zero row
+    if (spec_ok) {  // the speculative rows into LDS (before the ring takes registers)
+        u16* const l = &Ab[0][0];
+#pragma unroll
+        for (int q = 0; q < SPEC_PER; ++q) {
+            const int e = tid + q * 256 * WS;
+            const int r = e / CPR;
+            if (e < SPEC_CHUNKS) *(u32x4*)&l[r * RP + (((e - r * CPR) ^ (r & 7)) * 8)] = sp[q];
+        }
+        if (tid < CPR) *(u32x4*)&l[SPEC * RP + ((tid ^ (SPEC & 7)) * 8)] = u32x4{0u, 0u, 0u, 0u};
+    }
 
-    const rsrc_t rs_src = make_rsrc(src, (uint32_t)(n * CR * 2));
     const int nf = (n_out + 15) / 16;
     const uint32_t step_bytes = (uint32_t)nf * 1024u;  // one reduction step, all column blocks
     const rsrc_t rs_w = make_rsrc(wb, 9u * NC * step_bytes);
@@ -466,11 +528,13 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     for (int d = 0; d < D; ++d) load_b(slab + (uint32_t)d * step_bytes, ring[d]);
 
     if (window) {
-        // rows wlo .. wlo + wrows - 1 into LDS rows 0 .., zeros in row wrows
-        for (int e = tid; e < (wrows + 1) * CPR; e += 256 * WS) {
-            const int r = e / CPR, q = e - r * CPR;
-            const u32x4 v = bload16(rs_src, r < wrows ? (uint32_t)(wlo + r) * (uint32_t)(CR * 2) + (uint32_t)q * 16u : kOOB);
-            *(u32x4*)&lds[r * RP + ((q ^ (r & 7)) * 8)] = v;
+        if (!spec_ok) {
+            // rows wlo .. wlo + wrows - 1 into LDS rows 0 .., zeros in row wrows
+            for (int e = tid; e < (wrows + 1) * CPR; e += 256 * WS) {
+                const int r = e / CPR, q = e - r * CPR;
+                const u32x4 v = bload16(rs_src, r < wrows ? (uint32_t)(wlo + r) * (uint32_t)(CR * 2) + (uint32_t)q * 16u : kOOB);
+                *(u32x4*)&lds[r * RP + ((q ^ (r & 7)) * 8)] = v;
+            }
         }
         __syncthreads();
         // no barrier from here on: the sets walk their slices independently
@@ -481,7 +545,7 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
 #pragma unroll
             for (int a = 0; a < FM; ++a) {
                 const int r = srow[k][a * 16 + arow];
-                row_offs(r >= 0 ? r - wlo : wrows, off0[a], off1[a]);
+                row_offs(r >= 0 ? (int)(r - wlo) : zrow, off0[a], off1[a]);
             }
             compute(off0, off1, slab, slab_next);
             slab = slab_next;
