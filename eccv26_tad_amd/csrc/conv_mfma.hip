@@ -500,17 +500,22 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     // holds the slice's first D steps and is refilled D steps ahead, into the
     // next slice (slab_next) at the end.
     auto compute = [&](const int* off0, const int* off1, uint32_t slab, uint32_t slab_next) {
+        // the row fragments of step c + 1 are read while step c's MFMAs run
+        u32x4 fa[2][FM];
+#pragma unroll
+        for (int a = 0; a < FM; ++a) fa[0][a] = *(const u32x4*)&lds[off0[a]];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const int d = c % D;
-            u32x4 fa[FM];
+            if (c + 1 < NC) {
+#pragma unroll
+                for (int a = 0; a < FM; ++a)
+                    fa[(c + 1) & 1][a] = *(const u32x4*)&lds[(((c + 1) & 1) ? off1[a] : off0[a]) + ((c + 1) & ~1) * KS];
+            }
 #pragma unroll
             for (int a = 0; a < FM; ++a)
-                fa[a] = *(const u32x4*)&lds[((c & 1) ? off1[a] : off0[a]) + (c & ~1) * KS];
 #pragma unroll
-            for (int a = 0; a < FM; ++a)
-#pragma unroll
-                for (int f = 0; f < FN; ++f) acc[a][f] = MfmaOp<T>::run(ring[d][f], fa[a], acc[a][f]);
+                for (int f = 0; f < FN; ++f) acc[a][f] = MfmaOp<T>::run(ring[d][f], fa[c & 1][a], acc[a][f]);
             const int cn = c + D;
             load_b(cn < NC ? slab + (uint32_t)cn * step_bytes : slab_next + (uint32_t)(cn - NC) * step_bytes, ring[d]);
         }
@@ -1147,8 +1152,9 @@ bool gg_mfma_supported(int dtype, int c_red, int n_out) {
 
 // Reduction widths with a wide-kernel instantiation and its (FM, FN, D).
 struct WideCfg { int cr, fm, fn, d; };
-static const WideCfg kWide[] = {{64, 8, 1, 2}, {128, 8, 2, 4}, {192, 8, 3, 6},
-                                {256, 8, 4, 4}, {512, 4, 4, 4}};
+// A two-step weight ring measured faster than deeper ones (fewer registers).
+static const WideCfg kWide[] = {{64, 8, 1, 2}, {128, 8, 2, 2}, {192, 8, 3, 2},
+                                {256, 8, 4, 2}, {512, 4, 4, 2}};
 
 static const WideCfg* wide_cfg(int c_red, int n_out) {
     for (const WideCfg& c : kWide)
@@ -1263,10 +1269,10 @@ static bool gg_dispatch(const void* src, const int32_t* nbr, const void* w, cons
         return flag != nullptr;                                                                  \
     }
         SVTAD_WIDE_CASE(64, 8, 1, 2)
-        SVTAD_WIDE_CASE(128, 8, 2, 4)
-        SVTAD_WIDE_CASE(192, 8, 3, 6)
-        SVTAD_WIDE_CASE(256, 8, 4, 4)
-        SVTAD_WIDE_CASE(512, 4, 4, 4)
+        SVTAD_WIDE_CASE(128, 8, 2, 2)
+        SVTAD_WIDE_CASE(192, 8, 3, 2)
+        SVTAD_WIDE_CASE(256, 8, 4, 2)
+        SVTAD_WIDE_CASE(512, 4, 4, 2)
 #undef SVTAD_WIDE_CASE
     }
     if (n_out % 96 == 0)
