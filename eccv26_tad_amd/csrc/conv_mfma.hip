@@ -940,7 +940,17 @@ __device__ __forceinline__ void bw_reduce_one(int64_t e, const float* __restrict
     const int64_t quads = per_split / 4;
     if (e < quads) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int q = 0; q < splits; ++q) acc += *(const f32x4*)(part + q * per_split + e * 4);
+        // eight loads in flight at a time, summed in split order
+        const float* pe = part + e * 4;
+        int q = 0;
+        for (; q + 8 <= splits; q += 8) {
+            f32x4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = *(const f32x4*)(pe + (int64_t)(q + u) * per_split);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; q < splits; ++q) acc += *(const f32x4*)(pe + (int64_t)q * per_split);
         // decode the fragment-order position
         int64_t rest = e * 4;
         const int64_t tile_sz = (int64_t)bm * bn;
@@ -963,7 +973,15 @@ __device__ __forceinline__ void bw_reduce_one(int64_t e, const float* __restrict
     } else if (gb && e - quads < c_out) {
         const int c = (int)(e - quads);
         float v = 0.f;
-        for (int q = 0; q < splits; ++q) v += part_b[(int64_t)q * c_out + c];
+        int q = 0;
+        for (; q + 8 <= splits; q += 8) {
+            float t[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) t[u] = part_b[(int64_t)(q + u) * c_out + c];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += t[u];
+        }
+        for (; q < splits; ++q) v += part_b[(int64_t)q * c_out + c];
         gb[c] = (T)v;
     }
 }

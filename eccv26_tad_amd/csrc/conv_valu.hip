@@ -219,8 +219,17 @@ __global__ __launch_bounds__(256) void k_split_reduce(const A* __restrict__ ws, 
                                                       int splits, T* __restrict__ out) {
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < count;
          e += (int64_t)gridDim.x * 256) {
+        // eight loads in flight at a time, summed in split order
         A s = 0;
-        for (int q = 0; q < splits; ++q) s += ws[(int64_t)q * count + e];
+        int q = 0;
+        for (; q + 8 <= splits; q += 8) {
+            A v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)(q + u) * count + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; q < splits; ++q) s += ws[(int64_t)q * count + e];
         out[e] = from_acc<T>(s);
     }
 }
