@@ -17,3 +17,15 @@ def oracle():
     from oracle import sv_oracle
     sv_oracle.lib()
     return sv_oracle
+
+
+@pytest.fixture(scope="session")
+def dev():
+    """cuda:0 with the extension loaded; a GPU test fails (not skips) without one."""
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible")
+    import eccv26_tad_amd  # noqa: F401
+
+    return torch.device("cuda:0")

@@ -62,17 +62,6 @@ def test_oracle_depthwise(oracle):
 # HIP kernels (GPU)
 # --------------------------------------------------------------------------
 
-@pytest.fixture(scope="module")
-def dev():
-    import torch
-
-    if not torch.cuda.is_available():
-        pytest.fail("no GPU visible")
-    import eccv26_tad_amd  # noqa: F401
-
-    return torch.device("cuda:0")
-
-
 def _err(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)

@@ -18,17 +18,6 @@ pytestmark = pytest.mark.gpu
 TOL = {"float32": 1e-5, "float16": 1e-2, "bfloat16": 1e-2, "float64": 1e-12}
 
 
-@pytest.fixture(scope="module")
-def dev():
-    import torch
-
-    if not torch.cuda.is_available():
-        pytest.fail("no GPU visible")
-    import eccv26_tad_amd  # noqa: F401
-
-    return torch.device("cuda:0")
-
-
 def _say(*a):
     print(*a, flush=True)
     sys.stdout.flush()
