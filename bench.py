@@ -73,15 +73,16 @@ TRAFFIC_PROFILE = os.path.join("profiles", "sparseconv2d_c2_keep055_hbm_traffic.
 
 
 def pmc_traffic(kernel_key):
-    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, KiB per dispatch) of the
-    kernel whose name contains kernel_key, from the committed rocprofv3 --pmc
-    summary of this workload at keep 0.55; None if absent."""
+    """HBM bytes per launch of the kernel whose name contains kernel_key: the
+    committed rocprofv3 --pmc summary's last column, FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch) each scaled by what the counter reads for a plain 1 GiB
+    copy, for this workload at keep 0.55; None if absent."""
     try:
         with open(os.path.join(ROOT, TRAFFIC_PROFILE)) as f:
             for line in f:
                 cells = [c.strip() for c in line.strip().strip("|").split("|")]
-                if len(cells) == 4 and kernel_key in cells[0]:
-                    return int((float(cells[2]) + float(cells[3])) * 1024)
+                if len(cells) == 5 and kernel_key in cells[0]:
+                    return int(cells[4])
     except (OSError, ValueError):
         pass
     return None

@@ -40,8 +40,9 @@ static int check_common(const char* who, int64_t n, int c_in, int c_out, int64_t
 }
 
 // Full conv plan. Rows are split so that the partial-tile workgroups fill the
-// chip (about 256 of them) without splits shorter than 256 rows, and so that
-// no split is longer than 2048 rows.
+// chip's compute units at most once (a second round of workgroups on a few
+// units would nearly double the kernel time), without splits shorter than 256
+// rows, and so that no split is longer than 2048 rows.
 static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     BwPlan p;
     p.path = bw_mfma_supported(dtype, n, c_in, c_out) ? 1 : 0;
@@ -51,7 +52,7 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     int64_t splits;
     if (p.path) {
         splits = std::max<int64_t>(cdiv(n, kMaxSplitRows - 128),
-                                   std::min<int64_t>(cdiv(256, tiles), cdiv(n, 256)));
+                                   std::min<int64_t>(std::max<int64_t>(1, cu_count() / tiles), cdiv(n, 256)));
     } else {
         splits = std::min<int64_t>(cdiv(1024, tiles), std::max<int64_t>(1, n / 128));
     }

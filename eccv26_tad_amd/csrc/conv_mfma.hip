@@ -890,26 +890,42 @@ __global__ __launch_bounds__(256) void k_bw_mfma(
 // ---------------------------------------------------------------------------
 // Backward-weight partials, large tiles (the shapes of the adapter convs).
 // A workgroup owns one offset k, a BM x BN (ci x co) tile of gw and one row
-// split. Per 64-row stage each thread loads an 8-row x 8-channel block of the
-// gathered x rows (or of the go rows) with 16-byte loads (consecutive lanes
-// on consecutive channel chunks of a row), transposes it in registers
-// (v_perm_b32) and writes eight 16-byte rows of a [channel][row] LDS tile
-// (swizzled by bw_swz); the MFMA fragments (8 consecutive rows of one
-// channel) are then single 16-byte LDS reads. Each wave stages only x or only
-// go rows. Two register stages keep the loads of stage t+2 in flight while
-// stage t runs. Partials are stored in fragment order (each lane's 4 values
-// contiguous); k_bw_reduce sums the splits in a fixed order. The k == 4,
-// ci-tile 0 workgroups also sum the staged go rows per column (bias).
+// split, and has two kinds of waves:
+//  * WGM x WGN matrix waves, each owning FM x FN 16x16 fragments of the tile;
+//    per 64-row stage they read their fragments from LDS and run the MFMAs.
+//  * WA + WB staging waves: per stage each thread loads an 8-row x 8-channel
+//    block of the gathered x rows (waves [0, WA)) or of the go rows (the
+//    next WB) with 16-byte loads (consecutive lanes on consecutive channel
+//    chunks of a row), transposes it in registers (v_perm_b32) and writes
+//    eight 16-byte rows of a [channel][row] LDS tile (swizzled by bw_swz), so
+//    that an MFMA fragment (8 consecutive rows of one channel) is one 16-byte
+//    LDS read.
+// Between two barriers the matrix waves consume stage t from one LDS buffer
+// while the staging waves fill the other with stage t+1 and have the loads of
+// stage t+2 in flight: the MFMAs, the transposes and LDS writes, and the
+// global loads run at the same time on different waves. (With one kind of
+// wave doing both, every wave of a SIMD is in its transpose phase at the same
+// time and the matrix core idles.) Partials are stored in fragment order
+// (each lane's 4 values contiguous); k_bw_reduce sums the splits in a fixed
+// order. In the k == 4, ci-tile 0 workgroups the staging waves also sum the
+// staged go rows per column (bias).
 // ---------------------------------------------------------------------------
 // A transposed stage row (one channel, KR = 64 source rows) is 128 bytes with
 // no padding; its eight 16-byte chunks (8 rows each) are stored at position
-// chunk ^ (channel & 7) ^ ((channel >> 3) & 7). The MFMA fragment reads (16
-// consecutive channels x 4 chunks per instruction) and the transposed stores
-// (8 lanes on 8 consecutive channel chunks, i.e. channels 8 apart) then both
-// run at the full LDS rate on gfx950; a padded 144-byte pitch halves the
-// fragment-read rate. Returns the element offset in the row.
+// chunk ^ (channel & 7) ^ rot3((channel >> 3) & 7), rot3 a 3-bit rotate left.
+// On gfx950 (measured with bank-conflict counters) a 16-byte LDS read serves
+// lanes {0-7, 24-31}, {8-15, 16-23} (and the same in the upper half) together,
+// and a 16-byte LDS write serves 8 consecutive lanes together; the 16 lanes
+// served together must touch distinct 16-byte bank groups (64 banks of 4
+// bytes). The fragment reads (16 consecutive channels x 4 chunks) then have
+// no conflicts because rot3 changes between the two 8-channel halves of a
+// fragment by an even amount, while (channel >> 3) alone changes by 1 and
+// makes lanes i and 24+i collide; the transposed stores (8 lanes on 8
+// consecutive channel chunks) have none because rot3 is a bijection. A padded
+// 144-byte pitch halves the read rate. Returns the element offset in the row.
 __device__ __forceinline__ int bw_swz(int channel, int chunk) {
-    return (chunk ^ (channel & 7) ^ ((channel >> 3) & 7)) * 8;
+    const int hi = (channel >> 3) & 7;
+    return (chunk ^ (channel & 7) ^ (((hi << 1) | (hi >> 2)) & 7)) * 8;
 }
 
 // 8x8 transpose of 16-bit values: in[r] holds channels 0..7 of row r; out[c]
@@ -986,34 +1002,47 @@ __device__ __forceinline__ void bw_reduce_one(int64_t e, const float* __restrict
     }
 }
 
+// staging waves of k_bw_big: one 8-row x 8-channel block of x rows or of go
+// rows per thread and stage
+constexpr int BW_IROWS = 8;
+constexpr int bw_stage_waves(int fm, int fn, int wgm, int wgn) {
+    return ((KR / BW_IROWS) * (wgm * fm * 2) + 63) / 64 + ((KR / BW_IROWS) * (wgn * fn * 2) + 63) / 64;
+}
+constexpr int bw_big_threads(int fm, int fn, int wgm, int wgn) {
+    return 64 * (wgm * wgn + bw_stage_waves(fm, fn, wgm, wgn));
+}
+
 template <typename T, int FM, int FN, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
+__global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     const T* __restrict__ go, const T* __restrict__ x, const int32_t* __restrict__ nbr,
     float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int c_in, int c_out,
     int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks) {
-    constexpr int NT = 64 * WGM * WGN;
+    constexpr int NT = bw_big_threads(FM, FN, WGM, WGN);
+    constexpr int NMW = WGM * WGN;     // matrix waves
     constexpr int BM = WGM * FM * 16;  // ci
     constexpr int BN = WGN * FN * 16;  // co
-    constexpr int A_ITEMS = (KR / 8) * (BM / 8);  // 8x8 blocks per stage
-    constexpr int B_ITEMS = (KR / 8) * (BN / 8);
-    // Consecutive items walk the 8-channel chunks of one row group, so four
-    // consecutive lanes load 64 contiguous bytes of a row (lanes walking the
+    constexpr int A_ITEMS = (KR / BW_IROWS) * (BM / 8);  // 8x8 blocks per stage
+    constexpr int B_ITEMS = (KR / BW_IROWS) * (BN / 8);
+    // Consecutive items walk the 8-channel chunks of one row group, so eight
+    // consecutive lanes load 128 contiguous bytes of a row (lanes walking the
     // row groups instead load 16 bytes from each of 8 rows per 8 lanes, which
     // costs more address-unit cycles than the LDS conflicts it avoids; the
     // bw_swz swizzle keeps the chunk-major stores conflict-free).
     constexpr int CPT_A = BM / 8, CPT_B = BN / 8;  // channel chunks per row group
-    // Each wave stages one operand: waves [0, WA) the gathered x rows (A
-    // items), waves [WA, WA + WB) the go rows (B items), any others nothing.
-    // With a wave-uniform role the loads are one straight-line path writing
-    // one register set; two load paths writing the same registers (even if
-    // a wave only ever takes one) make the compiler wait for every load in
-    // flight before issuing the next stage's, which serialises the prefetch.
     constexpr int WA = (A_ITEMS + 63) / 64, WB = (B_ITEMS + 63) / 64;
-    static_assert(WA + WB <= NT / 64, "one staging item per thread");
+    static_assert(NMW + WA + WB == NT / 64, "wave roles");
+    constexpr int NST = 64 * (WA + WB);         // staging threads
+    constexpr int BPT = (BN + NST - 1) / NST;  // bias columns per staging thread
 
-    __shared__ __align__(16) u16 As[2][BM][KR];
-    __shared__ __align__(16) u16 Bs[2][BN][KR];
-    __shared__ __align__(16) uint32_t srow[kMaxSplitRows];
+    // [buf][channel][row] tiles: the x operand's two buffers, then go's
+    __shared__ __align__(16) u16 stage_lds[2 * (BM + BN) * KR];
+    u16(*const As)[BM][KR] = (u16(*)[BM][KR])stage_lds;
+    u16(*const Bs)[BN][KR] = (u16(*)[BN][KR])(stage_lds + 2 * BM * KR);
+    // byte offsets of the split's rows in x (gathered) and in go (linear),
+    // kOOB for missing neighbors and for rows past the split; two stages
+    // past the last one so that the prefetch needs no bounds test
+    constexpr int TROWS = kMaxSplitRows + 2 * KR;
+    __shared__ __align__(16) uint32_t srow[2][TROWS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -1030,113 +1059,155 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_bw_big(
     const int steps = (rows + KR - 1) / KR;
     const bool do_bias = ws_bias != nullptr && k == 4 && ci0 == 0;  // uniform
 
-    for (int r = tid; r < steps * KR; r += NT) {
+    for (int r = tid; r < (steps + 2) * KR; r += NT) {
         const int64_t sr = r < rows ? src_row(nbr, r_begin + r, k, n, tpb) : -1;
-        srow[r] = sr >= 0 ? (uint32_t)sr * (uint32_t)(c_in * 2) : kOOB;
+        srow[0][r] = sr >= 0 ? (uint32_t)sr * (uint32_t)(c_in * 2) : kOOB;
+        srow[1][r] = r < rows ? (uint32_t)r * (uint32_t)(c_out * 2) : kOOB;
     }
     __syncthreads();
 
-    // item e of the wave's operand: rows 8*(e / cpt) .. +7 of the stage,
-    // channels 8*(e % cpt) .. +7 of the tile. Stages at or past `steps`, and
-    // threads without an item, load zeros (out-of-range buffer offsets).
     const int wv = __builtin_amdgcn_readfirstlane(wave);
-    const bool role_a = wv < WA;
-    const int e = role_a ? tid : tid - WA * 64;
-    const int n_items = role_a ? A_ITEMS : (wv < WA + WB ? B_ITEMS : 0);
-    const bool has_item = e < n_items;
-    const int cpt = role_a ? CPT_A : CPT_B;
-    const int rgp = has_item ? e / cpt : 0, cl = has_item ? (e % cpt) * 8 : 0;
-    const int chan = (role_a ? ci0 : co0) + cl;
-    const bool chan_ok = has_item && chan < (role_a ? c_in : c_out);
-    const rsrc_t rs = make_rsrc(role_a ? (const void*)x : (const void*)(go + r_begin * c_out),
-                                role_a ? (uint32_t)(n * c_in * 2) : (uint32_t)((int64_t)rows * c_out * 2));
-    const uint32_t chan_b = (uint32_t)chan * 2u, row_b = (uint32_t)c_out * 2u;
-
-    u32x4 r0s[8], r1s[8];
-    auto load = [&](int t, u32x4* rg) {
-        const bool live = t < steps;
-        const int rbase = live ? t * KR : 0;
-        const bool ok = live && chan_ok;
-        const u32x4 s0 = *(const u32x4*)&srow[rbase + rgp * 8];
-        const u32x4 s1 = *(const u32x4*)&srow[rbase + rgp * 8 + 4];
+    if (wv < NMW) {
+        // ---------------- matrix waves ----------------
+        f32x4 acc[FM][FN];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const uint32_t so = r < 4 ? s0[r] : s1[r - 4];
-            const uint32_t off = role_a ? (so != kOOB ? so + chan_b : kOOB)
-                                        : (uint32_t)(rbase + rgp * 8 + r) * row_b + chan_b;
-            rg[r] = bload16(rs, ok ? off : kOOB);
-        }
-    };
-    auto store = [&](int buf, const u32x4* rg) {
-        u32x4 o[8];
-        transpose8(rg, o);
-        if (has_item) {
-            u16(*dst)[KR] = role_a ? As[buf] : Bs[buf];
+        for (int a = 0; a < FM; ++a)
 #pragma unroll
-            for (int c = 0; c < 8; ++c) *(u32x4*)&dst[cl + c][bw_swz(cl + c, rgp)] = o[c];
-        }
-    };
-
-    f32x4 acc[FM][FN];
+            for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int wm = wv / WGN, wn = wv % WGN;
+        const int arow = wm * FM * 16 + (lane & 15), brow = wn * FN * 16 + (lane & 15);
+        // fragment chunk of k-step h is h*4 + lane/16 (bw_swz gives its position)
+        const int kq = lane >> 4;
+        auto compute = [&](int buf) {
 #pragma unroll
-    for (int a = 0; a < FM; ++a)
+            for (int h = 0; h < KR / KS; ++h) {
+                u32x4 fb[FN];
 #pragma unroll
-        for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int wm = wave / WGN, wn = wave % WGN;
-    const int arow = wm * FM * 16 + (lane & 15), brow = wn * FN * 16 + (lane & 15);
-    // fragment chunk of k-step h is h*4 + lane/16 (bw_swz gives its position)
-    const int kq = lane >> 4;
-    float bsum = 0.f;
-    auto compute = [&](int buf) {
-        if (do_bias && tid < BN) {  // column sums of the staged go rows
+                for (int b = 0; b < FN; ++b)
+                    fb[b] = *(const u32x4*)&Bs[buf][brow + b * 16][bw_swz(brow + b * 16, h * 4 + kq)];
 #pragma unroll
-            for (int r = 0; r < KR / 8; ++r) {
-                const u32x4 v = *(const u32x4*)&Bs[buf][tid][bw_swz(tid, r)];
+                for (int a = 0; a < FM; ++a) {
+                    const u32x4 fa = *(const u32x4*)&As[buf][arow + a * 16][bw_swz(arow + a * 16, h * 4 + kq)];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    bsum += (float)__builtin_bit_cast(T, (u16)(v[q] & 0xffffu));
-                    bsum += (float)__builtin_bit_cast(T, (u16)(v[q] >> 16));
+                    for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fa, fb[b], acc[a][b]);
                 }
             }
+        };
+        __syncthreads();  // stage 0 staged
+        for (int t = 0; t < steps; t += 2) {
+            compute(0);  // stage t
+            __syncthreads();
+            compute(1);  // stage t+1 (zeros past the end)
+            __syncthreads();
         }
+        // partial tile in fragment order: [wave][a][b][lane][4]
+        float* dst = ws + (((int64_t)s * 9 + k) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
 #pragma unroll
-        for (int h = 0; h < KR / KS; ++h) {
-            u32x4 fb[FN];
+        for (int a = 0; a < FM; ++a)
 #pragma unroll
-            for (int b = 0; b < FN; ++b) fb[b] = *(const u32x4*)&Bs[buf][brow + b * 16][bw_swz(brow + b * 16, h * 4 + kq)];
+            for (int b = 0; b < FN; ++b)
+                *(f32x4*)(dst + (((wv * FM + a) * FN + b) * 64 + lane) * 4) = acc[a][b];
+    } else {
+        // ---------------- staging waves ----------------
+        // item e of the wave's operand: rows 8*(e / cpt) .. +7 of the
+        // stage, channels 8*(e % cpt) .. +7 of the tile. Stages at or past
+        // `steps`, and threads without an item, load zeros (out-of-range
+        // offsets). Everything that depends on the wave's operand is fixed
+        // here, so the loop's loads and stores are one code path for both
+        // operands (a select on a wave-uniform value inside the loop becomes
+        // a branch around each load, and every branch makes the compiler wait
+        // for the loads in flight).
+        const int sw = wv - NMW;  // staging wave index
+        const int st = tid - NMW * 64;
+        const bool role_a = sw < WA;
+        const int e = role_a ? st : st - WA * 64;
+        const int n_items = role_a ? A_ITEMS : B_ITEMS;
+        const bool has_item = e < n_items;
+        const int cpt = role_a ? CPT_A : CPT_B;
+        const int rgp = has_item ? e / cpt : 0, cl = has_item ? (e % cpt) * 8 : 0;
+        const int chan = (role_a ? ci0 : co0) + cl;
+        const bool chan_ok = has_item && chan < (role_a ? c_in : c_out);
+        const rsrc_t rs = make_rsrc(role_a ? (const void*)x : (const void*)(go + r_begin * c_out),
+                                    role_a ? (uint32_t)(n * c_in * 2) : (uint32_t)((int64_t)rows * c_out * 2));
+        // offsets stay below 2^31 + 2^16 (kOOB plus a channel offset): no wrap
+        const uint32_t chan_b = chan_ok ? (uint32_t)chan * 2u : kOOB;
+        const uint32_t* const tab = srow[role_a ? 0 : 1] + rgp * BW_IROWS;
+        // this thread's 8 LDS rows (channels cl .. cl+7) of buffer 0; buffer
+        // 1 is buf_step elements further
+        u16* const dst0 = role_a ? &As[0][cl][0] : &Bs[0][cl][0];
+        const int buf_step = role_a ? BM * KR : BN * KR;
+
+        // two register sets: the loads of stage t+2 are in flight while stage
+        // t+1 is transposed and stored
+        u32x4 r0s[8], r1s[8];
+        auto load = [&](int t, u32x4* rg) {
+            const u32x4 s0 = *(const u32x4*)&tab[t * KR];
+            const u32x4 s1 = *(const u32x4*)&tab[t * KR + 4];
 #pragma unroll
-            for (int a = 0; a < FM; ++a) {
-                const u32x4 fa = *(const u32x4*)&As[buf][arow + a * 16][bw_swz(arow + a * 16, h * 4 + kq)];
+            for (int r = 0; r < 8; ++r) {
+                const uint32_t so = r < 4 ? s0[r] : s1[r - 4];
+                rg[r] = bload16(rs, chan_ok ? so + chan_b : kOOB);
+            }
+        };
+        auto store = [&](int buf, const u32x4* rg) {
+            u32x4 o[8];
+            transpose8(rg, o);
+            if (has_item) {
+                u16* const d = dst0 + buf * buf_step;
 #pragma unroll
-                for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fa, fb[b], acc[a][b]);
+                for (int c = 0; c < 8; ++c) *(u32x4*)&d[c * KR + bw_swz(cl + c, rgp)] = o[c];
+            }
+        };
+        // column sums of the staged go rows (the bias gradient; one
+        // workgroup per column tile), while the matrix waves use the buffer
+        float bsum[BPT];
+#pragma unroll
+        for (int j = 0; j < BPT; ++j) bsum[j] = 0.f;
+        auto bias_sums = [&](int buf) {
+            if (do_bias) {
+#pragma unroll
+                for (int j = 0; j < BPT; ++j) {
+                    const int col = st + j * NST;
+                    if (col < BN) {
+                        // per-lane chunk order chosen so that the 16 lanes
+                        // read together hit distinct bank groups (fixed per
+                        // lane: same sum every run)
+                        const int hi = (col >> 3) & 7, perm = hi ^ (((hi << 1) | (hi >> 2)) & 7);
+#pragma unroll
+                        for (int r = 0; r < KR / 8; ++r) {
+                            const u32x4 v = *(const u32x4*)&Bs[buf][col][bw_swz(col, r ^ perm)];
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                bsum[j] += (float)__builtin_bit_cast(T, (u16)(v[q] & 0xffffu));
+                                bsum[j] += (float)__builtin_bit_cast(T, (u16)(v[q] >> 16));
+                            }
+                        }
+                    }
+                }
+            }
+        };
+        load(0, r0s);
+        load(1, r1s);
+        store(0, r0s);
+        __syncthreads();  // stage 0 staged
+        for (int t = 0; t < steps; t += 2) {
+            load(t + 2, r0s);  // registers of set 0 are free again
+            store(1, r1s);     // stage t+1 (zeros past the end)
+            bias_sums(0);
+            __syncthreads();
+            load(t + 3, r1s);
+            store(0, r0s);     // stage t+2
+            bias_sums(1);
+            __syncthreads();
+        }
+        if (do_bias) {
+#pragma unroll
+            for (int j = 0; j < BPT; ++j) {
+                const int col = st + j * NST;
+                if (col < BN && co0 + col < c_out) ws_bias[(int64_t)s * c_out + co0 + col] = bsum[j];
             }
         }
-    };
-
-    load(0, r0s);
-    load(1, r1s);
-    store(0, r0s);
-    __syncthreads();
-    for (int t = 0; t < steps; t += 2) {
-        load(t + 2, r0s);  // registers of set 0 are free again
-        compute(0);        // stage t
-        store(1, r1s);     // stage t+1 (zeros past the end)
-        __syncthreads();
-        load(t + 3, r1s);
-        compute(1);        // stage t+1
-        store(0, r0s);     // stage t+2
-        __syncthreads();
     }
-
-    // partial tile in fragment order: [wave][a][b][lane][4]
-    float* dst = ws + (((int64_t)s * 9 + k) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
-#pragma unroll
-    for (int a = 0; a < FM; ++a)
-#pragma unroll
-        for (int b = 0; b < FN; ++b)
-            *(f32x4*)(dst + (((wave * FM + a) * FN + b) * 64 + lane) * 4) = acc[a][b];
-    if (do_bias && tid < BN && co0 + tid < c_out) ws_bias[(int64_t)s * c_out + co0 + tid] = bsum;
 }
 
 // The reduction of the partials; with a job (oj.gi != NULL) its workgroups
@@ -1198,7 +1269,7 @@ static void launch_gg(const void* src, const int32_t* nbr, const void* w, const 
 }
 
 // Compute units of the current device (cached per device).
-static int cu_count() {
+int cu_count() {
     static int cached[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -1384,7 +1455,8 @@ static void launch_big(const BwPlan& p, const void* go, const void* x, const int
     constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
     const int nci = (int)cdiv(c_in, BM), nco = (int)cdiv(c_out, BN);
     const int64_t blocks = (int64_t)9 * nci * nco * p.splits;
-    hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks), dim3(64 * WGM * WGN),
+    hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks),
+                       dim3(bw_big_threads(FM, FN, WGM, WGN)),
                        0, s, (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
                        p.rows_per_split, nci, nco, blocks);
 }

@@ -70,6 +70,8 @@ void pack_weight(const void* w, void* wf_fwd, void* wf_bwd, int c_in, int c_out,
 bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out);
 // Rows per split of the MFMA backward-weight (its row list lives in LDS).
 constexpr int kMaxSplitRows = 2048;
+// compute units of the current device (256 on MI355X)
+int cu_count();
 int bw_mfma_tile(int c);
 // (ci, co) tile edges of the MFMA backward-weight kernel chosen for a shape.
 void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn);
