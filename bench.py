@@ -179,6 +179,59 @@ def dense_ms(dev, dtype, reps):
     return best
 
 
+PRUNE_C = 768  # ViT-B token width, where the Block prune step runs
+
+
+def prune_bytes(b, n_key, n_prev, n_new, row_bytes):
+    """Algorithmic HBM bytes of one prune step (vit_sparse_adapter_poguise.py
+    :899-977): kept and key rows read and written once; keep_idx and last_idx
+    read and the new idx written (8 B each); the kept table rows read and
+    the new table written (36 B each); the old -> new mapping filled, scattered
+    and read once per table entry (4 B each)."""
+    rows = b * (n_key + n_new)
+    return (2 * rows * row_bytes + b * n_new * (8 + 8 + 8) + b * n_new * 36 * 2
+            + b * n_prev * 4 + b * n_new * 4 + b * n_new * 9 * 4)
+
+
+def prune_measure(dev, reps, cpu: bool):
+    """The fused prune step on config 2's ViT-B tokens: x [B, 1 + T*H*W, 768]
+    fp16, keep 0.55 of the patch tokens (sorted top-k), with the index
+    bookkeeping and the table remap. Timed with HIP events; the oracle's numpy
+    restatement of the reference step is timed on the host beside it."""
+    import numpy as np
+    import torch
+
+    import eccv26_tad_amd as sv
+
+    n = T * H * W
+    g = torch.Generator().manual_seed(SEED + 7)
+    k = math.ceil(0.55 * n)
+    idx = torch.topk(torch.rand(B, n, generator=g), k, dim=1).indices.sort(dim=1).values
+    x = torch.randn(B, 1 + n, PRUNE_C, generator=g).to(dev, torch.float16)
+    last = torch.arange(n, dtype=torch.long).repeat(B, 1).to(dev)
+    table = sv.get_initial_neighbor_indices(H, W, T, dev, B)
+    idx_d = idx.to(dev)
+    ms = time_events(lambda: sv.prune_tokens(x, idx_d, last, table, 1), reps)
+    by = prune_bytes(B, 1, n, k, PRUNE_C * 2)
+    out = {"workload": f"x [{B}, 1+{n}, {PRUNE_C}] fp16, keep 0.55, idx + table", "us": round(ms * 1e3, 2),
+           "gbs": round(by / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "bytes": by, "launches": 3}
+    if cpu:
+        from oracle import sv_oracle
+
+        xs, ids, ls, ts = x.cpu().numpy(), idx.numpy(), last.cpu().numpy(), table.cpu().numpy()
+        t0 = time.perf_counter()
+        reps_c = 0
+        while True:
+            sv_oracle.ref_prune_step(xs, ids, ls, ts, 1)
+            reps_c += 1
+            if time.perf_counter() - t0 > 2.0 or reps_c >= 20:
+                break
+        out["cpu_reference_us"] = round((time.perf_counter() - t0) / reps_c * 1e6, 1)
+        out["cpu_reference"] = "numpy restatement of the reference step (oracle.ref_prune_step), 1 thread"
+    return out
+
+
 def cpu_baseline(budget_s: float):
     """The OpenMP fp32 port of the reference dataflow (oracle/sv_oracle.c,
     svo_fwd_f32 / svo_bwd_in_f32 / svo_bwd_w_f32) on the host cores, on the
@@ -370,6 +423,7 @@ def main():
             log(f"bench: sweep {row}")
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    prune = None if args.no_sweep else prune_measure(dev, 20, not args.no_cpu)
 
     out = {
         "metric": "SparseConv2D fwd+bwd µs & HBM GB/s (% roofline), speedup vs dense @10-55% keep",
@@ -401,6 +455,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "prune_step": prune,
     }
     print(json.dumps(out), flush=True)
 

@@ -37,6 +37,7 @@ ops = opentad_sparse_ops
 from .neighbor import (  # noqa: E402
     build_neighbor_table,
     get_initial_neighbor_indices,
+    prune_tokens,
     remap_neighbor_table,
     transpose_neighbor_table,
     validate_neighbor_table,
@@ -54,7 +55,7 @@ LIB_PATH = os.path.join(_PKG, "libsvtad_sparse.so")
 __all__ = [
     "opentad_sparse_ops", "ops", "SparseConv2d", "SparseConv2dFunction",
     "SparseDepthwiseConv2d", "SparseDepthwiseConv2dFunction",
-    "build_neighbor_table", "get_initial_neighbor_indices", "remap_neighbor_table",
+    "build_neighbor_table", "get_initial_neighbor_indices", "prune_tokens", "remap_neighbor_table",
     "transpose_neighbor_table", "validate_neighbor_table", "remap_legacy_sparse_conv_weights",
     "LIB_PATH",
 ]

@@ -148,6 +148,52 @@ __global__ void k_remap_gather(const int32_t* __restrict__ table, const int64_t*
 }
 
 // ---------------------------------------------------------------------------
+// fused prune step (restates vit_sparse_adapter_poguise.py:899-977)
+// ---------------------------------------------------------------------------
+
+// One pass over the output rows of x, one wave per row: the n_key key rows of
+// each sample are copied, the kept token rows gathered
+// (x[:, n_key + keep[b, j]]), in chunks of type V (16 bytes when the row
+// allows it). For kept rows lane 0 also gathers last_idx (:908) and scatters
+// the old -> new global mapping (:930-951) that k_remap_gather then reads.
+// The row arithmetic is per wave (scalar), not per element. A keep index
+// outside [0, n_prev) yields a zero row, idx_out -1 and no mapping entry.
+// With x_out == NULL only the index work is done.
+template <typename V>
+__global__ __launch_bounds__(256) void k_prune_rows(const V* __restrict__ x, int64_t batch,
+                                                    int64_t n_key, int64_t n_prev, int64_t row_chunks,
+                                                    const int64_t* __restrict__ keep, int64_t n_new,
+                                                    const int64_t* __restrict__ last_idx,
+                                                    int32_t* __restrict__ mapping,
+                                                    V* __restrict__ x_out, int64_t* __restrict__ idx_out) {
+    const int64_t rows_out = n_key + n_new, rows_in = n_key + n_prev;
+    const int64_t total = batch * rows_out;
+    const int lane = threadIdx.x & 63;
+    const int64_t w0 = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for (int64_t r = w0; r < total; r += (int64_t)gridDim.x * 4) {
+        const int64_t b = r / rows_out, q = r - b * rows_out;
+        int64_t src = -1;
+        if (q < n_key) {
+            src = b * rows_in + q;
+        } else {
+            const int64_t j = q - n_key;
+            const int64_t kidx = keep[b * n_new + j];
+            const bool ok = kidx >= 0 && kidx < n_prev;
+            if (ok) src = b * rows_in + n_key + kidx;
+            if (lane == 0) {
+                if (idx_out) idx_out[b * n_new + j] = ok ? last_idx[b * n_prev + kidx] : -1;
+                if (mapping && ok) mapping[b * n_prev + kidx] = (int32_t)(b * n_new + j);
+            }
+        }
+        if (x_out) {
+            const V* sp = x + src * row_chunks;
+            V* dp = x_out + r * row_chunks;
+            for (int64_t c = lane; c < row_chunks; c += 64) dp[c] = src >= 0 ? sp[c] : V{};
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // transpose + validate
 // ---------------------------------------------------------------------------
 
@@ -252,6 +298,58 @@ extern "C" int svtad_remap_table(const int32_t* table, int64_t batch, int64_t n_
                        keep_idx, batch, n_prev, n_new, mapping_ws);
     hipLaunchKernelGGL(k_remap_gather, dim3(grid_for(batch * n_new * 9, 256)), dim3(256), 0, s,
                        table, keep_idx, batch, n_prev, n_new, (const int32_t*)mapping_ws, out);
+    return launch_status();
+}
+
+extern "C" int svtad_prune_step(const void* x, int64_t batch, int64_t n_key, int64_t n_prev,
+                                int64_t row_bytes, const int64_t* keep_idx, int64_t n_new,
+                                const int64_t* last_idx, const int32_t* table, int32_t* mapping_ws,
+                                void* x_out, int64_t* idx_out, int32_t* table_out, void* stream) {
+    if (batch < 0 || n_key < 0 || n_prev < 0 || n_new < 0 || n_new > n_prev || row_bytes < 0)
+        return set_error(SVTAD_ERR_INVALID, "prune_step: bad sizes");
+    if (batch * (n_key + n_prev) >= (int64_t)INT32_MAX)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "prune_step: more than 2^31-1 rows");
+    const int64_t rows_out = batch * (n_key + n_new);
+    if (batch * n_new == 0) {
+        // nothing kept: no index or table output (their buffers may be empty)
+        last_idx = nullptr, idx_out = nullptr, table = nullptr, table_out = nullptr;
+    } else if ((last_idx == nullptr) != (idx_out == nullptr) ||
+               (table == nullptr) != (table_out == nullptr) || (table && !mapping_ws)) {
+        return set_error(SVTAD_ERR_INVALID,
+                         "prune_step: last_idx/idx_out and table/table_out/mapping_ws go together");
+    }
+    if (rows_out == 0) return SVTAD_OK;
+    if (!keep_idx || (row_bytes > 0 && (!x || !x_out)))
+        return set_error(SVTAD_ERR_INVALID, "prune_step: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    if (table)
+        hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(batch * n_prev, 256)), dim3(256), 0, s, mapping_ws,
+                           batch * n_prev, -1);
+    // widest chunk that divides the row and both base addresses
+    const uintptr_t al = (uintptr_t)x | (uintptr_t)x_out | (uintptr_t)row_bytes;
+    const int64_t work_rows = row_bytes > 0 ? rows_out : 0;
+    int32_t* map = table ? mapping_ws : nullptr;
+    const unsigned g = grid_for(cdiv(rows_out, (int64_t)4), 1);
+    if (work_rows == 0) {
+        // no row bytes: only the index bookkeeping and the mapping
+        hipLaunchKernelGGL((k_prune_rows<uint8_t>), dim3(g), dim3(256), 0, s, (const uint8_t*)nullptr,
+                           batch, n_key, n_prev, (int64_t)0, keep_idx, n_new, last_idx, map,
+                           (uint8_t*)nullptr, idx_out);
+    } else if ((al & 15) == 0) {
+        hipLaunchKernelGGL((k_prune_rows<uint4>), dim3(g), dim3(256), 0, s, (const uint4*)x, batch, n_key,
+                           n_prev, row_bytes / 16, keep_idx, n_new, last_idx, map, (uint4*)x_out, idx_out);
+    } else if ((al & 3) == 0) {
+        hipLaunchKernelGGL((k_prune_rows<uint32_t>), dim3(g), dim3(256), 0, s, (const uint32_t*)x, batch,
+                           n_key, n_prev, row_bytes / 4, keep_idx, n_new, last_idx, map,
+                           (uint32_t*)x_out, idx_out);
+    } else {
+        hipLaunchKernelGGL((k_prune_rows<uint8_t>), dim3(g), dim3(256), 0, s, (const uint8_t*)x, batch,
+                           n_key, n_prev, row_bytes, keep_idx, n_new, last_idx, map, (uint8_t*)x_out,
+                           idx_out);
+    }
+    if (table)
+        hipLaunchKernelGGL(k_remap_gather, dim3(grid_for(batch * n_new * 9, 256)), dim3(256), 0, s,
+                           table, keep_idx, batch, n_prev, n_new, (const int32_t*)mapping_ws, table_out);
     return launch_status();
 }
 

@@ -482,6 +482,61 @@ at::Tensor op_remap_neighbor_table(const at::Tensor& table_in, const at::Tensor&
     return out;
 }
 
+// prune_tokens(x [B, n_key + N_prev, ...], keep_idx [B, N_new] int64, last_idx [B, N_prev]
+// int64 or empty, table [B, N_prev, 9] int32 or empty, n_key)
+//   -> (x_out [B, n_key + N_new, ...], idx_out [B, N_new] or empty, table_out [B, N_new, 9] or empty)
+std::tuple<at::Tensor, at::Tensor, at::Tensor> op_prune_tokens(const at::Tensor& x_in,
+                                                               const at::Tensor& keep_in,
+                                                               const at::Tensor& last_in,
+                                                               const at::Tensor& table_in,
+                                                               int64_t n_key) {
+    check_gpu(x_in, "x");
+    check_gpu(keep_in, "keep_idx");
+    TORCH_CHECK(x_in.dim() >= 2, "x must be [B, n_key + N_prev, ...]");
+    TORCH_CHECK(keep_in.dim() == 2 && keep_in.size(0) == x_in.size(0), "keep_idx must be [B, N_new]");
+    const int64_t B = x_in.size(0);
+    TORCH_CHECK(n_key >= 0 && n_key <= x_in.size(1), "num_key_tokens out of range");
+    const int64_t n_prev = x_in.size(1) - n_key, n_new = keep_in.size(1);
+    TORCH_CHECK(n_new <= n_prev, "keep_idx keeps more tokens than there are");
+    at::Tensor x = x_in.contiguous();
+    at::Tensor keep = keep_in.to(at::kLong).contiguous();
+    const bool with_idx = last_in.defined() && last_in.numel() > 0;
+    const bool with_table = table_in.defined() && table_in.numel() > 0;
+    at::Tensor last, table;
+    if (with_idx) {
+        check_gpu(last_in, "last_idx");
+        TORCH_CHECK(last_in.dim() == 2 && last_in.size(0) == B && last_in.size(1) == n_prev,
+                    "last_idx must be [B, N_prev]");
+        last = last_in.to(at::kLong).contiguous();
+    }
+    if (with_table) {
+        check_gpu(table_in, "neighbor_indices");
+        TORCH_CHECK(table_in.dim() == 3 && table_in.size(0) == B && table_in.size(1) == n_prev &&
+                        table_in.size(2) == 9,
+                    "neighbor_indices must be [B, N_prev, 9]");
+        TORCH_CHECK(table_in.scalar_type() == at::kInt, "neighbor_indices must be int32");
+        table = table_in.contiguous();
+    }
+    c10::DeviceGuard g(x.device());
+    std::vector<int64_t> shape = x.sizes().vec();
+    shape[1] = n_key + n_new;
+    at::Tensor x_out = at::empty(shape, x.options());
+    const int64_t rows_in = B * x.size(1);
+    const int64_t row_bytes = rows_in > 0 ? x.numel() / rows_in * (int64_t)x.element_size() : 0;
+    at::Tensor idx_out = with_idx ? at::empty({B, n_new}, last.options()) : at::empty({0}, keep.options());
+    at::Tensor table_out = with_table ? at::empty({B, n_new, 9}, table.options())
+                                      : at::empty({0}, keep.options().dtype(at::kInt));
+    at::Tensor mapping = with_table ? at::empty({B * n_prev}, table.options()) : at::Tensor();
+    check_status(svtad_prune_step(x.data_ptr(), B, n_key, n_prev, row_bytes, keep.data_ptr<int64_t>(),
+                                  n_new, with_idx ? last.data_ptr<int64_t>() : nullptr,
+                                  with_table ? table.data_ptr<int32_t>() : nullptr,
+                                  with_table ? mapping.data_ptr<int32_t>() : nullptr, x_out.data_ptr(),
+                                  with_idx ? idx_out.data_ptr<int64_t>() : nullptr,
+                                  with_table ? table_out.data_ptr<int32_t>() : nullptr, stream_of(x)),
+                 "prune_tokens");
+    return {x_out, idx_out, table_out};
+}
+
 // transpose_neighbor_table(table [N, 9], tokens_per_batch) -> (table_t [N, 9], collisions [1])
 std::tuple<at::Tensor, at::Tensor> op_transpose_neighbor_table(const at::Tensor& table_in,
                                                                int64_t tpb) {
@@ -559,6 +614,10 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("mask"));
     m.def("remap_neighbor_table", &op_remap_neighbor_table, "Neighbor table remap after a prune",
           py::arg("table"), py::arg("keep_idx"));
+    m.def("prune_tokens", &op_prune_tokens,
+          "Fused prune step: kept-token gather, index gather and table remap",
+          py::arg("x"), py::arg("keep_idx"), py::arg("last_idx"), py::arg("neighbor_indices"),
+          py::arg("num_key_tokens"));
     m.def("transpose_neighbor_table", &op_transpose_neighbor_table, "Transposed neighbor table",
           py::arg("table"), py::arg("tokens_per_batch") = 0);
     m.def("validate_neighbor_table", &op_validate_neighbor_table,

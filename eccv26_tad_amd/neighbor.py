@@ -49,6 +49,40 @@ def remap_neighbor_table(neighbor_indices: torch.Tensor, keep_idx: torch.Tensor)
     return out if dt == torch.int32 else out.to(dt)
 
 
+def prune_tokens(x: torch.Tensor, keep_idx: torch.Tensor, last_idx=None, neighbor_indices=None,
+                 num_key_tokens: int = 0):
+    """The Block prune step (vit_sparse_adapter_poguise.py:899-977) in two or
+    three launches.
+
+    ``x`` is ``[B, num_key_tokens + N_prev, C]``, where the first
+    ``num_key_tokens`` rows are kept as they are. ``keep_idx`` ``[B, N_new]``
+    holds local indices into the ``N_prev`` other rows, as from topk.
+
+    Returns ``(x_new, idx_new, neighbor_indices_new)``:
+    * ``x_new = cat(x[:, :S], gather(x[:, S:], keep_idx))``;
+    * ``idx_new = gather(last_idx, keep_idx)``, or None without ``last_idx``;
+    * the table remapped like ``remap_neighbor_table``, or None without
+      ``neighbor_indices``. Its dtype follows the input.
+    """
+    empty = torch.empty(0, dtype=torch.long, device=x.device)
+    tab = empty
+    dt = None
+    if neighbor_indices is not None:
+        dt = neighbor_indices.dtype
+        tab = neighbor_indices if dt == torch.int32 else neighbor_indices.to(torch.int32)
+    last = empty if last_idx is None else last_idx
+    x_new, idx_new, t_new = _ops.prune_tokens(x, keep_idx, last, tab, int(num_key_tokens))
+    if last_idx is None:
+        idx_new = None
+    elif idx_new.dtype != last_idx.dtype:
+        idx_new = idx_new.to(last_idx.dtype)
+    if neighbor_indices is None:
+        t_new = None
+    elif dt != torch.int32:
+        t_new = t_new.to(dt)
+    return x_new, idx_new, t_new
+
+
 def transpose_neighbor_table(table: torch.Tensor, tokens_per_batch: int = 0):
     """``(table_t, collisions)``: table_t[j,k] = i where src(i,k) = j. For
     mask-built tables table_t[:, k] == table[:, 8-k] and collisions == 0."""

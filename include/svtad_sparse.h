@@ -208,6 +208,29 @@ int svtad_remap_table(const int32_t* table, int64_t batch, int64_t n_prev, const
                       int64_t n_new, int32_t* mapping_ws, int32_t* out, void* stream);
 
 /*
+ * Fused prune step of a Block (poguise.py:899-977; internvideo_next.py:1447-1492
+ * for the table part), replacing the reference's gather / cat / gather /
+ * fill / scatter / where sequence:
+ *   x_out[b, :n_key]          = x[b, :n_key]                      (key tokens)
+ *   x_out[b, n_key + j]       = x[b, n_key + keep_idx[b, j]]      (:901-910)
+ *   idx_out[b, j]             = last_idx[b, keep_idx[b, j]]       (:908)
+ *   table_out                 = svtad_remap_table(table, keep_idx) (:913-977)
+ * x is [batch, n_key + n_prev] rows of row_bytes bytes (any element type),
+ * x_out [batch, n_key + n_new] rows. last_idx / idx_out are int64 [batch,
+ * n_prev] / [batch, n_new] and may both be NULL; table / table_out /
+ * mapping_ws (batch*n_prev int32) may all be NULL (no table update, as when
+ * the reference's neighbor_indices is None). With batch * n_new == 0 only the
+ * key rows are written and the index / table pointers are ignored. A keep
+ * index outside
+ * [0, n_prev) gives a zero row, idx -1 and no mapping entry (the reference's
+ * gather would raise). Two or three launches on `stream`.
+ */
+int svtad_prune_step(const void* x, int64_t batch, int64_t n_key, int64_t n_prev, int64_t row_bytes,
+                     const int64_t* keep_idx, int64_t n_new, const int64_t* last_idx,
+                     const int32_t* table, int32_t* mapping_ws, void* x_out, int64_t* idx_out,
+                     int32_t* table_out, void* stream);
+
+/*
  * Transposed table: table_t[j,k] = i for the entry with src(i,k) = j
  * (global indices), -1 where no entry maps there. When several entries map to
  * the same (j,k) one of them is kept and *collisions (device int32, caller

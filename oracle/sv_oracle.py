@@ -14,7 +14,8 @@ Two layers:
   pin the C closed form:
   ``ref_initial_table`` restates ``get_initial_neighbor_indices``
   (opentad/models/backbones/vit_sparse_adapter_poguise.py:1623-1670), and
-  ``ref_remap`` restates the Block remap (same file, :913-977).
+  ``ref_remap`` restates the Block remap (same file, :913-977), and
+  ``ref_prune_step`` the whole prune step around it (:899-977).
 
 Parity status: every function here is pinned by a check in
 ``tests/test_oracle.py`` that is independent of the function's own formula
@@ -153,6 +154,23 @@ def ref_remap(table: np.ndarray, keep_idx: np.ndarray) -> np.ndarray:
     valid = flat != -1
     new_flat = np.where(valid, mapping[np.clip(flat, 0, None)], np.int32(-1))
     return new_flat.reshape(B, n_new, 9).astype(np.int32)
+
+
+def ref_prune_step(x: np.ndarray, keep_idx: np.ndarray, last_idx, table, n_key: int):
+    """numpy restatement of the Block prune step (vit_sparse_adapter_poguise.py:899-977):
+    ``x`` [B, n_key + N_prev, C] -> cat(x[:, :n_key], gather(x[:, n_key:], keep_idx));
+    ``last_idx`` [B, N_prev] -> gather(last_idx, keep_idx) (:908); ``table``
+    [B, N_prev, 9] -> the remapped table (:913-977, ``ref_remap``). ``last_idx``
+    and ``table`` may be None (the reference skips the table when it is None, :913)."""
+    x = np.asarray(x)
+    keep_idx = np.asarray(keep_idx, dtype=np.int64)
+    x_key = x[:, :n_key]
+    x_nonkey = x[:, n_key:]
+    kept = np.take_along_axis(x_nonkey, keep_idx[:, :, None], axis=1)
+    x_new = np.concatenate([x_key, kept], axis=1)
+    idx_new = None if last_idx is None else np.take_along_axis(np.asarray(last_idx, dtype=np.int64), keep_idx, axis=1)
+    t_new = None if table is None else ref_remap(table, keep_idx)
+    return x_new, idx_new, t_new
 
 
 def ref_topk_sorted(score: np.ndarray, keep: int) -> np.ndarray:

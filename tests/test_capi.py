@@ -105,6 +105,27 @@ def test_workspace_too_small_rejected(lib):
     assert st == -2 and b"workspace" in lib.svtad_last_error()
 
 
+def test_prune_step_arguments_checked_on_host(lib):
+    # last_idx without idx_out, and a table without its mapping workspace
+    buf = ctypes.create_string_buffer(64)
+    st = lib.svtad_prune_step(buf, I64(1), I64(0), I64(4), I64(16), buf, I64(2), buf, None, None,
+                              buf, None, None, None)
+    assert st == -1 and b"go together" in lib.svtad_last_error()
+    st = lib.svtad_prune_step(buf, I64(1), I64(0), I64(4), I64(16), buf, I64(2), None, buf, None,
+                              buf, None, buf, None)
+    assert st == -1 and b"go together" in lib.svtad_last_error()
+    # nothing kept: the index / table pointers are not needed
+    assert lib.svtad_prune_step(None, I64(1), I64(0), I64(4), I64(0), buf, I64(0), buf, None, None,
+                                None, None, None, None) == 0
+    # more kept than present
+    st = lib.svtad_prune_step(buf, I64(1), I64(0), I64(2), I64(16), buf, I64(3), None, None, None,
+                              buf, None, None, None)
+    assert st == -1 and b"bad sizes" in lib.svtad_last_error()
+    # nothing to do
+    assert lib.svtad_prune_step(None, I64(0), I64(0), I64(0), I64(16), None, I64(0), None, None,
+                                None, None, None, None, None) == 0
+
+
 def test_table_limits_rejected(lib):
     st = lib.svtad_table_scan(ctypes.create_string_buffer(8), I64(1), 200, 200,
                               ctypes.create_string_buffer(8), None)
@@ -119,7 +140,7 @@ def test_extension_module_api():
         assert hasattr(ops, name)
     for name in ("fwd_bias", "bwd_w_bias", "dw_fwd", "dw_bwd_in", "dw_bwd_w",
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
-                 "validate_neighbor_table"):
+                 "validate_neighbor_table", "prune_tokens", "bwd_packed"):
         assert hasattr(ops, name)
     import torch
 

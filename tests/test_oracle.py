@@ -225,3 +225,30 @@ def test_planted_table_mistakes_are_caught(oracle):
     # a bwd_in that gathers with W[k] instead of W[8-k] (symmetric-table shortcut done wrong)
     gi_wrong = oracle.bwd_in(go, t[:, ::-1].copy(), w)
     assert not np.allclose(gi_wrong, gi_ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_prune_step_equals_row_loop_and_closed_form(oracle, seed):
+    """ref_prune_step against a plain per-row loop (x rows, index bookkeeping)
+    and, for its table, against the closed form of the pruned mask."""
+    rng = np.random.default_rng(seed)
+    B, T, H, W, S, C = 2, 2, 5, 4, 1, 3
+    n = T * H * W
+    table = oracle.ref_initial_table(H, W, T, B)
+    x = rng.standard_normal((B, S + n, C)).astype(np.float32)
+    last = np.stack([rng.permutation(1000)[:n] for _ in range(B)]).astype(np.int64)
+    k = int(np.ceil(0.6 * n))
+    idx = oracle.ref_topk_sorted(rng.random((B, n)), k)
+    x_new, idx_new, t_new = oracle.ref_prune_step(x, idx, last, table, S)
+    for b in range(B):
+        np.testing.assert_array_equal(x_new[b, :S], x[b, :S])
+        for j in range(k):
+            np.testing.assert_array_equal(x_new[b, S + j], x[b, S + idx[b, j]])
+            assert idx_new[b, j] == last[b, idx[b, j]]
+    mask = np.zeros((B, n), np.uint8)
+    np.put_along_axis(mask, idx, 1, axis=1)
+    np.testing.assert_array_equal(t_new.reshape(-1, 9), oracle.build_table(mask.reshape(B, T, H, W)))
+    # without the optional parts
+    x2, i2, t2 = oracle.ref_prune_step(x, idx, None, None, S)
+    np.testing.assert_array_equal(x2, x_new)
+    assert i2 is None and t2 is None
