@@ -943,63 +943,78 @@ __device__ __forceinline__ void transpose8(const u32x4* in, u32x4* out) {
 }
 
 // gw[k][ci][co] = T(sum_s part[s]...) for the fragment-ordered partials of
-// k_bw_big (quadruple e: 4 consecutive floats of one lane), splits summed in
-// order; and gb[co] = T(sum_s part_b[s][co]) for "quadruple" quads + co.
+// k_bw_big (quadruple e: 4 consecutive floats of one lane). Four threads
+// (one per wave of the workgroup) share a quadruple: thread g sums its
+// quarter of the splits with all its loads in flight, and the quarters are
+// added in order g = 0..3 through LDS, so the order of the sum is fixed.
 template <typename T>
-__device__ __forceinline__ void bw_reduce_one(int64_t e, const float* __restrict__ part,
-                                              const float* __restrict__ part_b, int splits,
-                                              int c_in, int c_out, int fm, int fn, int wgm, int wgn,
-                                              int n_ci_tiles, int n_co_tiles, T* __restrict__ gw,
-                                              T* __restrict__ gb) {
+__device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __restrict__ part,
+                                                int splits, int c_in, int c_out, int fm, int fn,
+                                                int wgm, int wgn, int n_ci_tiles, int n_co_tiles,
+                                                T* __restrict__ gw) {
+    __shared__ f32x4 qsum[4][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int bm = wgm * fm * 16, bn = wgn * fn * 16;
     const int64_t per_split = (int64_t)9 * c_in * c_out;
     const int64_t quads = per_split / 4;
+    const int64_t e = blk * 64 + lane;
+    const int spt = (splits + 3) / 4;
+    const int s0 = g * spt, s1 = min(splits, s0 + spt);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (e < quads) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        // eight loads in flight at a time, summed in split order
         const float* pe = part + e * 4;
-        int q = 0;
-        for (; q + 8 <= splits; q += 8) {
+        for (int q = s0; q < s1; q += 8) {
             f32x4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = *(const f32x4*)(pe + (int64_t)(q + u) * per_split);
+            for (int u = 0; u < 8; ++u)
+                v[u] = q + u < s1 ? *(const f32x4*)(pe + (int64_t)(q + u) * per_split) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < 8; ++u) acc += v[u];
         }
-        for (; q < splits; ++q) acc += *(const f32x4*)(pe + (int64_t)q * per_split);
-        // decode the fragment-order position
-        int64_t rest = e * 4;
-        const int64_t tile_sz = (int64_t)bm * bn;
-        const int64_t tile = rest / tile_sz;
-        rest -= tile * tile_sz;
-        const int k = (int)(tile / (n_ci_tiles * n_co_tiles));
-        const int tr = (int)(tile - (int64_t)k * n_ci_tiles * n_co_tiles);
-        const int ci0 = (tr / n_co_tiles) * bm, co0 = (tr % n_co_tiles) * bn;
-        const int lane = (int)((rest >> 2) & 63);
-        int fr = (int)(rest >> 8);  // (wave * fm + a) * fn + b
-        const int b = fr % fn;
-        fr /= fn;
-        const int a = fr % fm;
-        const int wave = fr / fm;
-        const int ci = ci0 + (wave / wgn) * fm * 16 + a * 16 + (lane >> 4) * 4;
-        const int co = co0 + (wave % wgn) * fn * 16 + b * 16 + (lane & 15);
-        T* g = gw + ((int64_t)k * c_in + ci) * c_out + co;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) g[(int64_t)j * c_out] = (T)acc[j];
-    } else if (gb && e - quads < c_out) {
-        const int c = (int)(e - quads);
-        float v = 0.f;
-        int q = 0;
-        for (; q + 8 <= splits; q += 8) {
-            float t[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) t[u] = part_b[(int64_t)(q + u) * c_out + c];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v += t[u];
-        }
-        for (; q < splits; ++q) v += part_b[(int64_t)q * c_out + c];
-        gb[c] = (T)v;
     }
+    qsum[g][lane] = acc;
+    __syncthreads();
+    if (g != 0 || e >= quads) return;
+    acc = qsum[0][lane] + qsum[1][lane];
+    acc += qsum[2][lane];
+    acc += qsum[3][lane];
+    // decode the fragment-order position
+    int64_t rest = e * 4;
+    const int64_t tile_sz = (int64_t)bm * bn;
+    const int64_t tile = rest / tile_sz;
+    rest -= tile * tile_sz;
+    const int k = (int)(tile / (n_ci_tiles * n_co_tiles));
+    const int tr = (int)(tile - (int64_t)k * n_ci_tiles * n_co_tiles);
+    const int ci0 = (tr / n_co_tiles) * bm, co0 = (tr % n_co_tiles) * bn;
+    const int ln = (int)((rest >> 2) & 63);
+    int fr = (int)(rest >> 8);  // (wave * fm + a) * fn + b
+    const int b = fr % fn;
+    fr /= fn;
+    const int a = fr % fm;
+    const int wave = fr / fm;
+    const int ci = ci0 + (wave / wgn) * fm * 16 + a * 16 + (ln >> 4) * 4;
+    const int co = co0 + (wave % wgn) * fn * 16 + b * 16 + (ln & 15);
+    T* gp = gw + ((int64_t)k * c_in + ci) * c_out + co;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gp[(int64_t)j * c_out] = (T)acc[j];
+}
+
+// gb[c] = T(sum_s part_b[s][c]), splits summed in order.
+template <typename T>
+__device__ __forceinline__ void bw_reduce_bias(int64_t c, const float* __restrict__ part_b,
+                                               int splits, int c_out, T* __restrict__ gb) {
+    if (c >= c_out) return;
+    float v = 0.f;
+    int q = 0;
+    for (; q + 8 <= splits; q += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t[u] = part_b[(int64_t)(q + u) * c_out + c];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v += t[u];
+    }
+    for (; q < splits; ++q) v += part_b[(int64_t)q * c_out + c];
+    gb[c] = (T)v;
 }
 
 // staging waves of k_bw_big: one 8-row x 8-channel block of x rows or of go
@@ -1220,8 +1235,13 @@ __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ par
                                                    int wgn, int n_ci_tiles, int n_co_tiles,
                                                    T* __restrict__ gw, T* __restrict__ gb,
                                                    OrphanJob oj) {
-    bw_reduce_one<T>((int64_t)blockIdx.x * 256 + threadIdx.x, part, part_b, splits, c_in, c_out, fm,
-                     fn, wgm, wgn, n_ci_tiles, n_co_tiles, gw, gb);
+    // workgroups [0, quad_blocks) reduce gw, the rest the bias
+    const int64_t quad_blocks = ((int64_t)9 * c_in * c_out / 4 + 63) / 64;
+    if ((int64_t)blockIdx.x < quad_blocks)
+        bw_reduce_quads<T>(blockIdx.x, part, splits, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles,
+                           n_co_tiles, gw);
+    else if (gb)
+        bw_reduce_bias<T>(((int64_t)blockIdx.x - quad_blocks) * 256 + threadIdx.x, part_b, splits, c_out, gb);
     if (!oj.gi || (oj.flag && *oj.flag == 0u)) return;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < oj.n * 9; e += (int64_t)gridDim.x * 256)
         orphan_entry<T, false>(e, (const T*)oj.go, oj.nbr, (const T*)oj.w, (T*)oj.gi, oj.n, oj.c_in,
@@ -1508,8 +1528,8 @@ bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const in
     BigCfg bc;
     if (big_cfg(c_in, c_out, &bc)) {
         const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
-        const int64_t threads = (int64_t)9 * c_in * c_out / 4 + (gb ? c_out : 0);
-        const dim3 grid((unsigned)cdiv(threads, 256));
+        const int64_t blocks = cdiv((int64_t)9 * c_in * c_out / 4, 64) + (gb ? cdiv(c_out, 256) : 0);
+        const dim3 grid((unsigned)blocks);
         const OrphanJob job = oj ? *oj : OrphanJob{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
         if (dtype == SVTAD_F16)
             hipLaunchKernelGGL((k_bw_reduce<f16>), grid, dim3(256), 0, s, (const float*)part,
