@@ -18,6 +18,8 @@
 // l%16 of A and column l%16 of B with 8 reduction values at slot l/16; it
 // receives C[(l/16)*4 + j][l%16], j = 0..3. A and B use the same slot
 // mapping, so the pairing of reduction values matches by construction.
+#include <type_traits>
+
 #include "sv_common.h"
 #include "sv_conv.h"
 
@@ -486,14 +488,28 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
 #pragma unroll
     for (int f = 0; f < FN; ++f)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = col0 + wave * FN * 16 + f * 16 + g * 4 + j;
-            bv[f][j] = 0.f;
-            if (MODE == MODE_FWD && set == 0 && col < n_out) {
-                if (bias_mode == SVTAD_BIAS_FP32) bv[f][j] = ((const float*)bias)[col];
-                else if (bias_mode != SVTAD_BIAS_NONE) bv[f][j] = (float)((const T*)bias)[col];
-            }
+        for (int j = 0; j < 4; ++j) bv[f][j] = 0.f;
+    if (MODE == MODE_FWD && set == 0 && bias_mode != SVTAD_BIAS_NONE) {  // uniform
+        // one straight-line loop per bias dtype
+        const int c0 = col0 + wave * FN * 16 + g * 4;
+        if (bias_mode == SVTAD_BIAS_FP32) {
+#pragma unroll
+            for (int f = 0; f < FN; ++f)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = c0 + f * 16 + j;
+                    bv[f][j] = col < n_out ? ((const float*)bias)[col] : 0.f;
+                }
+        } else {
+#pragma unroll
+            for (int f = 0; f < FN; ++f)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int col = c0 + f * 16 + j;
+                    bv[f][j] = col < n_out ? (float)((const T*)bias)[col] : 0.f;
+                }
         }
+    }
 
     // One offset's slice: this lane's fragment rows start at element offsets
     // off0[a] (even steps) / off1[a] (odd steps) of the LDS rows; the ring
@@ -612,7 +628,10 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     constexpr int OP = BN + 8;
     static_assert((size_t)BM * OP * 2 <= sizeof(Ab), "output tile must fit in LDS");
     u16* ot = &Ab[0][0];
-    if (set == 0) {
+    // one straight-line copy per bias mode (a mode test per element compiles
+    // to a branch per element, which cost more than the rest of the epilogue)
+    auto epilogue = [&](auto mode) {
+        constexpr int M = decltype(mode)::value;
 #pragma unroll
         for (int f = 0; f < FN; ++f) {
             const int lc = wave * FN * 16 + f * 16 + g * 4;
@@ -623,8 +642,8 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
                 for (int j = 0; j < 4; ++j) {
                     const float v = acc[a][f][j];
                     T o;
-                    if (bias_mode == SVTAD_BIAS_PRE || bias_mode == SVTAD_BIAS_FP32) o = (T)(v + bv[f][j]);
-                    else if (bias_mode == SVTAD_BIAS_AFTER) o = (T)((float)(T)v + bv[f][j]);
+                    if constexpr (M == 1) o = (T)(v + bv[f][j]);
+                    else if constexpr (M == 2) o = (T)((float)(T)v + bv[f][j]);
                     else o = (T)v;
                     h[j] = (unsigned)__builtin_bit_cast(u16, o);
                 }
@@ -632,6 +651,14 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
                 *(u32x2*)&ot[(a * 16 + arow) * OP + lc] = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
             }
         }
+    };
+    if (set == 0) {
+        if (bias_mode == SVTAD_BIAS_PRE || bias_mode == SVTAD_BIAS_FP32)
+            epilogue(std::integral_constant<int, 1>{});
+        else if (bias_mode == SVTAD_BIAS_AFTER)
+            epilogue(std::integral_constant<int, 2>{});
+        else
+            epilogue(std::integral_constant<int, 0>{});
     }
     __syncthreads();
     constexpr int CH = BN / 8;
