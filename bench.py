@@ -14,7 +14,8 @@ resident in HBM before the timed region.
 Printed: ONE JSON line on stdout. ``value`` is the algorithmic HBM throughput
 of fwd+bwd (GB/s) at the headline keep rate; ``sweep`` holds us / GB/s /
 TFLOP/s / speedup over a dense 3x3 conv (MIOpen, same shape) for every keep
-rate; ``roofline`` covers the dominant kernel, timed with HIP events on the
+rate, and over the reference adapter's dense path on the same kept tokens
+(scatter -> conv2d -> gather, fwd + bwd); ``roofline`` covers the dominant kernel, timed with HIP events on the
 stream it is launched on; ``cpu_baseline`` times the OpenMP fp32 port of the
 reference dataflow (oracle/, kind "port") on the host cores.
 """
@@ -177,6 +178,29 @@ def dense_ms(dev, dtype, reps):
         t = time_events(run, reps, warm=5)
         best = t if best is None else min(best, t)
     return best
+
+
+def dense_adapter_ms(prob, dev, dtype, reps):
+    """The reference adapter's dense ``2d_conv`` branch on the same kept tokens
+    (vit_sparse_adapter_poguise.py:372-412,484-490: scatter into the zero grid,
+    NCHW conv2d, gather), forward + input / weight / bias gradients: the
+    speedup denominator as the paper's model would run it."""
+    import torch
+
+    import eccv26_tad_amd as sv
+
+    torch.backends.cudnn.benchmark = True
+    n_kept = prob.n // B
+    idx = torch.nonzero(prob.mask.view(B, -1))[:, 1].view(B, n_kept)
+    x = prob.x.view(B, n_kept, C).detach().clone().requires_grad_(True)
+    go = prob.go.view(B, n_kept, C)
+    conv = torch.nn.Conv2d(C, C, 3, padding=1).to(dev, dtype)
+
+    def run():
+        y = sv.dense_conv_tokens(x, idx, T * H * W, H, W, conv)
+        return torch.autograd.grad(y, (x, conv.weight, conv.bias), go)
+
+    return time_events(run, reps, warm=5)
 
 
 PRUNE_C = 768  # ViT-B token width, where the Block prune step runs
@@ -417,6 +441,9 @@ def main():
                                               fu / (MFMA_PEAK_TFLOPS[dname] * 1e12)) / (t * 1e-3), 4)}
             if dense is not None:
                 row["speedup_vs_dense"] = round(dense / t, 3)
+                da = dense_adapter_ms(p, dev, dtype, 20)
+                row["dense_adapter_us"] = round(da * 1e3, 2)
+                row["speedup_vs_dense_adapter"] = round(da / t, 3)
             sweep.append(row)
             if p is not prob:
                 del p

@@ -42,6 +42,12 @@ from .neighbor import (  # noqa: E402
     transpose_neighbor_table,
     validate_neighbor_table,
 )
+from .dense_path import (  # noqa: E402
+    conv2d_weight_from_sparse,
+    dense_conv_tokens,
+    keep_mask_from_indices,
+    sparse_weight_from_conv2d,
+)
 from .sparse_conv_layer import (  # noqa: E402
     SparseConv2d,
     SparseConv2dFunction,
@@ -57,5 +63,6 @@ __all__ = [
     "SparseDepthwiseConv2d", "SparseDepthwiseConv2dFunction",
     "build_neighbor_table", "get_initial_neighbor_indices", "prune_tokens", "remap_neighbor_table",
     "transpose_neighbor_table", "validate_neighbor_table", "remap_legacy_sparse_conv_weights",
-    "LIB_PATH",
+    "dense_conv_tokens", "keep_mask_from_indices", "sparse_weight_from_conv2d",
+    "conv2d_weight_from_sparse", "LIB_PATH",
 ]
