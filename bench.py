@@ -203,6 +203,57 @@ def dense_adapter_ms(prob, dev, dtype, reps):
     return time_events(run, reps, warm=5)
 
 
+def adapter_measure(dev, reps):
+    """SparseConvAdapter (fused GEMM epilogues, no host sync) against the
+    unfused chain of the reference adapter (vit_sparse_adapter_poguise.py:
+    305-362,652-653, with the .max() heuristic) at the ViT-B adapter shape:
+    B2 x (1 CLS + kept tokens of T80 x 14x14 at 55 % keep) x 768, hidden 256
+    (the reference rounds 768 / 4 up to a power of two), float16. Forward
+    alone and forward + backward (input and all parameter gradients)."""
+    import torch
+
+    import eccv26_tad_amd as sv
+
+    dtype = torch.float16
+    mask = make_mask(0.55).to(dev)
+    table = sv.build_neighbor_table(mask)
+    n_kept = table.shape[0] // B
+    table = table.view(B, n_kept, 9)
+    idx = torch.nonzero(mask.view(B, -1))[:, 1].view(B, n_kept)
+    g = torch.Generator().manual_seed(SEED + 5)
+    mod = sv.SparseConvAdapter(768, 0.25)
+    with torch.no_grad():
+        mod.up_proj.weight.copy_(torch.randn(mod.up_proj.weight.shape, generator=g) * 0.02)
+    mod = mod.to(dev, dtype)
+    x = torch.randn(B, 1 + n_kept, 768, generator=g).to(dev, dtype).requires_grad_(True)
+    go = torch.randn(B, 1 + n_kept, 768, generator=g).to(dev, dtype)
+    params = [x] + list(mod.parameters())
+    args = (H, W, idx, T * H * W, table)
+
+    def fwd_fused():
+        with torch.no_grad():
+            return mod(x, *args)
+
+    def fwd_unfused():
+        with torch.no_grad():
+            return mod.reference_forward(x, *args)
+
+    def step_fused():
+        return torch.autograd.grad(mod(x, *args), params, go)
+
+    def step_unfused():
+        return torch.autograd.grad(mod.reference_forward(x, *args), params, go)
+
+    t = {name: time_events(fn, reps, warm=5) for name, fn in
+         (("fwd", fwd_fused), ("fwd_unfused", fwd_unfused), ("step", step_fused), ("step_unfused", step_unfused))}
+    out = {"workload": f"x [{B}, 1+{n_kept}, 768] fp16, hidden {mod.hidden_dims}, keep 0.55"}
+    for k, v in t.items():
+        out[k + "_us"] = round(v * 1e3, 2)
+    out["fwd_speedup"] = round(t["fwd_unfused"] / t["fwd"], 3)
+    out["step_speedup"] = round(t["step_unfused"] / t["step"], 3)
+    return out
+
+
 PRUNE_C = 768  # ViT-B token width, where the Block prune step runs
 
 
@@ -451,6 +502,9 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     prune = None if args.no_sweep else prune_measure(dev, 20, not args.no_cpu)
+    adapter = None if args.no_sweep else adapter_measure(dev, 20)
+    if adapter is not None:
+        log(f"bench: adapter {adapter}")
 
     out = {
         "metric": "SparseConv2D fwd+bwd µs & HBM GB/s (% roofline), speedup vs dense @10-55% keep",
@@ -483,6 +537,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "prune_step": prune,
+        "adapter": adapter,
     }
     print(json.dumps(out), flush=True)
 

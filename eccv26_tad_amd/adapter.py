@@ -1,0 +1,183 @@
+"""The sparse-conv adapter with fused GEMM epilogues.
+
+Reference: the ``conv_type == "sparse_conv"`` adapter of
+``opentad/models/backbones/vit_sparse_adapter_poguise.py`` (constructor
+``:95-111,163-166``, forward ``:290-362`` and ``:652-653``), without the
+optional heatmap injection (``:316-355``) and attention branch, which this
+module does not implement (it raises when asked for them):
+
+    x_proj = GELU(down_proj(x))                      # [B, N, hidden]
+    special, patches = x_proj[:, :S], x_proj[:, S:]  # S = N - indices.shape[1]
+    processed = sparse_conv(patches, neighbor_indices)
+    y = up_proj(cat(special, processed)) * gamma + x
+
+The forward runs in three launches (``opentad_sparse_ops.adapter_down``, the
+SparseConv2D forward, ``opentad_sparse_ops.adapter_up``):
+
+* the down GEMM's epilogue adds the bias, rounds the Linear output, applies
+  GELU and writes the special tokens and the (contiguous) SparseConv2D input
+  directly: no GELU pass and no slice copy;
+* the up GEMM reads the special tokens and the SparseConv2D output in place of
+  the concatenation and applies bias, ``gamma`` and the residual before its
+  single store: no cat, no scale pass, no add pass;
+* ``tokens_per_batch`` defaults to 0 (the tables the backbone builds are
+  global), so there is no host sync; ``None`` restores the reference's
+  ``max()`` heuristic (``sparse_conv_layer.py:174-177``).
+
+The backward runs on library GEMMs (``torch.matmul``) and PyTorch's own GELU
+backward. ``gamma``'s gradient needs ``z = cat(...) W_u^T + b_u``, which the
+fused forward never stores: ``sum(go * z) = <W_u, go^T c> + <b_u, sum(go)>``,
+and ``go^T c`` is the up-projection's weight-gradient GEMM anyway.
+
+The fused path takes float16 / bfloat16 (the matrix-core dtypes) and raises
+otherwise; ``reference_forward`` runs the unfused chain in the reference's op
+order (for tests and the benchmark).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+from torch.autograd import Function
+
+from . import opentad_sparse_ops as _ops
+from .sparse_conv_layer import SparseConv2d
+
+_FUSED_DTYPES = (torch.float16, torch.bfloat16)
+
+
+class AdapterDownFunction(Function):
+    """``(act_special, act_patch) = split(GELU(x W^T + b))``; x ``[B, N, k]``."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, n_special):
+        pre, sp, pa = _ops.adapter_down(x, weight, bias, int(n_special))
+        ctx.save_for_backward(x, weight, pre)
+        ctx.has_bias = bias is not None
+        ctx.n_special = int(n_special)
+        return sp, pa
+
+    @staticmethod
+    def backward(ctx, g_sp, g_pa):
+        x, weight, pre = ctx.saved_tensors
+        B, N, n = pre.shape
+        S = ctx.n_special
+        dg = torch.empty_like(pre)
+        if g_sp is None:
+            dg[:, :S].zero_()
+        else:
+            dg[:, :S] = g_sp
+        if g_pa is None:
+            dg[:, S:].zero_()
+        else:
+            dg[:, S:] = g_pa.reshape(B, N - S, n)
+        du = torch.ops.aten.gelu_backward(dg, pre)
+        du2 = du.reshape(-1, n)
+        gx = torch.matmul(du, weight) if ctx.needs_input_grad[0] else None
+        gw = torch.matmul(du2.t(), x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
+        gb = du2.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return gx, gw, gb, None
+
+
+class AdapterUpFunction(Function):
+    """``out = T(z * gamma) + residual``, ``z = cat(a_special, a_patch) W^T + b``."""
+
+    @staticmethod
+    def forward(ctx, a_special, a_patch, weight, bias, gamma, residual):
+        out = _ops.adapter_up(a_special, a_patch, weight, bias, gamma, residual)
+        ctx.save_for_backward(a_special, a_patch, weight, bias, gamma)
+        return out
+
+    @staticmethod
+    def backward(ctx, go):
+        a_sp, a_pa, weight, bias, gamma = ctx.saved_tensors
+        B, N, n = go.shape
+        S = a_sp.shape[1]
+        k = weight.shape[1]
+        go = go.contiguous()
+        go_sp = go[:, :S].reshape(-1, n)
+        go_pa = go[:, S:].reshape(-1, n)
+        # go^T c without building c = cat(a_special, a_patch)
+        G = torch.matmul(go_pa.t(), a_pa)
+        if S > 0:
+            G = G + torch.matmul(go_sp.t(), a_sp.reshape(-1, k))
+        gsum = go.reshape(-1, n).sum(0)
+        g_gamma = None
+        if ctx.needs_input_grad[4]:
+            s = (weight.float() * G.float()).sum()
+            if bias is not None:
+                s = s + (bias.float() * gsum.float()).sum()
+            g_gamma = s.reshape(1).to(gamma.dtype)
+        dz = go * gamma
+        g_sp = g_pa = None
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+            dc = torch.matmul(dz, weight)  # [B, N, k]
+            g_sp = dc[:, :S] if ctx.needs_input_grad[0] else None
+            g_pa = dc[:, S:].reshape(-1, k) if ctx.needs_input_grad[1] else None
+        gw = G * gamma if ctx.needs_input_grad[2] else None
+        gb = gsum * gamma if bias is not None and ctx.needs_input_grad[3] else None
+        return g_sp, g_pa, gw, gb, g_gamma, go
+
+
+class SparseConvAdapter(nn.Module):
+    """The reference adapter with ``conv_type="sparse_conv"``, ``use_attn=0``
+    and no heatmap injection, on fused HIP GEMM epilogues."""
+
+    def __init__(self, embed_dims: int, mlp_ratio: float = 0.25, n_key_tokens: int = 1,
+                 heatmap_grid_size=None):
+        super().__init__()
+        if n_key_tokens > 1 and heatmap_grid_size is not None:
+            raise NotImplementedError("SparseConvAdapter: heatmap injection is not implemented")
+        self.embed_dims = embed_dims
+        hidden = int(embed_dims * mlp_ratio)
+        hidden = int(2 ** round(math.log2(hidden)))  # power of two, as the reference rounds
+        self.hidden_dims = hidden
+        self.down_proj = nn.Linear(embed_dims, hidden)
+        nn.init.trunc_normal_(self.down_proj.weight, std=0.02)
+        nn.init.zeros_(self.down_proj.bias)
+        self.act = nn.GELU()
+        self.up_proj = nn.Linear(hidden, embed_dims)
+        nn.init.zeros_(self.up_proj.weight)
+        nn.init.zeros_(self.up_proj.bias)
+        self.gamma = nn.Parameter(torch.ones(1))
+        self.sparse_conv = SparseConv2d(hidden, hidden)
+
+    @staticmethod
+    def _n_special(x, indices):
+        return x.shape[1] - indices.shape[1]
+
+    def forward(self, x, h, w, indices, total_num_patches, neighbor_indices=None, tokens_per_batch=0):
+        """``x [B, N, embed]``; ``indices [B, N_kept]``; ``neighbor_indices``
+        ``[B, N_kept, 9]`` or ``[B * N_kept, 9]``. ``h``, ``w`` and
+        ``total_num_patches`` are accepted for signature compatibility."""
+        if x.dtype not in _FUSED_DTYPES or not x.is_cuda:
+            raise RuntimeError(f"SparseConvAdapter: the fused path takes float16 / bfloat16 GPU "
+                               f"tensors, got {x.dtype} on {x.device}")
+        if self.down_proj.weight.dtype != x.dtype:
+            raise RuntimeError("SparseConvAdapter: convert the module to the input dtype first")
+        S = self._n_special(x, indices)
+        if indices.shape[1] == 0:
+            return self.reference_forward(x, h, w, indices, total_num_patches, neighbor_indices)
+        sp, pa = AdapterDownFunction.apply(x, self.down_proj.weight, self.down_proj.bias, S)
+        nbr = neighbor_indices.reshape(-1, 9)
+        if tokens_per_batch is None:
+            tokens_per_batch = indices.shape[1] if int(nbr.max()) < indices.shape[1] else 0
+        processed = self.sparse_conv(pa, nbr, tokens_per_batch=tokens_per_batch)
+        return AdapterUpFunction.apply(sp, processed, self.up_proj.weight, self.up_proj.bias,
+                                       self.gamma, x)
+
+    def reference_forward(self, x, h, w, indices, total_num_patches, neighbor_indices=None):
+        """The unfused chain in the reference's op order
+        (vit_sparse_adapter_poguise.py:305-362,652-653), including its
+        ``.max()`` heuristic inside SparseConv2d."""
+        inputs = x
+        x_proj = self.act(self.down_proj(x))
+        S = self._n_special(x, indices)
+        special = x_proj[:, :S, :]
+        patches = x_proj[:, S:, :]
+        if patches.shape[1] == 0:
+            # the reference applies the activation a second time here (:356-358)
+            return self.up_proj(self.act(x_proj)) * self.gamma + inputs
+        processed = self.sparse_conv(patches, neighbor_indices)
+        return self.up_proj(torch.cat([special, processed], dim=1)) * self.gamma + inputs

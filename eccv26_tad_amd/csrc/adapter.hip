@@ -1,0 +1,324 @@
+// Dense GEMMs of the sparse-conv adapter with fused epilogues (gfx950 MFMA).
+//
+// The adapter around SparseConv2D (reference
+// opentad/models/backbones/vit_sparse_adapter_poguise.py:305-362,652-653) is
+//   u = x W_d^T + b_d,  g = GELU(u)      (down_proj, act)
+//   split g into special tokens and patch tokens; patches -> SparseConv2D
+//   c = cat(special, conv(patches))
+//   y = (c W_u^T + b_u) * gamma + x      (up_proj, gamma, residual)
+// Both GEMMs read their operands with the reduction index contiguous (token
+// rows and nn.Linear's (out, in) weight rows), so the LDS tiles need no
+// transposes. The epilogues remove the activation round trips of the
+// unfused chain:
+//  * down: bias, the rounding of the Linear output, GELU, and the split: u is
+//    written (autograd keeps it for the GELU backward) and GELU(u) goes
+//    straight into a special-token buffer and a contiguous patch buffer (the
+//    SparseConv2D input), so there is no GELU pass and no slice copy;
+//  * up: the A rows come from the special-token buffer and the SparseConv2D
+//    output in place of the concatenation, and bias, gamma and the residual
+//    are applied before the single store (no cat, no scale pass, no add pass).
+// Roundings follow the unfused chain in the same dtype: the Linear output is
+// rounded to T, GELU is evaluated in fp32 on the rounded value, z * gamma is
+// rounded to T before the residual add.
+#include "sv_common.h"
+#include "sv_internal.h"
+#include "sv_mfma.h"
+
+namespace svtad {
+
+enum { EPI_DOWN_GELU = 0, EPI_UP_SCALE_RES = 1 };
+
+// Row m of a [batch, n_tokens, *] token tensor as a special-token row
+// (b * n_special + r) or a patch row (b * n_patch + r - n_special).
+// Rows are below 2^31 (checked on the host), so the division is 32-bit.
+struct RowMap {
+    int64_t n_tokens, n_special, n_patch;
+    __device__ __forceinline__ int64_t split(int64_t m, bool& special) const {
+        const uint32_t b = (uint32_t)m / (uint32_t)n_tokens;
+        const int64_t r = m - (int64_t)b * n_tokens;
+        special = r < n_special;
+        return special ? (int64_t)b * n_special + r : (int64_t)b * n_patch + (r - n_special);
+    }
+};
+
+constexpr int cmax_i(int a, int b) { return a > b ? a : b; }
+
+__device__ __forceinline__ float gelu_erf(float u) { return 0.5f * u * (1.0f + erff(u * 0.70710678118654752f)); }
+
+// out = epilogue(A W^T + bias): A [m_rows, k_red], W [n_out, k_red]. Four waves
+// as 2 x 2, each with FM x FN fragments: a BM = 32 FM by BN = 32 FN tile,
+// BK reduction values per stage (BK / 32 MFMA steps between barriers). The
+// weight fragment is the MFMA's A operand, so a lane accumulates 4
+// consecutive output columns of one row.
+// LDS rows are BK + 8 elements: for BK = 64 (144 bytes) and BK = 32 (80
+// bytes) the 16 rows one fragment read touches fall on distinct bank groups.
+// Global rows of the output and residual are moved as 16-byte pieces.
+template <typename T, int EPI, int FM, int FN, int BK>
+__global__ __launch_bounds__(256) void k_adapter_gemm(
+    const T* __restrict__ a0, const T* __restrict__ a1, const T* __restrict__ w,
+    const T* __restrict__ bias, const T* __restrict__ gamma, const T* __restrict__ res,
+    T* __restrict__ out0, T* __restrict__ out1, T* __restrict__ out2, int64_t m_rows, int k_red,
+    int n_out, RowMap rm, int n_col_tiles, int64_t n_tiles) {
+    constexpr int BM = 2 * FM * 16, BN = 2 * FN * 16;
+    constexpr int CPR = BK / 8;                                  // 16-byte chunks per row and stage
+    constexpr int LP = BK + 8;                                   // LDS pitch in elements
+    constexpr int A_PER = BM * CPR / 256, B_PER = BN * CPR / 256;  // chunks per thread
+    static_assert(A_PER * 256 == BM * CPR && B_PER * 256 == BN * CPR, "tile / thread count");
+    constexpr int OP = BN + 8;  // pitch (elements) of the output tiles of the epilogue
+    constexpr int SMEM = cmax_i(2 * (BM + BN) * LP, 2 * BM * OP);
+    // one array: the stage buffers, reused by the epilogue's two output tiles
+    __shared__ __align__(16) u16 smem[SMEM];
+    u16(*const As)[BM][LP] = (u16(*)[BM][LP])smem;
+    u16(*const Bs)[BN][LP] = (u16(*)[BN][LP])(smem + 2 * BM * LP);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t tile = xcd_tile(blockIdx.x, n_tiles);
+    const int64_t row0 = (tile / n_col_tiles) * BM;
+    const int col0 = (int)(tile % n_col_tiles) * BN;
+
+    // the thread's A rows and weight rows. Rows past the end read the last row
+    // instead (their outputs are not stored, and an output row depends on its
+    // own A row only), so every load is unconditional: a load under a
+    // condition becomes a branch, and the branch merge a wait for all loads
+    // in flight.
+    const T* arow[A_PER];
+#pragma unroll
+    for (int q = 0; q < A_PER; ++q) {
+        const int e = tid + q * 256;
+        const int64_t m = min<int64_t>(row0 + e / CPR, m_rows - 1);
+        const T* p;
+        if constexpr (EPI == EPI_UP_SCALE_RES) {
+            bool sp;
+            const int64_t r = rm.split(m, sp);
+            p = (sp ? a0 : a1) + r * k_red;
+        } else {
+            p = a0 + m * k_red;
+        }
+        arow[q] = p + (e % CPR) * 8;
+    }
+    const T* wrow[B_PER];
+#pragma unroll
+    for (int q = 0; q < B_PER; ++q) {
+        const int e = tid + q * 256;
+        wrow[q] = w + (int64_t)(col0 + e / CPR) * k_red + (e % CPR) * 8;
+    }
+
+    const int steps = k_red / BK;
+    u32x4 ra0[A_PER], rb0[B_PER], ra1[A_PER], rb1[B_PER];
+    auto load = [&](int t, u32x4* ra, u32x4* rb) {
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) ra[q] = *(const u32x4*)(arow[q] + t * BK);
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) rb[q] = *(const u32x4*)(wrow[q] + t * BK);
+    };
+    auto store = [&](int buf, const u32x4* ra, const u32x4* rb) {
+#pragma unroll
+        for (int q = 0; q < A_PER; ++q) {
+            const int e = tid + q * 256;
+            *(u32x4*)&As[buf][e / CPR][(e % CPR) * 8] = ra[q];
+        }
+#pragma unroll
+        for (int q = 0; q < B_PER; ++q) {
+            const int e = tid + q * 256;
+            *(u32x4*)&Bs[buf][e / CPR][(e % CPR) * 8] = rb[q];
+        }
+    };
+
+    f32x4 acc[FM][FN];
+#pragma unroll
+    for (int a = 0; a < FM; ++a)
+#pragma unroll
+        for (int b = 0; b < FN; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int wm = wave >> 1, wn = wave & 1;
+    const int arw = wm * FM * 16 + (lane & 15), brw = wn * FN * 16 + (lane & 15);
+    const int kof = (lane >> 4) * 8;
+
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < BK / KS; ++h) {
+            u32x4 fa[FM], fb[FN];
+#pragma unroll
+            for (int a = 0; a < FM; ++a) fa[a] = *(const u32x4*)&As[buf][arw + a * 16][h * KS + kof];
+#pragma unroll
+            for (int b = 0; b < FN; ++b) fb[b] = *(const u32x4*)&Bs[buf][brw + b * 16][h * KS + kof];
+#pragma unroll
+            for (int a = 0; a < FM; ++a)
+#pragma unroll
+                for (int b = 0; b < FN; ++b) acc[a][b] = MfmaOp<T>::run(fb[b], fa[a], acc[a][b]);
+        }
+    };
+    // Two register sets: the loads of stage t+2 are issued before the MFMAs
+    // of stage t, so each load has two stages to arrive. Past the last stage
+    // the loads re-read it (clamped index: no conditional loads) and the
+    // stores fill a buffer nobody reads.
+    const int last = steps - 1;
+    load(0, ra0, rb0);
+    store(0, ra0, rb0);
+    load(min(1, last), ra1, rb1);
+    __syncthreads();
+    for (int t = 0; t < steps; t += 2) {
+        load(min(t + 2, last), ra0, rb0);
+        compute(0);
+        store(1, ra1, rb1);
+        __syncthreads();
+        load(min(t + 3, last), ra1, rb1);
+        if (t + 1 < steps) compute(1);  // uniform
+        store(0, ra0, rb0);
+        __syncthreads();
+    }
+
+    // epilogue: acc[a][b][j] = C[m][n0 + j] (m = ... + lane % 16, n0 = ... +
+    // (lane / 16) * 4). The rounded tile goes through LDS (the stage buffers
+    // are free after the last barrier) so that global rows are read and
+    // written as 16-byte pieces of 8 consecutive lanes (whole 128-byte lines)
+    // rather than 8-byte pieces of 16 rows.
+    u16* const tile0 = smem;             // z (down: the Linear output) or T(z * gamma)
+    u16* const tile1 = smem + BM * OP;   // down: GELU(z)
+    const float gm = EPI == EPI_UP_SCALE_RES ? (float)gamma[0] : 0.f;
+#pragma unroll
+    for (int b = 0; b < FN; ++b) {
+        const int nl = wn * FN * 16 + b * 16 + (lane >> 4) * 4;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (bias) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[j] = (float)bias[col0 + nl + j];
+        }
+#pragma unroll
+        for (int a = 0; a < FM; ++a) {
+            const int ml = wm * FM * 16 + a * 16 + (lane & 15);
+            u16 z[4], gz[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const T zt = (T)(acc[a][b][j] + bv[j]);
+                if constexpr (EPI == EPI_DOWN_GELU) {
+                    z[j] = __builtin_bit_cast(u16, zt);
+                    gz[j] = __builtin_bit_cast(u16, (T)gelu_erf((float)zt));
+                } else {
+                    z[j] = __builtin_bit_cast(u16, (T)((float)zt * gm));
+                }
+            }
+            *(uint2*)&tile0[ml * OP + nl] = uint2{(unsigned)z[0] | ((unsigned)z[1] << 16),
+                                                 (unsigned)z[2] | ((unsigned)z[3] << 16)};
+            if constexpr (EPI == EPI_DOWN_GELU)
+                *(uint2*)&tile1[ml * OP + nl] = uint2{(unsigned)gz[0] | ((unsigned)gz[1] << 16),
+                                                     (unsigned)gz[2] | ((unsigned)gz[3] << 16)};
+        }
+    }
+    __syncthreads();
+    constexpr int RC = BN / 8;  // 16-byte chunks per tile row
+#pragma unroll
+    for (int c = tid; c < BM * RC; c += 256) {
+        const int ml = c / RC, nc = (c % RC) * 8;
+        const int64_t m = row0 + ml;
+        if (m >= m_rows) continue;
+        const u32x4 v0 = *(const u32x4*)&tile0[ml * OP + nc];
+        if constexpr (EPI == EPI_DOWN_GELU) {
+            *(u32x4*)(out0 + m * n_out + col0 + nc) = v0;
+            bool sp;
+            const int64_t r = rm.split(m, sp);
+            *(u32x4*)((sp ? out1 : out2) + r * n_out + col0 + nc) = *(const u32x4*)&tile1[ml * OP + nc];
+        } else {
+            const u32x4 rr = *(const u32x4*)(res + m * n_out + col0 + nc);
+            u32x4 y;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float lo = (float)__builtin_bit_cast(T, (u16)(v0[q] & 0xffffu)) +
+                                 (float)__builtin_bit_cast(T, (u16)(rr[q] & 0xffffu));
+                const float hi = (float)__builtin_bit_cast(T, (u16)(v0[q] >> 16)) +
+                                 (float)__builtin_bit_cast(T, (u16)(rr[q] >> 16));
+                y[q] = (unsigned)__builtin_bit_cast(u16, (T)lo) | ((unsigned)__builtin_bit_cast(u16, (T)hi) << 16);
+            }
+            *(u32x4*)(out0 + m * n_out + col0 + nc) = y;
+        }
+    }
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// shape checks shared by both entry points; 0 when the launch may proceed
+static int adapter_check(const char* what, int64_t batch, int64_t n_tokens, int64_t n_special, int k,
+                         int n, int dtype) {
+    if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
+        return set_error(SVTAD_ERR_UNSUPPORTED, what);
+    if (batch < 0 || n_tokens < 0 || n_special < 0 || n_special > n_tokens || k <= 0 || n <= 0)
+        return set_error(SVTAD_ERR_INVALID, what);
+    if (k % KS != 0 || n % 64 != 0) return set_error(SVTAD_ERR_UNSUPPORTED, what);
+    if (batch * n_tokens >= (int64_t)INT32_MAX) return set_error(SVTAD_ERR_UNSUPPORTED, what);
+    return SVTAD_OK;
+}
+
+template <typename T, int EPI, int FN, int BK, int FM = 4>
+static void launch_tiles(const void* a0, const void* a1, const void* w, const void* bias,
+                         const void* gamma, const void* res, void* o0, void* o1, void* o2,
+                         int64_t rows, int k, int n, RowMap rm, hipStream_t s) {
+    constexpr int BM = 32 * FM, BN = 32 * FN;
+    const int nct = n / BN;
+    const int64_t tiles = cdiv(rows, BM) * nct;
+    hipLaunchKernelGGL((k_adapter_gemm<T, EPI, FM, FN, BK>), dim3((unsigned)tiles), dim3(256), 0, s,
+                       (const T*)a0, (const T*)a1, (const T*)w, (const T*)bias, (const T*)gamma,
+                       (const T*)res, (T*)o0, (T*)o1, (T*)o2, rows, k, n, rm, nct, tiles);
+}
+
+// 64 x 64 tiles (enough workgroups per CU to cover the load latency), 64-deep
+// stages when k allows
+template <typename T, int EPI>
+static void launch_adapter(const void* a0, const void* a1, const void* w, const void* bias,
+                           const void* gamma, const void* res, void* o0, void* o1, void* o2,
+                           int64_t rows, int k, int n, RowMap rm, hipStream_t s) {
+    if (k % 64 == 0) launch_tiles<T, EPI, 2, 64, 2>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, s);
+    else launch_tiles<T, EPI, 2, 32, 2>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, s);
+}
+
+}  // namespace svtad
+
+using namespace svtad;
+
+extern "C" int svtad_adapter_down(const void* x, const void* weight, const void* bias, void* pre_act,
+                                  void* act_special, void* act_patch, int64_t batch, int64_t n_tokens,
+                                  int64_t n_special, int k, int n, int dtype, void* stream) {
+    int st = adapter_check("adapter_down: needs f16/bf16, k % 32 == 0, n % 64 == 0, 0 <= n_special <= n_tokens",
+                           batch, n_tokens, n_special, k, n, dtype);
+    if (st) return st;
+    const int64_t rows = batch * n_tokens;
+    if (rows == 0) return SVTAD_OK;
+    if (!x || !weight || !pre_act || (n_special > 0 && !act_special) || (n_tokens > n_special && !act_patch))
+        return set_error(SVTAD_ERR_INVALID, "adapter_down: null pointer");
+    if (!al16(x) || !al16(weight) || !al16(pre_act) || (act_special && !al16(act_special)) ||
+        (act_patch && !al16(act_patch)))
+        return set_error(SVTAD_ERR_INVALID, "adapter_down: x, weight and outputs need 16-byte alignment");
+    const RowMap rm{n_tokens, n_special, n_tokens - n_special};
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == SVTAD_F16)
+        launch_adapter<f16, EPI_DOWN_GELU>(x, nullptr, weight, bias, nullptr, nullptr, pre_act, act_special,
+                                           act_patch, rows, k, n, rm, s);
+    else
+        launch_adapter<bf16, EPI_DOWN_GELU>(x, nullptr, weight, bias, nullptr, nullptr, pre_act, act_special,
+                                            act_patch, rows, k, n, rm, s);
+    return launch_status();
+}
+
+extern "C" int svtad_adapter_up(const void* a_special, const void* a_patch, const void* weight,
+                                const void* bias, const void* gamma, const void* residual, void* out,
+                                int64_t batch, int64_t n_tokens, int64_t n_special, int k, int n,
+                                int dtype, void* stream) {
+    int st = adapter_check("adapter_up: needs f16/bf16, k % 32 == 0, n % 64 == 0, 0 <= n_special <= n_tokens",
+                           batch, n_tokens, n_special, k, n, dtype);
+    if (st) return st;
+    const int64_t rows = batch * n_tokens;
+    if (rows == 0) return SVTAD_OK;
+    if (!weight || !gamma || !residual || !out || (n_special > 0 && !a_special) ||
+        (n_tokens > n_special && !a_patch))
+        return set_error(SVTAD_ERR_INVALID, "adapter_up: null pointer");
+    if (!al16(weight) || (a_special && !al16(a_special)) || (a_patch && !al16(a_patch)) || !al16(residual) ||
+        !al16(out))
+        return set_error(SVTAD_ERR_INVALID, "adapter_up: inputs, weight, residual and out need 16-byte alignment");
+    const RowMap rm{n_tokens, n_special, n_tokens - n_special};
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == SVTAD_F16)
+        launch_adapter<f16, EPI_UP_SCALE_RES>(a_special, a_patch, weight, bias, gamma, residual, out, nullptr,
+                                              nullptr, rows, k, n, rm, s);
+    else
+        launch_adapter<bf16, EPI_UP_SCALE_RES>(a_special, a_patch, weight, bias, gamma, residual, out, nullptr,
+                                               nullptr, rows, k, n, rm, s);
+    return launch_status();
+}

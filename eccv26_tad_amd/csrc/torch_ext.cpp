@@ -567,6 +567,74 @@ at::Tensor op_validate_neighbor_table(const at::Tensor& table_in, int64_t bound)
     return stats;
 }
 
+// Adapter GEMMs with fused epilogues (f16 / bf16).
+void adapter_common(const at::Tensor& t, const at::Tensor& w, const char* name) {
+    check_gpu(t, name);
+    check_gpu(w, "weight");
+    TORCH_CHECK(t.scalar_type() == w.scalar_type(), name, " and weight dtypes differ");
+    TORCH_CHECK(t.scalar_type() == at::kHalf || t.scalar_type() == at::kBFloat16,
+                "adapter GEMMs take float16 / bfloat16, got ", t.scalar_type());
+    TORCH_CHECK(w.dim() == 2, "weight must be (out_features, in_features)");
+}
+
+const void* opt_ptr(const c10::optional<at::Tensor>& b, int64_t n, const at::Tensor& like) {
+    if (!bias_present(b)) return nullptr;
+    TORCH_CHECK(b->numel() == n && b->scalar_type() == like.scalar_type() && b->is_cuda(),
+                "bias must have ", n, " elements of the input dtype");
+    TORCH_CHECK(b->is_contiguous(), "bias must be contiguous");
+    return b->data_ptr();
+}
+
+// adapter_down(x [B, N, k], weight [n, k], bias [n] or None, n_special)
+//   -> (pre_act [B, N, n], act_special [B, S, n], act_patch [B * (N - S), n])
+std::tuple<at::Tensor, at::Tensor, at::Tensor> op_adapter_down(const at::Tensor& x_in, const at::Tensor& w_in,
+                                                               const c10::optional<at::Tensor>& bias,
+                                                               int64_t n_special) {
+    adapter_common(x_in, w_in, "x");
+    TORCH_CHECK(x_in.dim() == 3, "x must be [B, N, C]");
+    const int64_t B = x_in.size(0), N = x_in.size(1), k = x_in.size(2), n = w_in.size(0);
+    TORCH_CHECK(w_in.size(1) == k, "weight must be (n, ", k, ")");
+    TORCH_CHECK(n_special >= 0 && n_special <= N, "n_special out of range");
+    at::Tensor x = x_in.contiguous(), w = w_in.contiguous();
+    c10::DeviceGuard g(x.device());
+    at::Tensor pre = at::empty({B, N, n}, x.options());
+    at::Tensor sp = at::empty({B, n_special, n}, x.options());
+    at::Tensor pa = at::empty({B * (N - n_special), n}, x.options());
+    check_status(svtad_adapter_down(x.data_ptr(), w.data_ptr(), opt_ptr(bias, n, x), pre.data_ptr(),
+                                    sp.numel() ? sp.data_ptr() : nullptr, pa.numel() ? pa.data_ptr() : nullptr,
+                                    B, N, n_special, (int)k, (int)n, dtype_code(x), stream_of(x)),
+                 "adapter_down");
+    return {pre, sp, pa};
+}
+
+// adapter_up(a_special [B, S, k], a_patch [B * (N - S), k], weight [n, k], bias [n] or None,
+//            gamma [1], residual [B, N, n]) -> out [B, N, n]
+at::Tensor op_adapter_up(const at::Tensor& sp_in, const at::Tensor& pa_in, const at::Tensor& w_in,
+                         const c10::optional<at::Tensor>& bias, const at::Tensor& gamma_in,
+                         const at::Tensor& res_in) {
+    adapter_common(res_in, w_in, "residual");
+    TORCH_CHECK(res_in.dim() == 3, "residual must be [B, N, C]");
+    const int64_t B = res_in.size(0), N = res_in.size(1), n = res_in.size(2), k = w_in.size(1);
+    TORCH_CHECK(w_in.size(0) == n, "weight must be (", n, ", k)");
+    TORCH_CHECK(sp_in.dim() == 3 && sp_in.size(0) == B && sp_in.size(2) == k, "a_special must be [B, S, k]");
+    const int64_t S = sp_in.size(1);
+    TORCH_CHECK(S <= N && pa_in.dim() == 2 && pa_in.size(0) == B * (N - S) && pa_in.size(1) == k,
+                "a_patch must be [B * (N - S), k]");
+    TORCH_CHECK(sp_in.scalar_type() == res_in.scalar_type() && pa_in.scalar_type() == res_in.scalar_type() &&
+                    gamma_in.scalar_type() == res_in.scalar_type(),
+                "a_special, a_patch, gamma and residual must share the dtype");
+    TORCH_CHECK(gamma_in.numel() == 1 && gamma_in.is_cuda(), "gamma must be one element on the GPU");
+    at::Tensor sp = sp_in.contiguous(), pa = pa_in.contiguous(), w = w_in.contiguous(),
+               res = res_in.contiguous(), gm = gamma_in.contiguous();
+    c10::DeviceGuard g(res.device());
+    at::Tensor out = at::empty({B, N, n}, res.options());
+    check_status(svtad_adapter_up(sp.numel() ? sp.data_ptr() : nullptr, pa.numel() ? pa.data_ptr() : nullptr,
+                                  w.data_ptr(), opt_ptr(bias, n, res), gm.data_ptr(), res.data_ptr(),
+                                  out.data_ptr(), B, N, S, (int)k, (int)n, dtype_code(res), stream_of(res)),
+                 "adapter_up");
+    return out;
+}
+
 PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.doc() = "MI355X (gfx950) SparseConv2D: drop-in for the reference opentad_sparse_ops";
     m.def("fwd", &op_fwd, "Forward", py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
@@ -622,5 +690,10 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("table"), py::arg("tokens_per_batch") = 0);
     m.def("validate_neighbor_table", &op_validate_neighbor_table,
           "(out-of-range count, min, max) of a neighbor table", py::arg("table"), py::arg("bound"));
+    m.def("adapter_down", &op_adapter_down, "Adapter down_proj + GELU + special / patch split",
+          py::arg("x"), py::arg("weight"), py::arg("bias"), py::arg("n_special"));
+    m.def("adapter_up", &op_adapter_up, "Adapter up_proj on cat(special, patch) * gamma + residual",
+          py::arg("a_special"), py::arg("a_patch"), py::arg("weight"), py::arg("bias"), py::arg("gamma"),
+          py::arg("residual"));
     m.def("version", []() { return std::string(svtad_version()); });
 }

@@ -250,6 +250,40 @@ int svtad_transpose_table(const int32_t* table, int64_t n, int64_t tokens_per_ba
 int svtad_validate_table(const int32_t* table, int64_t n_entries, int64_t bound, int32_t* stats,
                          void* stream);
 
+/*
+ * Adapter down projection with the GELU epilogue (the down_proj + act of the
+ * sparse-conv adapter, vit_sparse_adapter_poguise.py:305-306, and the
+ * special / patch split of :307-309):
+ *   pre_act[m, :] = T(x[m, :] W^T + bias)                (nn.Linear, W [n, k])
+ *   act[m, :]     = T(GELU(float(pre_act[m, :])))       (exact erf GELU)
+ * x is [batch, n_tokens, k]; row r of sample b goes to act_special[b *
+ * n_special + r] when r < n_special and to act_patch[b * (n_tokens -
+ * n_special) + r - n_special] otherwise (the contiguous SparseConv2D input),
+ * pre_act keeps the [batch, n_tokens, n] layout. bias may be NULL. f16 / bf16
+ * only; k % 32 == 0, n % 64 == 0; x, weight and the outputs 16-byte aligned.
+ * One launch on `stream`.
+ */
+int svtad_adapter_down(const void* x, const void* weight, const void* bias, void* pre_act,
+                       void* act_special, void* act_patch, int64_t batch, int64_t n_tokens,
+                       int64_t n_special, int k, int n, int dtype, void* stream);
+
+/*
+ * Adapter up projection with the scale-and-residual epilogue (the cat of
+ * special tokens and SparseConv2D output, up_proj, gamma and residual of
+ * vit_sparse_adapter_poguise.py:362,652-653):
+ *   z[m, :]   = T(c[m, :] W^T + bias)       c = cat(a_special, a_patch) per sample
+ *   out[m, :] = T(T(z * gamma[0]) + residual[m, :])
+ * a_special [batch * n_special, k], a_patch [batch * (n_tokens - n_special), k]
+ * are read in place of the concatenation; residual and out are [batch,
+ * n_tokens, n]; gamma is one element of `dtype` on the device (no host read).
+ * bias may be NULL. f16 / bf16 only; k % 32 == 0, n % 64 == 0; inputs,
+ * weight, residual and out 16-byte aligned. One launch.
+ */
+int svtad_adapter_up(const void* a_special, const void* a_patch, const void* weight,
+                     const void* bias, const void* gamma, const void* residual, void* out,
+                     int64_t batch, int64_t n_tokens, int64_t n_special, int k, int n, int dtype,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -126,6 +126,29 @@ def test_prune_step_arguments_checked_on_host(lib):
                                 None, None, None, None, None) == 0
 
 
+def test_adapter_arguments_checked_on_host(lib):
+    buf = ctypes.create_string_buffer(256)
+    # dtype: the fused adapter GEMMs take f16 / bf16 only
+    st = lib.svtad_adapter_down(buf, buf, None, buf, buf, buf, I64(1), I64(4), I64(1), 64, 64, 0, None)
+    assert st == -3 and b"f16/bf16" in lib.svtad_last_error()
+    # k % 32, n % 64
+    st = lib.svtad_adapter_down(buf, buf, None, buf, buf, buf, I64(1), I64(4), I64(1), 48, 64, 1, None)
+    assert st == -3
+    st = lib.svtad_adapter_up(buf, buf, buf, None, buf, buf, buf, I64(1), I64(4), I64(1), 64, 96, 1, None)
+    assert st == -3
+    # more special tokens than tokens
+    st = lib.svtad_adapter_up(buf, buf, buf, None, buf, buf, buf, I64(1), I64(4), I64(5), 64, 64, 1, None)
+    assert st == -1
+    # missing gamma / patch output
+    st = lib.svtad_adapter_up(buf, buf, buf, None, None, buf, buf, I64(1), I64(4), I64(1), 64, 64, 1, None)
+    assert st == -1 and b"null pointer" in lib.svtad_last_error()
+    st = lib.svtad_adapter_down(buf, buf, None, buf, buf, None, I64(1), I64(4), I64(1), 64, 64, 2, None)
+    assert st == -1 and b"null pointer" in lib.svtad_last_error()
+    # nothing to do
+    assert lib.svtad_adapter_down(None, None, None, None, None, None, I64(0), I64(4), I64(1), 64, 64, 1,
+                                  None) == 0
+
+
 def test_table_limits_rejected(lib):
     st = lib.svtad_table_scan(ctypes.create_string_buffer(8), I64(1), 200, 200,
                               ctypes.create_string_buffer(8), None)
@@ -140,7 +163,8 @@ def test_extension_module_api():
         assert hasattr(ops, name)
     for name in ("fwd_bias", "bwd_w_bias", "dw_fwd", "dw_bwd_in", "dw_bwd_w",
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
-                 "validate_neighbor_table", "prune_tokens", "bwd_packed"):
+                 "validate_neighbor_table", "prune_tokens", "bwd_packed", "adapter_down",
+                 "adapter_up"):
         assert hasattr(ops, name)
     import torch
 

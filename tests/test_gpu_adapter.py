@@ -1,0 +1,126 @@
+"""The fused sparse-conv adapter (down GEMM + GELU epilogue -> SparseConv2D ->
+up GEMM + gamma / residual epilogue) against the unfused chain of the
+reference (vit_sparse_adapter_poguise.py:305-362,652-653) run in float32 on
+the same rounded weights and inputs: output and every gradient (x, down_proj,
+up_proj, gamma, the sparse conv's weight and bias). Bar: max-scaled error
+<= 1e-2 (float16 / bfloat16). The kernels' direct outputs (pre-activation,
+split GELU, fused up projection) are checked the same way.
+
+Shapes: the ViT-B adapter (embed 768, hidden 256 after the reference's
+power-of-two rounding) on B2 x T80 x 14x14 at 55 % keep with one CLS token,
+and a small case with no special token.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import topk_mask
+
+pytestmark = pytest.mark.gpu
+
+
+def _err(got, ref):
+    got, ref = got.double(), ref.double()
+    return float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+def _setup(dev, dt, B, T, H, W, keep, embed, mlp_ratio, S, seed):
+    import eccv26_tad_amd as sv
+
+    rng = np.random.default_rng(seed)
+    mask = topk_mask(rng, B, T, H, W, keep)
+    flat = mask.reshape(B, -1)
+    idx = torch.from_numpy(np.stack([np.flatnonzero(flat[b]) for b in range(B)])).to(dev)
+    table = sv.build_neighbor_table(torch.from_numpy(mask).to(dev)).view(B, -1, 9)
+    g = torch.Generator().manual_seed(seed)
+    mod = sv.SparseConvAdapter(embed, mlp_ratio)
+    with torch.no_grad():  # non-trivial up_proj / gamma / conv bias (the init zeroes up_proj)
+        mod.up_proj.weight.copy_(torch.randn(mod.up_proj.weight.shape, generator=g) * 0.05)
+        mod.up_proj.bias.copy_(torch.randn(embed, generator=g) * 0.1)
+        mod.down_proj.bias.copy_(torch.randn(mod.hidden_dims, generator=g) * 0.1)
+        mod.gamma.fill_(0.75)
+        mod.sparse_conv.bias.copy_(torch.randn(mod.hidden_dims, generator=g) * 0.1)
+    mod = mod.to(dev, dt)
+    ref = sv.SparseConvAdapter(embed, mlp_ratio).to(dev)
+    ref.load_state_dict({k: v.float() for k, v in mod.state_dict().items()})
+    N = S + idx.shape[1]
+    x = torch.randn(B, N, embed, generator=g).to(dev, dt)
+    go = torch.randn(B, N, embed, generator=g).to(dev, dt)
+    return mod, ref, idx, table, x, go
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("case", [
+    dict(B=2, T=80, H=14, W=14, keep=0.55, embed=768, mlp_ratio=0.25, S=1, seed=31),
+    dict(B=3, T=4, H=6, W=7, keep=0.3, embed=128, mlp_ratio=0.5, S=0, seed=32),
+])
+def test_fused_adapter_matches_unfused_chain(dev, dname, case):
+    dt = getattr(torch, dname)
+    c = dict(case)
+    S = c.pop("S")
+    mod, ref, idx, table, x, go = _setup(dev, dt, S=S, **c)
+    B, T, H, W = c["B"], c["T"], c["H"], c["W"]
+    print("adapter", dname, case, "N", x.shape[1], "hidden", mod.hidden_dims, flush=True)
+
+    xf = x.detach().clone().requires_grad_(True)
+    y = mod(xf, H, W, idx, T * H * W, table)
+    y.backward(go)
+
+    xr = x.detach().float().requires_grad_(True)
+    yr = ref.reference_forward(xr, H, W, idx, T * H * W, table)
+    yr.backward(go.float())
+
+    tol = 1e-2
+    assert y.dtype == dt and y.shape == yr.shape
+    assert _err(y.detach(), yr.detach()) <= tol
+    assert _err(xf.grad, xr.grad) <= tol
+    params = dict(mod.named_parameters())
+    for name, pr in ref.named_parameters():
+        assert _err(params[name].grad, pr.grad) <= tol, name
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+def test_adapter_kernels_direct(dev, dname):
+    import eccv26_tad_amd as sv
+
+    dt = getattr(torch, dname)
+    g = torch.Generator().manual_seed(7)
+    B, N, S, k, n = 2, 301, 3, 256, 192
+    x = torch.randn(B, N, k, generator=g).to(dev, dt)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(dev, dt)
+    b = (torch.randn(n, generator=g) * 0.1).to(dev, dt)
+    pre, sp, pa = sv.ops.adapter_down(x, w, b, S)
+    u_ref = x.float() @ w.float().t() + b.float()
+    assert _err(pre, u_ref) <= 1e-2
+    gl = torch.nn.functional.gelu(pre.float())
+    assert _err(sp, gl[:, :S]) <= 1e-2 and _err(pa, gl[:, S:].reshape(-1, n)) <= 1e-2
+    # GELU is evaluated on the rounded pre-activation, as PyTorch's GELU of it
+    assert _err(sp, torch.nn.functional.gelu(pre[:, :S]).float()) <= (2e-3 if dt == torch.float16 else 1e-2)
+
+    wu = (torch.randn(k, n, generator=g) * 0.05).to(dev, dt)
+    bu = (torch.randn(k, generator=g) * 0.1).to(dev, dt)
+    gm = torch.tensor([0.6], device=dev, dtype=dt)
+    res = torch.randn(B, N, k, generator=g).to(dev, dt)
+    y = sv.ops.adapter_up(sp, pa, wu, bu, gm, res)
+    c = torch.cat([sp, pa.view(B, N - S, n)], dim=1).float()
+    y_ref = (c @ wu.float().t() + bu.float()) * 0.6 + res.float()
+    assert _err(y, y_ref) <= 1e-2
+    # without bias, and no special tokens
+    pre0, sp0, pa0 = sv.ops.adapter_down(x, w, None, 0)
+    assert sp0.numel() == 0 and _err(pa0, torch.nn.functional.gelu(x.float() @ w.float().t()).reshape(-1, n)) <= 1e-2
+    y0 = sv.ops.adapter_up(sp0, pa0, wu, None, gm, res)
+    assert _err(y0, (pa0.float() @ wu.float().t()).view(B, N, k) * 0.6 + res.float()) <= 1e-2
+
+
+def test_fused_adapter_rejects_float32(dev):
+    import eccv26_tad_amd as sv
+
+    mod = sv.SparseConvAdapter(128, 0.5).to(dev)
+    x = torch.randn(1, 5, 128, device=dev)
+    with pytest.raises(RuntimeError, match="float16 / bfloat16"):
+        mod(x, 2, 2, torch.arange(4, device=dev).view(1, 4), 4, torch.zeros(4, 9, dtype=torch.int32, device=dev))
+    assert math.isfinite(float(mod.gamma))
