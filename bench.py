@@ -368,6 +368,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
+    ap.add_argument("--only", choices=("adapter", "prune"), default=None,
+                    help="only time the fused adapter or the prune step, print its JSON and exit "
+                         "(for kernel traces of those paths)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the SparseConv2D path has no "
@@ -390,6 +393,12 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 5}), flush=True)
+        return
+    if args.only == "adapter":
+        print(json.dumps({"adapter": adapter_measure(dev, args.steps)}), flush=True)
+        return
+    if args.only == "prune":
+        print(json.dumps({"prune_step": prune_measure(dev, args.steps, False)}), flush=True)
         return
 
     log(f"bench: building problem keep={args.keep}")
