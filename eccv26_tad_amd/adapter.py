@@ -24,10 +24,15 @@ SparseConv2D forward, ``opentad_sparse_ops.adapter_up``):
   global), so there is no host sync; ``None`` restores the reference's
   ``max()`` heuristic (``sparse_conv_layer.py:174-177``).
 
-The backward runs on library GEMMs (``torch.matmul``) and PyTorch's own GELU
-backward. ``gamma``'s gradient needs ``z = cat(...) W_u^T + b_u``, which the
-fused forward never stores: ``sum(go * z) = <W_u, go^T c> + <b_u, sum(go)>``,
-and ``go^T c`` is the up-projection's weight-gradient GEMM anyway.
+The backward's weight gradients (sums over every token row) run on the
+split-row kernel of SparseConv2D's backward-weight pass with one offset
+(``opentad_sparse_ops.linear_wgrad``: deterministic, and a grid that fills the
+chip where a library GEMM with a 17k-long reduction gets a dozen workgroups);
+the input gradients use library GEMMs (``torch.matmul``) and PyTorch's own
+GELU backward. ``gamma``'s gradient needs ``z = cat(...) W_u^T + b_u``, which
+the fused forward never stores: ``sum(go * z) = <W_u, go^T c> + <b_u,
+sum(go)>``, and ``go^T c`` is the up-projection's weight-gradient reduction
+anyway.
 
 The fused path takes float16 / bfloat16 (the matrix-core dtypes) and raises
 otherwise; ``reference_forward`` runs the unfused chain in the reference's op
@@ -45,6 +50,18 @@ from . import opentad_sparse_ops as _ops
 from .sparse_conv_layer import SparseConv2d
 
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def _colsum(a):
+    """Column sums of a [rows, n] matrix as a ones-vector GEMM (fp32
+    accumulation, result in a's dtype): one library GEMM, where a dim-0
+    reduction over 17k rows is several times slower."""
+    return torch.matmul(torch.ones(1, a.shape[0], device=a.device, dtype=a.dtype), a).view(-1)
+
+
+def _NO_ROWS(like):
+    """Empty row list: the weight-gradient kernel then takes rows in order."""
+    return torch.empty(0, dtype=torch.int32, device=like.device)
 
 
 class AdapterDownFunction(Function):
@@ -75,8 +92,8 @@ class AdapterDownFunction(Function):
         du = torch.ops.aten.gelu_backward(dg, pre)
         du2 = du.reshape(-1, n)
         gx = torch.matmul(du, weight) if ctx.needs_input_grad[0] else None
-        gw = torch.matmul(du2.t(), x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
-        gb = du2.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        gw = _ops.linear_wgrad(du2, _NO_ROWS(du2), x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
+        gb = _colsum(du2) if ctx.has_bias and ctx.needs_input_grad[2] else None
         return gx, gw, gb, None
 
 
@@ -96,23 +113,29 @@ class AdapterUpFunction(Function):
         S = a_sp.shape[1]
         k = weight.shape[1]
         go = go.contiguous()
-        go_sp = go[:, :S].reshape(-1, n)
-        go_pa = go[:, S:].reshape(-1, n)
-        # go^T c without building c = cat(a_special, a_patch)
-        G = torch.matmul(go_pa.t(), a_pa)
+        go2 = go.reshape(-1, n)
+        # go^T c without building c = cat(a_special, a_patch): the patch rows
+        # on the split-row kernel (rows of go picked by a row list), the few
+        # special rows as a small GEMM
         if S > 0:
-            G = G + torch.matmul(go_sp.t(), a_sp.reshape(-1, k))
-        gsum = go.reshape(-1, n).sum(0)
+            P = N - S
+            r = torch.arange(B * P, device=go.device, dtype=torch.int32)
+            rows = (r // P) * N + S + r % P
+            G = _ops.linear_wgrad(go2, rows, a_pa)
+            G = G + torch.matmul(go[:, :S].reshape(-1, n).t(), a_sp.reshape(-1, k))
+        else:
+            G = _ops.linear_wgrad(go2, _NO_ROWS(go2), a_pa)
+        gsum = _colsum(go2)
         g_gamma = None
         if ctx.needs_input_grad[4]:
             s = (weight.float() * G.float()).sum()
             if bias is not None:
                 s = s + (bias.float() * gsum.float()).sum()
             g_gamma = s.reshape(1).to(gamma.dtype)
-        dz = go * gamma
         g_sp = g_pa = None
         if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
-            dc = torch.matmul(dz, weight)  # [B, N, k]
+            # (go * gamma) W = go (gamma W): gamma folded into the small weight
+            dc = torch.matmul(go, weight * gamma)  # [B, N, k]
             g_sp = dc[:, :S] if ctx.needs_input_grad[0] else None
             g_pa = dc[:, S:].reshape(-1, k) if ctx.needs_input_grad[1] else None
         gw = G * gamma if ctx.needs_input_grad[2] else None

@@ -21,6 +21,7 @@
 // rounded to T, GELU is evaluated in fp32 on the rounded value, z * gamma is
 // rounded to T before the residual add.
 #include "sv_common.h"
+#include "sv_conv.h"
 #include "sv_internal.h"
 #include "sv_mfma.h"
 
@@ -320,5 +321,32 @@ extern "C" int svtad_adapter_up(const void* a_special, const void* a_patch, cons
     else
         launch_adapter<bf16, EPI_UP_SCALE_RES>(a_special, a_patch, weight, bias, gamma, residual, out, nullptr,
                                                nullptr, rows, k, n, rm, s);
+    return launch_status();
+}
+
+extern "C" size_t svtad_linear_wgrad_workspace_bytes(int64_t n, int c_g, int c_x, int dtype) {
+    (void)dtype;
+    if (n < 0 || c_g <= 0 || c_x <= 0) return 0;
+    return plan_wgrad(n, c_g, c_x).ws_bytes;
+}
+
+extern "C" int svtad_linear_wgrad(const void* g, const int32_t* rows, const void* x, void* out, void* workspace,
+                                  size_t workspace_bytes, int64_t n, int64_t n_g_rows, int c_g, int c_x,
+                                  int dtype, void* stream) {
+    if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: needs f16/bf16");
+    if (n < 0 || n_g_rows < 0 || c_g <= 0 || c_x <= 0 || (!rows && n_g_rows < n))
+        return set_error(SVTAD_ERR_INVALID, "linear_wgrad: bad sizes");
+    const BwPlan p = plan_wgrad(n, c_g, c_x);
+    if (!p.path) return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: no tile configuration for these widths");
+    if (std::max(n, n_g_rows) * (int64_t)std::max(c_g, c_x) * 2 >= (int64_t)INT32_MAX)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: more than 2^31 bytes per operand");
+    if (!out || !workspace || (n > 0 && (!g || !x)))
+        return set_error(SVTAD_ERR_INVALID, "linear_wgrad: null pointer");
+    if ((g && !al16(g)) || (x && !al16(x)))
+        return set_error(SVTAD_ERR_INVALID, "linear_wgrad: g and x need 16-byte alignment");
+    if (workspace_bytes < p.ws_bytes)
+        return set_error(SVTAD_ERR_WORKSPACE, "linear_wgrad: workspace smaller than svtad_linear_wgrad_workspace_bytes()");
+    wgrad_mfma(dtype, p, g, rows, x, out, workspace, n, rows ? n_g_rows : n, c_g, c_x, (hipStream_t)stream);
     return launch_status();
 }

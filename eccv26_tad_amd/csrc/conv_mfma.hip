@@ -932,13 +932,13 @@ __device__ __forceinline__ void transpose8(const u32x4* in, u32x4* out) {
 // added in order g = 0..3 through LDS, so the order of the sum is fixed.
 template <typename T>
 __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __restrict__ part,
-                                                int splits, int c_in, int c_out, int fm, int fn,
+                                                int splits, int n_off, int c_in, int c_out, int fm, int fn,
                                                 int wgm, int wgn, int n_ci_tiles, int n_co_tiles,
                                                 T* __restrict__ gw) {
     __shared__ f32x4 qsum[4][64];
     const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int bm = wgm * fm * 16, bn = wgn * fn * 16;
-    const int64_t per_split = (int64_t)9 * c_in * c_out;
+    const int64_t per_split = (int64_t)n_off * c_in * c_out;
     const int64_t quads = per_split / 4;
     const int64_t e = blk * 64 + lane;
     const int spt = (splits + 3) / 4;
@@ -1001,7 +1001,12 @@ __device__ __forceinline__ void bw_reduce_bias(int64_t c, const float* __restric
 }
 
 // staging waves of k_bw_big: one 8-row x 8-channel block of x rows or of go
-// rows per thread and stage
+// rows per thread and stage.
+// With n_off = 9, nbr is the [n, 9] neighbor table and the partials cover the
+// 9 offsets. With n_off = 1, nbr is a list of n source rows of x (NULL: row i
+// itself) and the kernel computes the plain reduction gw[ci][co] = sum_i
+// x[nbr[i]][ci] go[i][co] (a linear layer's weight gradient); x then has
+// n_src rows.
 constexpr int BW_IROWS = 8;
 constexpr int bw_stage_waves(int fm, int fn, int wgm, int wgn) {
     return ((KR / BW_IROWS) * (wgm * fm * 2) + 63) / 64 + ((KR / BW_IROWS) * (wgn * fn * 2) + 63) / 64;
@@ -1014,7 +1019,8 @@ template <typename T, int FM, int FN, int WGM, int WGN>
 __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     const T* __restrict__ go, const T* __restrict__ x, const int32_t* __restrict__ nbr,
     float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int c_in, int c_out,
-    int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks) {
+    int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks, int n_off,
+    int64_t n_src) {
     constexpr int NT = bw_big_threads(FM, FN, WGM, WGN);
     constexpr int NMW = WGM * WGN;     // matrix waves
     constexpr int BM = WGM * FM * 16;  // ci
@@ -1045,7 +1051,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int64_t lin = xcd_tile(blockIdx.x, n_blocks);
-    const int tiles = 9 * n_ci_tiles * n_co_tiles;
+    const int tiles = n_off * n_ci_tiles * n_co_tiles;
     const int s = (int)(lin / tiles);
     int rem = (int)(lin - (int64_t)s * tiles);
     const int k = rem / (n_ci_tiles * n_co_tiles);
@@ -1055,10 +1061,18 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     const int64_t r_begin = (int64_t)s * rows_per_split;
     const int rows = (int)max<int64_t>(0, min(n, r_begin + rows_per_split) - r_begin);
     const int steps = (rows + KR - 1) / KR;
-    const bool do_bias = ws_bias != nullptr && k == 4 && ci0 == 0;  // uniform
+    const bool do_bias = ws_bias != nullptr && k == (n_off == 9 ? 4 : 0) && ci0 == 0;  // uniform
 
     for (int r = tid; r < (steps + 2) * KR; r += NT) {
-        const int64_t sr = r < rows ? src_row(nbr, r_begin + r, k, n, tpb) : -1;
+        int64_t sr = -1;
+        if (r < rows) {
+            if (n_off == 9) {
+                sr = src_row(nbr, r_begin + r, k, n, tpb);
+            } else {  // row list (NULL: identity)
+                sr = nbr ? (int64_t)nbr[r_begin + r] : r_begin + r;
+                if (sr >= n_src) sr = -1;
+            }
+        }
         srow[0][r] = sr >= 0 ? (uint32_t)sr * (uint32_t)(c_in * 2) : kOOB;
         srow[1][r] = r < rows ? (uint32_t)r * (uint32_t)(c_out * 2) : kOOB;
     }
@@ -1099,7 +1113,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
             __syncthreads();
         }
         // partial tile in fragment order: [wave][a][b][lane][4]
-        float* dst = ws + (((int64_t)s * 9 + k) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
+        float* dst = ws + (((int64_t)s * n_off + k) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
 #pragma unroll
         for (int a = 0; a < FM; ++a)
 #pragma unroll
@@ -1126,7 +1140,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
         const int chan = (role_a ? ci0 : co0) + cl;
         const bool chan_ok = has_item && chan < (role_a ? c_in : c_out);
         const rsrc_t rs = make_rsrc(role_a ? (const void*)x : (const void*)(go + r_begin * c_out),
-                                    role_a ? (uint32_t)(n * c_in * 2) : (uint32_t)((int64_t)rows * c_out * 2));
+                                    role_a ? (uint32_t)(n_src * c_in * 2) : (uint32_t)((int64_t)rows * c_out * 2));
         // offsets stay below 2^31 + 2^16 (kOOB plus a channel offset): no wrap
         const uint32_t chan_b = chan_ok ? (uint32_t)chan * 2u : kOOB;
         const uint32_t* const tab = srow[role_a ? 0 : 1] + rgp * BW_IROWS;
@@ -1214,14 +1228,14 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
 template <typename T>
 __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ part,
                                                    const float* __restrict__ part_b, int splits,
-                                                   int c_in, int c_out, int fm, int fn, int wgm,
+                                                   int n_off, int c_in, int c_out, int fm, int fn, int wgm,
                                                    int wgn, int n_ci_tiles, int n_co_tiles,
                                                    T* __restrict__ gw, T* __restrict__ gb,
                                                    OrphanJob oj) {
     // workgroups [0, quad_blocks) reduce gw, the rest the bias
-    const int64_t quad_blocks = ((int64_t)9 * c_in * c_out / 4 + 63) / 64;
+    const int64_t quad_blocks = ((int64_t)n_off * c_in * c_out / 4 + 63) / 64;
     if ((int64_t)blockIdx.x < quad_blocks)
-        bw_reduce_quads<T>(blockIdx.x, part, splits, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles,
+        bw_reduce_quads<T>(blockIdx.x, part, splits, n_off, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles,
                            n_co_tiles, gw);
     else if (gb)
         bw_reduce_bias<T>(((int64_t)blockIdx.x - quad_blocks) * 256 + threadIdx.x, part_b, splits, c_out, gb);
@@ -1472,7 +1486,7 @@ static void launch_big(const BwPlan& p, const void* go, const void* x, const int
     hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks),
                        dim3(bw_big_threads(FM, FN, WGM, WGN)),
                        0, s, (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
-                       p.rows_per_split, nci, nco, blocks);
+                       p.rows_per_split, nci, nco, blocks, 9, n);
 }
 
 template <typename T>
@@ -1527,17 +1541,73 @@ bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const in
         const OrphanJob job = oj ? *oj : OrphanJob{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
         if (dtype == SVTAD_F16)
             hipLaunchKernelGGL((k_bw_reduce<f16>), grid, dim3(256), 0, s, (const float*)part,
-                               (const float*)part_b, p.splits, c_in, c_out, bc.fm, bc.fn, bc.wgm,
+                               (const float*)part_b, p.splits, 9, c_in, c_out, bc.fm, bc.fn, bc.wgm,
                                bc.wgn, nci, nco, (f16*)gw, (f16*)gb, job);
         else
             hipLaunchKernelGGL((k_bw_reduce<bf16>), grid, dim3(256), 0, s, (const float*)part,
-                               (const float*)part_b, p.splits, c_in, c_out, bc.fm, bc.fn, bc.wgm,
+                               (const float*)part_b, p.splits, 9, c_in, c_out, bc.fm, bc.fn, bc.wgm,
                                bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb, job);
         return oj != nullptr;
     }
     split_reduce(dtype, part, 9LL * c_in * c_out, p.splits, gw, s);
     if (gb) split_reduce(dtype, part_b, (int64_t)c_out, p.splits, gb, s);
     return false;
+}
+
+// Row-split plan of a linear layer's weight gradient (one offset): splits
+// of whole 128-row pairs of stages, enough workgroups for every CU, at most
+// kMaxSplitRows - 128 rows each.
+BwPlan plan_wgrad(int64_t n, int c_in, int c_out) {
+    BwPlan p;
+    BigCfg c;
+    p.path = big_cfg(c_in, c_out, &c) ? 1 : 0;
+    const int64_t tiles = p.path ? (int64_t)(c_in / (16 * c.wgm * c.fm)) * (c_out / (16 * c.wgn * c.fn)) : 1;
+    int64_t splits = std::max<int64_t>(cdiv(std::max<int64_t>(n, 1), kMaxSplitRows - 128),
+                                       std::min<int64_t>(std::max<int64_t>(1, cu_count() / tiles),
+                                                         cdiv(std::max<int64_t>(n, 1), 256)));
+    int64_t rps = cdiv(cdiv(std::max<int64_t>(n, 1), splits), 128) * 128;
+    splits = std::max<int64_t>(1, cdiv(n, rps));
+    p.splits = (int)splits;
+    p.rows_per_split = rps;
+    p.ws_bytes = (size_t)splits * c_in * c_out * sizeof(float);
+    return p;
+}
+
+template <typename T, int FM, int FN, int WGM, int WGN>
+static void launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
+                         float* part, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s) {
+    constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
+    const int nci = c_in / BM, nco = c_out / BN;
+    const int64_t blocks = (int64_t)nci * nco * p.splits;
+    // the kernel's "x" (gathered, ci) is g and its "go" (linear, co) is x
+    hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks),
+                       dim3(bw_big_threads(FM, FN, WGM, WGN)), 0, s, (const T*)x, (const T*)g, rows,
+                       part, (float*)nullptr, n, c_in, c_out, (int64_t)0, p.rows_per_split, nci, nco,
+                       blocks, 1, n_src);
+    const dim3 grid((unsigned)cdiv((int64_t)c_in * c_out / 4, 64));
+    const OrphanJob none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
+    hipLaunchKernelGGL((k_bw_reduce<T>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
+                       p.splits, 1, c_in, c_out, FM, FN, WGM, WGN, nci, nco, (T*)out, (T*)nullptr, none);
+}
+
+bool wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
+                void* ws, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s) {
+    BigCfg bc;
+    if (!p.path || !big_cfg(c_in, c_out, &bc)) return false;
+#define SVTAD_WG_CASE(M, N, WM, WN)                                                                   \
+    if (bc.fm == M && bc.fn == N && bc.wgm == WM && bc.wgn == WN) {                                   \
+        if (dtype == SVTAD_F16) launch_wgrad<f16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, n, n_src, c_in, c_out, s); \
+        else launch_wgrad<bf16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, n, n_src, c_in, c_out, s);  \
+        found = true;                                                                                 \
+    }
+    bool found = false;
+    SVTAD_WG_CASE(6, 3, 2, 4)
+    else SVTAD_WG_CASE(4, 4, 2, 4)
+    else SVTAD_WG_CASE(4, 2, 2, 4)
+    else SVTAD_WG_CASE(3, 3, 2, 2)
+    else SVTAD_WG_CASE(2, 2, 2, 2)
+#undef SVTAD_WG_CASE
+    return found;
 }
 
 }  // namespace svtad

@@ -94,4 +94,12 @@ bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const in
              void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
              const OrphanJob* oj, hipStream_t s);
 
+// A linear layer's weight gradient out[ci][co] = sum_i g[rows[i]][ci] x[i][co]
+// (rows NULL: row i of g), i < n, on the backward-weight partial kernel with
+// one offset and its ordered reduction. path 0 in the plan: no large-tile
+// configuration for (c_in, c_out); wgrad_mfma then returns false.
+BwPlan plan_wgrad(int64_t n, int c_in, int c_out);
+bool wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
+                void* ws, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s);
+
 }  // namespace svtad

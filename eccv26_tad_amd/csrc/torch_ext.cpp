@@ -635,6 +635,35 @@ at::Tensor op_adapter_up(const at::Tensor& sp_in, const at::Tensor& pa_in, const
     return out;
 }
 
+// linear_wgrad(g [*, c_g], rows int32 [n] or empty, x [n, c_x]) -> out [c_g, c_x]
+// (out = g[rows]^T x, or g^T x with the first n rows of g when rows is empty)
+at::Tensor op_linear_wgrad(const at::Tensor& g_in, const at::Tensor& rows_in, const at::Tensor& x_in) {
+    adapter_common(g_in, g_in, "g");
+    check_gpu(x_in, "x");
+    TORCH_CHECK(x_in.scalar_type() == g_in.scalar_type(), "g and x dtypes differ");
+    TORCH_CHECK(g_in.dim() == 2 && x_in.dim() == 2, "g and x must be 2-D");
+    const int64_t n = x_in.size(0), c_g = g_in.size(1), c_x = x_in.size(1);
+    const bool with_rows = rows_in.defined() && rows_in.numel() > 0;
+    at::Tensor rows;
+    if (with_rows) {
+        check_gpu(rows_in, "rows");
+        TORCH_CHECK(rows_in.scalar_type() == at::kInt && rows_in.numel() == n, "rows must be int32 [n]");
+        rows = rows_in.contiguous();
+    } else {
+        TORCH_CHECK(g_in.size(0) >= n, "g has fewer rows than x");
+    }
+    at::Tensor g = g_in.contiguous(), x = x_in.contiguous();
+    c10::DeviceGuard guard(x.device());
+    at::Tensor out = at::empty({c_g, c_x}, x.options());
+    const size_t ws = svtad_linear_wgrad_workspace_bytes(n, (int)c_g, (int)c_x, dtype_code(x));
+    at::Tensor work = at::empty({(int64_t)std::max<size_t>(ws, 1)}, x.options().dtype(at::kByte));
+    check_status(svtad_linear_wgrad(g.data_ptr(), with_rows ? rows.data_ptr<int32_t>() : nullptr, x.data_ptr(),
+                                    out.data_ptr(), work.data_ptr(), ws, n, g.size(0), (int)c_g, (int)c_x,
+                                    dtype_code(x), stream_of(x)),
+                 "linear_wgrad");
+    return out;
+}
+
 PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.doc() = "MI355X (gfx950) SparseConv2D: drop-in for the reference opentad_sparse_ops";
     m.def("fwd", &op_fwd, "Forward", py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
@@ -695,5 +724,7 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.def("adapter_up", &op_adapter_up, "Adapter up_proj on cat(special, patch) * gamma + residual",
           py::arg("a_special"), py::arg("a_patch"), py::arg("weight"), py::arg("bias"), py::arg("gamma"),
           py::arg("residual"));
+    m.def("linear_wgrad", &op_linear_wgrad, "Linear-layer weight gradient g[rows]^T x (split rows, ordered sum)",
+          py::arg("g"), py::arg("rows"), py::arg("x"));
     m.def("version", []() { return std::string(svtad_version()); });
 }

@@ -284,6 +284,23 @@ int svtad_adapter_up(const void* a_special, const void* a_patch, const void* wei
                      int64_t batch, int64_t n_tokens, int64_t n_special, int k, int n, int dtype,
                      void* stream);
 
+/*
+ * A linear layer's weight gradient (the backward of the adapter's nn.Linear
+ * layers, vit_sparse_adapter_poguise.py:305,652; PyTorch computes it as
+ * grad_out^T @ input):
+ *   out[i, j] = sum_{r < n} g[rows[r], i] * x[r, j]     (fp32 accumulation)
+ * g has n_g_rows rows of c_g values (rows == NULL: row r of g, n_g_rows >= n),
+ * x is [n, c_x], out [c_g, c_x] in `dtype`. The sum runs over row splits
+ * whose fp32 partials (workspace, svtad_linear_wgrad_workspace_bytes) are
+ * added in a fixed order, so the result is deterministic. f16 / bf16; c_g
+ * and c_x need a tile configuration (multiples of 64 cover every case); g and
+ * x 16-byte aligned. Two launches on `stream`.
+ */
+size_t svtad_linear_wgrad_workspace_bytes(int64_t n, int c_g, int c_x, int dtype);
+int svtad_linear_wgrad(const void* g, const int32_t* rows, const void* x, void* out, void* workspace,
+                       size_t workspace_bytes, int64_t n, int64_t n_g_rows, int c_g, int c_x, int dtype,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

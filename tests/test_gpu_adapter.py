@@ -124,3 +124,32 @@ def test_fused_adapter_rejects_float32(dev):
     with pytest.raises(RuntimeError, match="float16 / bfloat16"):
         mod(x, 2, 2, torch.arange(4, device=dev).view(1, 4), 4, torch.zeros(4, 9, dtype=torch.int32, device=dev))
     assert math.isfinite(float(mod.gamma))
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("n,c_g,c_x,mapped", [
+    (17250, 256, 768, False), (17248, 768, 256, True), (1000, 64, 128, False), (77, 128, 64, True), (0, 256, 768, False),
+])
+def test_linear_wgrad(dev, dname, n, c_g, c_x, mapped):
+    """g[rows]^T x on the split-row kernel against an fp32 matmul (bar 1e-2)."""
+    import eccv26_tad_amd as sv
+
+    dt = getattr(torch, dname)
+    g_ = torch.Generator().manual_seed(n + c_g)
+    n_g = n + 3 if mapped else n
+    g = torch.randn(n_g, c_g, generator=g_).to(dev, dt)
+    x = torch.randn(n, c_x, generator=g_).to(dev, dt)
+    if mapped:
+        rows = torch.randperm(n_g, generator=g_)[:n].to(torch.int32).to(dev)
+        ref = g.float()[rows.long()].t() @ x.float()
+    else:
+        rows = torch.empty(0, dtype=torch.int32, device=dev)
+        ref = g.float().t() @ x.float()
+    print("linear_wgrad", dname, n, c_g, c_x, mapped, flush=True)
+    out = sv.ops.linear_wgrad(g, rows, x)
+    assert out.shape == (c_g, c_x) and out.dtype == dt
+    if n == 0:
+        assert torch.count_nonzero(out) == 0
+    else:
+        assert _err(out, ref) <= 1e-2
+        assert torch.equal(out, sv.ops.linear_wgrad(g, rows, x))  # deterministic
