@@ -254,6 +254,97 @@ def adapter_measure(dev, reps):
     return out
 
 
+def blob_mask(keep: float, seed: int = SEED + 1):
+    """[B, T, H, W] uint8 clustered keep mask: per frame a
+    score that is the sum of two isotropic 2D Gaussian blobs (sigma 2.5 cells,
+    centres drifting by a seeded random walk over the frames) plus 1e-3 U(0,1)
+    noise; per sample the top-k (k = ceil(keep * T*H*W)) of the score."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    ys = torch.arange(H).float().view(H, 1)
+    xs = torch.arange(W).float().view(1, W)
+    n = T * H * W
+    k = math.ceil(keep * n)
+    m = torch.zeros(B, n, dtype=torch.uint8)
+    for b in range(B):
+        c = torch.rand(2, 2, generator=g) * torch.tensor([H - 1.0, W - 1.0])
+        frames = []
+        for _ in range(T):
+            c = (c + torch.randn(2, 2, generator=g) * 0.7).clamp(min=0.0)
+            c[:, 0] = c[:, 0].clamp(max=H - 1.0)
+            c[:, 1] = c[:, 1].clamp(max=W - 1.0)
+            sc = sum(torch.exp(-((ys - c[j, 0]) ** 2 + (xs - c[j, 1]) ** 2) / (2 * 2.5 ** 2)) for j in range(2))
+            frames.append(sc + 1e-3 * torch.rand(H, W, generator=g))
+        score = torch.stack(frames).view(-1)
+        m[b, torch.topk(score, k).indices] = 1
+    return m.view(B, T, H, W)
+
+
+def depthwise_measure(dev, reps):
+    """depthwise (groups = C = 192) 3x3 SparseConv2D, fp16,
+    B2 x T80 x 14x14, clustered keep masks, fwd + bwd_in + bwd_w with bias (the
+    autograd step of SparseDepthwiseConv2d), at every keep rate. Algorithmic
+    bytes per step: the three passes each read their activation rows and the
+    table once and write their output once, plus weights."""
+    import torch
+
+    import eccv26_tad_amd as sv
+
+    ops = sv.ops
+    import torch.nn.functional as F
+
+    # dense comparator: grouped (depthwise) MIOpen conv2d fwd + input / weight
+    # / bias gradients on the full grid, best of NCHW and channels_last
+    torch.backends.cudnn.benchmark = True
+    gd = torch.Generator().manual_seed(SEED + 4)
+    dense = None
+    for fmt in (torch.contiguous_format, torch.channels_last):
+        xd = torch.randn(B * T, C, H, W, generator=gd).to(dev, torch.float16).contiguous(memory_format=fmt)
+        xd.requires_grad_(True)
+        wd = (torch.randn(C, 1, 3, 3, generator=gd) * 0.3).to(dev, torch.float16).requires_grad_(True)
+        bd = torch.zeros(C, device=dev, dtype=torch.float16, requires_grad=True)
+        dy = torch.randn(B * T, C, H, W, generator=gd).to(dev, torch.float16).contiguous(memory_format=fmt)
+
+        def run_dense():
+            y = F.conv2d(xd, wd, bd, padding=1, groups=C)
+            return torch.autograd.grad(y, (xd, wd, bd), dy)
+
+        td = time_events(run_dense, reps, warm=5)
+        dense = td if dense is None else min(dense, td)
+    rows = []
+    for kr in KEEPS:
+        mask = blob_mask(kr).to(dev)
+        table = sv.build_neighbor_table(mask)
+        n = int(table.shape[0])
+        g = torch.Generator().manual_seed(SEED + 3)
+        x = torch.randn(n, C, generator=g).to(dev, torch.float16)
+        w = (torch.rand(9, C, generator=g) * 2 - 1).div(3).to(dev, torch.float16)
+        b = (torch.rand(C, generator=g) * 0.2 - 0.1).to(dev, torch.float16)
+        go = torch.randn(n, C, generator=g).to(dev, torch.float16)
+        hit = float((table >= 0).sum()) / (9 * n)
+
+        def step():
+            y = ops.dw_fwd(x, table, w, b, 0)
+            gi = ops.dw_bwd_in(go, table, w, 0)
+            gw, gb = ops.dw_bwd_w(go, x, table, 0, True)
+            return y, gi, gw, gb
+
+        t = time_events(step, reps)
+        parts = {"fwd": lambda: ops.dw_fwd(x, table, w, b, 0), "bwd_in": lambda: ops.dw_bwd_in(go, table, w, 0),
+                 "bwd_w": lambda: ops.dw_bwd_w(go, x, table, 0, True)}
+        pt = {k2: round(time_events(f, reps) * 1e3, 2) for k2, f in parts.items()}
+        # fwd: x, y, table; bwd_in: go, gi, table; bwd_w: go, x, table; weights and bias
+        by = 3 * (2 * n * C * 2 + 36 * n) + 3 * 9 * C * 2 + 3 * C * 2
+        rows.append({"keep": kr, "n": n, "hit_rate": round(hit, 4), "us": round(t * 1e3, 2),
+                     "gbs": round(by / (t * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "pass_us": pt,
+                     "speedup_vs_dense": round(dense / t, 3)})
+        log(f"bench: depthwise {rows[-1]}")
+    return {"workload": f"depthwise 3x3, C={C} fp16, B{B} x T{T} x {H}x{W}, clustered (Gaussian-blob) keep masks",
+            "dense_us": round(dense * 1e3, 2), "sweep": rows}
+
+
 PRUNE_C = 768  # ViT-B token width, where the Block prune step runs
 
 
@@ -368,7 +459,7 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
-    ap.add_argument("--only", choices=("adapter", "prune"), default=None,
+    ap.add_argument("--only", choices=("adapter", "prune", "depthwise"), default=None,
                     help="only time the fused adapter or the prune step, print its JSON and exit "
                          "(for kernel traces of those paths)")
     args = ap.parse_args()
@@ -399,6 +490,9 @@ def main():
         return
     if args.only == "prune":
         print(json.dumps({"prune_step": prune_measure(dev, args.steps, False)}), flush=True)
+        return
+    if args.only == "depthwise":
+        print(json.dumps({"depthwise": depthwise_measure(dev, args.steps)}), flush=True)
         return
 
     log(f"bench: building problem keep={args.keep}")
@@ -512,6 +606,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     prune = None if args.no_sweep else prune_measure(dev, 20, not args.no_cpu)
     adapter = None if args.no_sweep else adapter_measure(dev, 20)
+    depthwise = None if args.no_sweep else depthwise_measure(dev, 20)
     if adapter is not None:
         log(f"bench: adapter {adapter}")
 
@@ -547,6 +642,7 @@ def main():
         "sweep": sweep,
         "prune_step": prune,
         "adapter": adapter,
+        "depthwise": depthwise,
     }
     print(json.dumps(out), flush=True)
 

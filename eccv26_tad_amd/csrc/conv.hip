@@ -71,9 +71,11 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
 static BwPlan plan_dw_bw(int64_t n, int c, int dtype) {
     BwPlan p;
     p.path = 0;
-    const int64_t cblocks = cdiv(c, 64);
-    int64_t splits = std::max<int64_t>(1, cdiv(1024, cblocks));
-    splits = std::min<int64_t>(splits, std::max<int64_t>(1, n / 64));
+    // about 64 rows per split, at most one split per CU: one workgroup of
+    // the vectorized kernel per split (it holds a CU alone), one per
+    // 64-channel block in the scalar one
+    (void)c;
+    int64_t splits = std::min<int64_t>(cu_count(), std::max<int64_t>(1, cdiv(n, 64)));
     int64_t rps = cdiv(std::max<int64_t>(n, 1), splits);
     rps = cdiv(rps, 4) * 4;
     splits = std::max<int64_t>(1, cdiv(n, rps));

@@ -5,6 +5,7 @@
 #include "sv_common.h"
 #include "sv_conv.h"
 #include "sv_internal.h"
+#include "sv_mfma.h"
 
 namespace svtad {
 
@@ -214,24 +215,41 @@ __global__ __launch_bounds__(256) void k_bw_valu(const T* __restrict__ go, const
 }
 
 // Ordered sum of the split partials, rounded once: out[e] = T(sum_s ws[s][e]).
+// out[e] = T(sum_s ws[s * stride + e]) for e < count0, out2[e - count0] for
+// count0 <= e < count (two outputs from one partial row, e.g. weight and
+// bias): a workgroup owns 64 outputs; its 16 groups of
+// 64 threads each sum a contiguous sixteenth of the splits (eight loads in
+// flight), and the 16 group sums are added in group order through LDS, so
+// the order of the sum is fixed.
 template <typename T, typename A>
-__global__ __launch_bounds__(256) void k_split_reduce(const A* __restrict__ ws, int64_t count,
-                                                      int splits, T* __restrict__ out) {
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < count;
-         e += (int64_t)gridDim.x * 256) {
-        // eight loads in flight at a time, summed in split order
-        A s = 0;
-        int q = 0;
-        for (; q + 8 <= splits; q += 8) {
+__global__ __launch_bounds__(1024) void k_split_reduce(const A* __restrict__ ws, int64_t count,
+                                                       int splits, T* __restrict__ out, int64_t stride,
+                                                       int64_t count0, T* __restrict__ out2) {
+    __shared__ A part[16][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int spt = (splits + 15) / 16;
+    const int q0 = min(splits, g * spt), q1 = min(splits, q0 + spt);
+    A s = 0;
+    if (e < count) {
+        int q = q0;
+        for (; q + 8 <= q1; q += 8) {
             A v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)(q + u) * count + e];
+            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)(q + u) * stride + e];
 #pragma unroll
             for (int u = 0; u < 8; ++u) s += v[u];
         }
-        for (; q < splits; ++q) s += ws[(int64_t)q * count + e];
-        out[e] = from_acc<T>(s);
+        for (; q < q1; ++q) s += ws[(int64_t)q * stride + e];
     }
+    part[g][lane] = s;
+    __syncthreads();
+    if (g != 0 || e >= count) return;
+    A t = part[0][lane];
+#pragma unroll
+    for (int h = 1; h < 16; ++h) t += part[h][lane];
+    if (e < count0) out[e] = from_acc<T>(t);
+    else out2[e - count0] = from_acc<T>(t);
 }
 
 // ---------------------------------------------------------------------------
@@ -303,8 +321,171 @@ __global__ __launch_bounds__(256) void k_dw_bw(const T* __restrict__ go, const T
 }
 
 // ---------------------------------------------------------------------------
+// Depthwise, vectorized (C a multiple of VEC = 16 / sizeof(T)): a thread owns
+// VEC consecutive channels (16 bytes) of one row. The 9 gathered 16-byte
+// loads are buffer loads whose offset is out of range for a missing neighbor
+// (they return zeros: no branch around a load), all in flight before the
+// first use; the row is written as one 16-byte store.
+// ---------------------------------------------------------------------------
+template <typename T> struct Vec16 {
+    static constexpr int N = 16 / (int)sizeof(T);
+    T e[N];
+};
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void k_dw_vec(const T* __restrict__ src, const int32_t* __restrict__ nbr,
+                                                const T* __restrict__ w, const T* __restrict__ bias,
+                                                T* __restrict__ out, int64_t n, int c, int64_t tpb) {
+    constexpr int VEC = Vec16<T>::N;
+    typedef typename Acc<T>::type A;
+    const int cpr = c / VEC;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n * cpr) return;
+    const int64_t i = e / cpr;
+    const int ch = (int)(e - i * cpr) * VEC;
+    const rsrc_t rs = make_rsrc(src, (uint32_t)(n * c * (int64_t)sizeof(T)));
+    uint32_t off[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const int64_t r = MODE == MODE_FWD ? src_row(nbr, i, k, n, tpb) : src_row_t(nbr, i, k, n, tpb);
+        off[k] = r >= 0 ? (uint32_t)((r * c + ch) * (int64_t)sizeof(T)) : kOOB;
+    }
+    u32x4 v[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) v[k] = bload16(rs, off[k]);
+    A acc[VEC];
+    if (bias) {
+        const Vec16<T> b = __builtin_bit_cast(Vec16<T>, *(const u32x4*)(bias + ch));
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] = to_acc<A>(b.e[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] = (A)0;
+    }
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        const Vec16<T> xv = __builtin_bit_cast(Vec16<T>, v[k]);
+        const Vec16<T> wv = __builtin_bit_cast(Vec16<T>, *(const u32x4*)(w + (int64_t)k * c + ch));
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[j] += to_acc<A>(xv.e[j]) * to_acc<A>(wv.e[j]);
+    }
+    Vec16<T> o;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) o.e[j] = from_acc<T>(acc[j]);
+    *(u32x4*)(out + i * c + ch) = __builtin_bit_cast(u32x4, o);
+}
+
+// ws[s][k][c] = sum over the rows i of split s of go[i,c] x[src(i,k),c] for
+// k < 9 and ws[s][9][c] = sum of go[i,c] (the bias; one partial row of 10 c
+// per split, reduced in one launch): one workgroup of 512 threads per split,
+// all channels. Thread (row lane rl, chunk q): R = 512 / cpr row lanes walk the
+// split's rows two at a time (rows rl + 2uR and rl + (2u+1)R: the table
+// reads and the 18 gathered loads of both are in flight together); each
+// thread keeps 10 x VEC sums, added over the row lanes in order 0 .. R-1
+// through LDS, five offsets at a time.
+template <typename T>
+__global__ __launch_bounds__(512) void k_dw_bw_vec(const T* __restrict__ go, const T* __restrict__ x,
+                                                   const int32_t* __restrict__ nbr,
+                                                   typename Acc<T>::type* __restrict__ ws, int64_t n, int c,
+                                                   int64_t tpb, int64_t rows_per_split) {
+    constexpr int VEC = Vec16<T>::N;
+    typedef typename Acc<T>::type A;
+    __shared__ __align__(16) A red[5 * 512 * VEC];
+    const int cpr = c / VEC, R = 512 / cpr;
+    const int tid = threadIdx.x, rl = tid / cpr, ch = (tid - rl * cpr) * VEC;
+    const bool active = rl < R;
+    const int s = blockIdx.x;
+    const int64_t r_begin = (int64_t)s * rows_per_split;
+    const int64_t r_end = min(n, r_begin + rows_per_split);
+    const rsrc_t rs = make_rsrc(x, (uint32_t)(n * c * (int64_t)sizeof(T)));
+    const rsrc_t rg = make_rsrc(go, (uint32_t)(n * c * (int64_t)sizeof(T)));
+    A acc[10][VEC];
+#pragma unroll
+    for (int k = 0; k < 10; ++k)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[k][j] = (A)0;
+    auto offs = [&](int64_t i, uint32_t* off) {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const int64_t r = i < r_end ? src_row(nbr, i, k, n, tpb) : -1;
+            off[k] = r >= 0 ? (uint32_t)((r * c + ch) * (int64_t)sizeof(T)) : kOOB;
+        }
+    };
+    auto add = [&](const u32x4& gv, const u32x4* v) {
+        const Vec16<T> g = __builtin_bit_cast(Vec16<T>, gv);
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[9][j] += to_acc<A>(g.e[j]);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            const Vec16<T> xv = __builtin_bit_cast(Vec16<T>, v[k]);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) acc[k][j] += to_acc<A>(g.e[j]) * to_acc<A>(xv.e[j]);
+        }
+    };
+    if (active) {
+        for (int64_t i = r_begin + rl; i < r_end; i += 2 * R) {
+            const int64_t i2 = i + R;  // may be past the split: zeros (go and x loads out of range)
+            uint32_t o1[9], o2[9];
+            offs(i, o1);
+            offs(i2, o2);
+            const u32x4 g1 = bload16(rg, (uint32_t)((i * c + ch) * (int64_t)sizeof(T)));
+            const u32x4 g2 = bload16(rg, i2 < r_end ? (uint32_t)((i2 * c + ch) * (int64_t)sizeof(T)) : kOOB);
+            u32x4 v1[9], v2[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) v1[k] = bload16(rs, o1[k]);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) v2[k] = bload16(rs, o2[k]);
+            add(g1, v1);
+            add(g2, v2);
+        }
+    }
+    // two rounds of five offsets (the bias is offset 9): row lane rl's sums
+    // of offset k0 + kk at red[(kk * R + rl) * c + channel]
+#pragma unroll
+    for (int k0 = 0; k0 < 10; k0 += 5) {
+        if (active) {
+#pragma unroll
+            for (int kk = 0; kk < 5; ++kk)
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) red[(kk * R + rl) * c + ch + j] = acc[k0 + kk][j];
+        }
+        __syncthreads();
+        // (offset, channel) pair p summed over the row lanes in order 0 .. R-1,
+        // eight LDS reads in flight at a time
+        for (int pi = tid; pi < 5 * c; pi += 512) {
+            const int kk = pi / c, t = pi - kk * c;
+            const A* col = red + (int64_t)kk * R * c + t;
+            A v = (A)0;
+            int q = 0;
+            for (; q + 8 <= R; q += 8) {
+                A u[8];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) u[h] = col[(q + h) * c];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) v += u[h];
+            }
+            for (; q < R; ++q) v += col[q * c];
+            const int k = k0 + kk;
+            ws[((int64_t)s * 10 + k) * c + t] = v;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
+
+static bool al16v(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// the vectorized depthwise kernels apply: whole 16-byte chunks per row, at
+// most 256 chunks per row, 32-bit buffer offsets, 16-byte aligned pointers
+template <typename T>
+static bool dw_vec_ok(int64_t n, int c, const void* a, const void* b, const void* d) {
+    constexpr int VEC = Vec16<T>::N;
+    return c % VEC == 0 && c / VEC <= 256 && n * c * (int64_t)sizeof(T) < (int64_t)INT32_MAX - 16 &&
+           al16v(a) && al16v(b) && (!d || al16v(d));
+}
 
 template <typename T> constexpr int dtype_of();
 template <> constexpr int dtype_of<float>() { return SVTAD_F32; }
@@ -316,9 +497,8 @@ template <typename T>
 static void launch_split_reduce(const void* part, int64_t count, int splits, void* out,
                                 hipStream_t s) {
     typedef typename Acc<T>::type A;
-    hipLaunchKernelGGL((k_split_reduce<T, A>),
-                       dim3((unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(count, 256), 4096))),
-                       dim3(256), 0, s, (const A*)part, count, splits, (T*)out);
+    hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, 64))),
+                       dim3(1024), 0, s, (const A*)part, count, splits, (T*)out, count, count, (T*)nullptr);
 }
 
 void split_reduce(int dtype, const void* part, int64_t count, int splits, void* out, hipStream_t s) {
@@ -409,6 +589,16 @@ void bw_valu(int dtype, const BwPlan& p, const void* go, const void* x, const in
 template <typename T>
 static void launch_dw(int mode, const void* src, const int32_t* nbr, const void* w,
                       const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s) {
+    if (dw_vec_ok<T>(n, c, src, w, out) && (!bias || al16v(bias))) {
+        const dim3 g((unsigned)cdiv(n * (c / Vec16<T>::N), 256));
+        if (mode == MODE_FWD)
+            hipLaunchKernelGGL((k_dw_vec<T, MODE_FWD>), g, dim3(256), 0, s, (const T*)src, nbr, (const T*)w,
+                               (const T*)bias, (T*)out, n, c, tpb);
+        else
+            hipLaunchKernelGGL((k_dw_vec<T, MODE_BWDIN>), g, dim3(256), 0, s, (const T*)src, nbr, (const T*)w,
+                               (const T*)nullptr, (T*)out, n, c, tpb);
+        return;
+    }
     dim3 grid((unsigned)cdiv(n * c, 256));
     if (mode == MODE_FWD)
         hipLaunchKernelGGL((k_dw_gather<T, MODE_FWD>), grid, dim3(256), 0, s, (const T*)src, nbr,
@@ -435,9 +625,19 @@ static void launch_dw_bw(const BwPlan& p, const void* go, const void* x, const i
     typedef typename Acc<T>::type A;
     A* part = (A*)ws;
     A* part_b = gb ? part + (int64_t)p.splits * 9 * c : nullptr;
-    dim3 grid((unsigned)cdiv(c, 64), (unsigned)p.splits);
-    hipLaunchKernelGGL((k_dw_bw<T>), grid, dim3(256), 0, s, (const T*)go, (const T*)x, nbr, part,
-                       part_b, n, c, tpb, p.rows_per_split);
+    if (dw_vec_ok<T>(n, c, go, x, nullptr)) {
+        hipLaunchKernelGGL((k_dw_bw_vec<T>), dim3((unsigned)p.splits), dim3(512), 0, s, (const T*)go,
+                           (const T*)x, nbr, part, n, c, tpb, p.rows_per_split);
+        const int64_t count = gb ? 10LL * c : 9LL * c;
+        hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, 64))),
+                           dim3(1024), 0, s, (const A*)part, count, p.splits, (T*)gw, 10LL * c, 9LL * c,
+                           (T*)gb);
+        return;
+    } else {
+        dim3 grid((unsigned)cdiv(c, 64), (unsigned)p.splits);
+        hipLaunchKernelGGL((k_dw_bw<T>), grid, dim3(256), 0, s, (const T*)go, (const T*)x, nbr, part,
+                           part_b, n, c, tpb, p.rows_per_split);
+    }
     split_reduce(dtype_of<T>(), part, 9LL * c, p.splits, gw, s);
     if (gb) split_reduce(dtype_of<T>(), part_b, (int64_t)c, p.splits, gb, s);
 }
