@@ -345,6 +345,60 @@ def depthwise_measure(dev, reps):
             "dense_us": round(dense * 1e3, 2), "sweep": rows}
 
 
+def large_channel_measure(dev, reps):
+    """BASELINE configs 4 and 5, the matrix-core path at large widths: the same
+    autograd step as config 2 (weight pack, forward with fp32 bias, combined
+    backward). Config 4: ViT-L adapter, C = 256 bf16, B2 x T96 x 16x16, top-k
+    keeps 10 / 25 / 55 %. Config 5: C = 512 bf16, B4 x T128 x 16x16, ragged
+    per-frame keeps ~ U(5 %, 15 %) (global table). Reported per case: step
+    µs and dense-K TFLOP/s (three GEMM passes of 2 * 9 * N * C^2) as a
+    fraction of the bf16 MFMA peak."""
+    import torch
+
+    import eccv26_tad_amd as sv
+
+    ops = sv.ops
+    out = []
+
+    def case(name, mask, c):
+        table = sv.build_neighbor_table(mask)
+        n = int(table.shape[0])
+        g = torch.Generator().manual_seed(SEED + 7)
+        bound = 1.0 / math.sqrt(9 * c)
+        x = torch.randn(n, c, generator=g).to(dev, torch.bfloat16)
+        w = ((torch.rand(9, c, c, generator=g) * 2 - 1) * bound).to(dev, torch.bfloat16)
+        b = ((torch.rand(c, generator=g) * 2 - 1) * bound).to(dev, torch.bfloat16)
+        go = torch.randn(n, c, generator=g).to(dev, torch.bfloat16)
+
+        def step():
+            pf, pb = ops.pack_weight(w, True, True)
+            y = ops.fwd_packed(x, table, w, pf, b, 0, 1)
+            return y, ops.bwd_packed(go, x, table, w, pb, c, 0, True)
+
+        t = time_events(step, reps)
+        f = 3 * 2 * 9 * n * c * c
+        row = {"config": name, "channels": c, "n": n, "us": round(t * 1e3, 2),
+               "tflops_9n": round(f / (t * 1e-3) / 1e12, 1),
+               "mfma_frac": round(f / (t * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4)}
+        out.append(row)
+        log(f"bench: large-channel {row}")
+
+    for kr in (0.10, 0.25, 0.55):
+        gm = torch.Generator().manual_seed(SEED + 2)
+        nc = 96 * 16 * 16
+        k = math.ceil(kr * nc)
+        m = torch.zeros(2, nc, dtype=torch.uint8)
+        m.scatter_(1, torch.topk(torch.rand(2, nc, generator=gm), k, dim=1).indices, 1)
+        case(f"c4 keep {kr}", m.view(2, 96, 16, 16).to(dev), 256)
+    gm = torch.Generator().manual_seed(SEED + 3)
+    m = torch.zeros(4 * 128, 256, dtype=torch.uint8)
+    for f in range(4 * 128):
+        kf = int(round(float(torch.empty(1).uniform_(0.05, 0.15, generator=gm)) * 256))
+        m[f, torch.randperm(256, generator=gm)[:kf]] = 1
+    case("c5 ragged 5-15 %", m.view(4, 128, 16, 16).to(dev), 512)
+    return out
+
+
 PRUNE_C = 768  # ViT-B token width, where the Block prune step runs
 
 
@@ -459,7 +513,7 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
-    ap.add_argument("--only", choices=("adapter", "prune", "depthwise"), default=None,
+    ap.add_argument("--only", choices=("adapter", "prune", "depthwise", "large"), default=None,
                     help="only time the fused adapter or the prune step, print its JSON and exit "
                          "(for kernel traces of those paths)")
     args = ap.parse_args()
@@ -493,6 +547,9 @@ def main():
         return
     if args.only == "depthwise":
         print(json.dumps({"depthwise": depthwise_measure(dev, args.steps)}), flush=True)
+        return
+    if args.only == "large":
+        print(json.dumps({"large_channel": large_channel_measure(dev, args.steps)}), flush=True)
         return
 
     log(f"bench: building problem keep={args.keep}")
@@ -607,6 +664,7 @@ def main():
     prune = None if args.no_sweep else prune_measure(dev, 20, not args.no_cpu)
     adapter = None if args.no_sweep else adapter_measure(dev, 20)
     depthwise = None if args.no_sweep else depthwise_measure(dev, 20)
+    large = None if args.no_sweep else large_channel_measure(dev, 10)
     if adapter is not None:
         log(f"bench: adapter {adapter}")
 
@@ -643,6 +701,7 @@ def main():
         "prune_step": prune,
         "adapter": adapter,
         "depthwise": depthwise,
+        "large_channel": large,
     }
     print(json.dumps(out), flush=True)
 

@@ -51,8 +51,26 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     const int64_t tiles = 9 * cdiv(c_in, tm) * cdiv(c_out, tn);
     int64_t splits;
     if (p.path) {
-        splits = std::max<int64_t>(cdiv(n, kMaxSplitRows - 128),
-                                   std::min<int64_t>(std::max<int64_t>(1, cu_count() / tiles), cdiv(n, 256)));
+        // Fewest workgroup rounds times the longest split, with a fixed cost
+        // per workgroup worth about 256 rows: splits of whole 128-row pairs of
+        // stages, at most kMaxSplitRows - 128 rows (the LDS row list), at
+        // least 256 rows where n allows. A partial second round costs a full
+        // round, so a count just above the CU count loses to twice as many
+        // half-length splits.
+        const int64_t cu = cu_count();
+        const int64_t s_min = std::max<int64_t>(1, cdiv(n, kMaxSplitRows - 128));
+        const int64_t s_cap = std::max<int64_t>(s_min, std::min<int64_t>(cdiv(n, 256), 4 * cu / tiles + 1));
+        splits = s_min;
+        int64_t best = INT64_MAX;
+        for (int64_t sc = s_min; sc <= s_cap; ++sc) {
+            const int64_t r = cdiv(cdiv(std::max<int64_t>(n, 1), sc), 128) * 128;
+            const int64_t se = std::max<int64_t>(1, cdiv(n, r));
+            const int64_t cost = cdiv(se * tiles, cu) * (r + 256);
+            if (cost < best) {
+                best = cost;
+                splits = se;
+            }
+        }
     } else {
         splits = std::min<int64_t>(cdiv(1024, tiles), std::max<int64_t>(1, n / 128));
     }

@@ -1334,8 +1334,11 @@ static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, 
                            uint32_t* flag, hipStream_t s) {
     const int n_col = (int)cdiv(n_out, 4 * FN * 16);
     if constexpr (CR == 192 || CR == 256) {
+        // at CR = 256, FM = 8 leaves room for one wave set only (one wave per
+        // SIMD); FM = 6 with two sets is faster even with a partial second
+        // round of workgroups
         static const int have[] = {1, 2, 3, 4, 5, 6, 8};
-        const int fm = pick_fm(n, n_col, have, 7);
+        const int fm = pick_fm(n, n_col, have, CR == 256 ? 6 : 7);
         if constexpr (CR == 192 && FN == 3) {
             // Few rows (one or two row fragments per full-width tile): 64-column
             // tiles of three row fragments instead. Each workgroup then streams

@@ -69,7 +69,7 @@ bool gg_mfma_packed_ok(int dtype, int64_t n, int c_red, int n_out);
 void pack_weight(const void* w, void* wf_fwd, void* wf_bwd, int c_in, int c_out, hipStream_t s);
 bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out);
 // Rows per split of the MFMA backward-weight (its row list lives in LDS).
-constexpr int kMaxSplitRows = 2048;
+constexpr int kMaxSplitRows = 4096;
 // compute units of the current device (256 on MI355X)
 int cu_count();
 int bw_mfma_tile(int c);
