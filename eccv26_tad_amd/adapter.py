@@ -32,7 +32,8 @@ the input gradients use library GEMMs (``torch.matmul``) and PyTorch's own
 GELU backward. ``gamma``'s gradient needs ``z = cat(...) W_u^T + b_u``, which
 the fused forward never stores: ``sum(go * z) = <W_u, go^T c> + <b_u,
 sum(go)>``, and ``go^T c`` is the up-projection's weight-gradient reduction
-anyway.
+anyway. The bias gradients (column sums over the token rows) use
+``opentad_sparse_ops.column_sums``.
 
 The fused path takes float16 / bfloat16 (the matrix-core dtypes) and raises
 otherwise; ``reference_forward`` runs the unfused chain in the reference's op
@@ -53,10 +54,11 @@ _FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
 
 def _colsum(a):
-    """Column sums of a [rows, n] matrix as a ones-vector GEMM (fp32
-    accumulation, result in a's dtype): one library GEMM, where a dim-0
-    reduction over 17k rows is several times slower."""
-    return torch.matmul(torch.ones(1, a.shape[0], device=a.device, dtype=a.dtype), a).view(-1)
+    """Column sums of a [rows, n] matrix (the Linear bias gradients): fp32
+    accumulation over row splits added in a fixed order, result in a's
+    dtype. PyTorch's dim-0 reduction and a ones-vector GEMM take 24 and 58 µs
+    at 17250 x 768."""
+    return _ops.column_sums(a)
 
 
 def _NO_ROWS(like):

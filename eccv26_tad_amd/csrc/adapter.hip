@@ -270,6 +270,42 @@ static void launch_adapter(const void* a0, const void* a1, const void* w, const 
     else launch_tiles<T, EPI, 2, 32, 2>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, s);
 }
 
+// Column sums out[c] = sum_r a[r][c] (the bias gradients of the adapter's
+// Linear layers), deterministic: a workgroup owns 64 columns (8 per thread,
+// 16-byte loads) of one row split; 32 row lanes walk the split's rows and
+// are added in order through LDS into part[split][c]; split_reduce adds the
+// splits in order.
+constexpr int kColRowsPerSplit = 512;
+template <typename T>
+__global__ __launch_bounds__(256) void k_colsum_part(const T* __restrict__ a, float* __restrict__ part,
+                                                     int64_t rows, int cols, int n_col_blocks) {
+    __shared__ float red[32][64 + 4];
+    const int tid = threadIdx.x, cl = tid & 7, rl = tid >> 3;
+    const int cb = blockIdx.x % n_col_blocks, sp = blockIdx.x / n_col_blocks;
+    const int c0 = cb * 64 + cl * 8;
+    const int64_t r0 = (int64_t)sp * kColRowsPerSplit, r1 = min(rows, r0 + kColRowsPerSplit);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (c0 < cols) {
+        for (int64_t r = r0 + rl; r < r1; r += 32) {
+            const u32x4 v = *(const u32x4*)(a + r * cols + c0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[2 * q] += (float)__builtin_bit_cast(T, (u16)(v[q] & 0xffffu));
+                acc[2 * q + 1] += (float)__builtin_bit_cast(T, (u16)(v[q] >> 16));
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) red[rl][cl * 8 + j] = acc[j];
+    __syncthreads();
+    if (tid < 64 && cb * 64 + tid < cols) {
+        float v = 0.f;
+#pragma unroll 8
+        for (int q = 0; q < 32; ++q) v += red[q][tid];
+        part[(int64_t)sp * cols + cb * 64 + tid] = v;
+    }
+}
+
 }  // namespace svtad
 
 using namespace svtad;
@@ -348,5 +384,35 @@ extern "C" int svtad_linear_wgrad(const void* g, const int32_t* rows, const void
     if (workspace_bytes < p.ws_bytes)
         return set_error(SVTAD_ERR_WORKSPACE, "linear_wgrad: workspace smaller than svtad_linear_wgrad_workspace_bytes()");
     wgrad_mfma(dtype, p, g, rows, x, out, workspace, n, rows ? n_g_rows : n, c_g, c_x, (hipStream_t)stream);
+    return launch_status();
+}
+
+extern "C" size_t svtad_column_sums_workspace_bytes(int64_t rows, int cols, int dtype) {
+    (void)dtype;
+    if (rows < 0 || cols <= 0) return 0;
+    return (size_t)std::max<int64_t>(1, cdiv(rows, kColRowsPerSplit)) * cols * sizeof(float);
+}
+
+extern "C" int svtad_column_sums(const void* a, void* out, void* workspace, size_t workspace_bytes, int64_t rows,
+                                 int cols, int dtype, void* stream) {
+    if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "column_sums: needs f16/bf16");
+    if (rows < 0 || cols <= 0 || cols % 8 != 0)
+        return set_error(SVTAD_ERR_INVALID, "column_sums: needs rows >= 0 and cols a positive multiple of 8");
+    if (!out || !workspace || (rows > 0 && !a))
+        return set_error(SVTAD_ERR_INVALID, "column_sums: null pointer");
+    if (a && !al16(a)) return set_error(SVTAD_ERR_INVALID, "column_sums: a needs 16-byte alignment");
+    const int64_t splits = std::max<int64_t>(1, cdiv(rows, kColRowsPerSplit));
+    if (workspace_bytes < (size_t)splits * cols * sizeof(float))
+        return set_error(SVTAD_ERR_WORKSPACE, "column_sums: workspace smaller than svtad_column_sums_workspace_bytes()");
+    hipStream_t s = (hipStream_t)stream;
+    const int ncb = (cols + 63) / 64;
+    if (dtype == SVTAD_F16)
+        hipLaunchKernelGGL((k_colsum_part<f16>), dim3((unsigned)(ncb * splits)), dim3(256), 0, s, (const f16*)a,
+                           (float*)workspace, rows, cols, ncb);
+    else
+        hipLaunchKernelGGL((k_colsum_part<bf16>), dim3((unsigned)(ncb * splits)), dim3(256), 0, s, (const bf16*)a,
+                           (float*)workspace, rows, cols, ncb);
+    split_reduce(dtype, workspace, cols, (int)splits, out, s);
     return launch_status();
 }

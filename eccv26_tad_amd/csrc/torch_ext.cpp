@@ -664,6 +664,21 @@ at::Tensor op_linear_wgrad(const at::Tensor& g_in, const at::Tensor& rows_in, co
     return out;
 }
 
+// column_sums(a [rows, cols]) -> [cols]: sum over rows, fp32 accumulation, ordered
+at::Tensor op_column_sums(const at::Tensor& a_in) {
+    adapter_common(a_in, a_in, "a");
+    at::Tensor a = a_in.contiguous();
+    const int64_t rows = a.size(0), cols = a.size(1);
+    c10::DeviceGuard guard(a.device());
+    at::Tensor out = at::empty({cols}, a.options());
+    const size_t ws = svtad_column_sums_workspace_bytes(rows, (int)cols, dtype_code(a));
+    at::Tensor work = at::empty({(int64_t)std::max<size_t>(ws, 1)}, a.options().dtype(at::kByte));
+    check_status(svtad_column_sums(a.data_ptr(), out.data_ptr(), work.data_ptr(), ws, rows, (int)cols,
+                                   dtype_code(a), stream_of(a)),
+                 "column_sums");
+    return out;
+}
+
 PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.doc() = "MI355X (gfx950) SparseConv2D: drop-in for the reference opentad_sparse_ops";
     m.def("fwd", &op_fwd, "Forward", py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
@@ -726,5 +741,7 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("residual"));
     m.def("linear_wgrad", &op_linear_wgrad, "Linear-layer weight gradient g[rows]^T x (split rows, ordered sum)",
           py::arg("g"), py::arg("rows"), py::arg("x"));
+    m.def("column_sums", &op_column_sums, "Column sums of a [rows, cols] matrix (ordered, fp32 accumulation)",
+          py::arg("a"));
     m.def("version", []() { return std::string(svtad_version()); });
 }

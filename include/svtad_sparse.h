@@ -301,6 +301,16 @@ int svtad_linear_wgrad(const void* g, const int32_t* rows, const void* x, void* 
                        size_t workspace_bytes, int64_t n, int64_t n_g_rows, int c_g, int c_x, int dtype,
                        void* stream);
 
+/*
+ * Column sums out[c] = sum_r a[r, c] of a [rows, cols] matrix (the bias
+ * gradient of a linear layer, vit_sparse_adapter_poguise.py:305,652), fp32
+ * accumulation over 512-row splits added in a fixed order; out in `dtype`.
+ * f16 / bf16, cols % 8 == 0, a 16-byte aligned. Two launches on `stream`.
+ */
+size_t svtad_column_sums_workspace_bytes(int64_t rows, int cols, int dtype);
+int svtad_column_sums(const void* a, void* out, void* workspace, size_t workspace_bytes, int64_t rows, int cols,
+                      int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -164,7 +164,7 @@ def test_extension_module_api():
     for name in ("fwd_bias", "bwd_w_bias", "dw_fwd", "dw_bwd_in", "dw_bwd_w",
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
                  "validate_neighbor_table", "prune_tokens", "bwd_packed", "adapter_down",
-                 "adapter_up"):
+                 "adapter_up", "linear_wgrad", "column_sums"):
         assert hasattr(ops, name)
     import torch
 

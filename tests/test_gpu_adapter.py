@@ -153,3 +153,21 @@ def test_linear_wgrad(dev, dname, n, c_g, c_x, mapped):
     else:
         assert _err(out, ref) <= 1e-2
         assert torch.equal(out, sv.ops.linear_wgrad(g, rows, x))  # deterministic
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("rows,cols", [(17250, 768), (17248, 256), (513, 64), (1, 8), (0, 16)])
+def test_column_sums(dev, dname, rows, cols):
+    """Ordered column sums against an fp32 sum (bar 1e-2, max-scaled)."""
+    import eccv26_tad_amd as sv
+
+    dt = getattr(torch, dname)
+    a = torch.randn(rows, cols, generator=torch.Generator().manual_seed(rows + cols)).to(dev, dt)
+    out = sv.ops.column_sums(a)
+    assert out.shape == (cols,) and out.dtype == dt
+    ref = a.float().sum(0)
+    if rows == 0:
+        assert torch.count_nonzero(out) == 0
+    else:
+        assert _err(out, ref) <= 1e-2
+        assert torch.equal(out, sv.ops.column_sums(a))
