@@ -1,6 +1,6 @@
 """SparseConv2D fwd+bwd benchmark on one MI355X.
 
-Workload (the ViT-B adapter bottleneck): B=2 samples x 80
+Workload (benchmark config 2, the ViT-B adapter bottleneck): B=2 samples x 80
 temporal slices x 14x14 grid, C_in = C_out = 192, fp16, 3x3 sparse conv with
 bias. Keep sets: per sample top-k of a seeded U(0,1) score (k = ceil(r*15680)),
 sorted; the neighbor table is built on the GPU from the keep mask.
@@ -255,7 +255,7 @@ def adapter_measure(dev, reps):
 
 
 def blob_mask(keep: float, seed: int = SEED + 1):
-    """[B, T, H, W] uint8 clustered keep mask: per frame a
+    """[B, T, H, W] uint8 clustered keep mask (benchmark config 3): per frame a
     score that is the sum of two isotropic 2D Gaussian blobs (sigma 2.5 cells,
     centres drifting by a seeded random walk over the frames) plus 1e-3 U(0,1)
     noise; per sample the top-k (k = ceil(keep * T*H*W)) of the score."""
@@ -282,7 +282,7 @@ def blob_mask(keep: float, seed: int = SEED + 1):
 
 
 def depthwise_measure(dev, reps):
-    """depthwise (groups = C = 192) 3x3 SparseConv2D, fp16,
+    """benchmark config 3: depthwise (groups = C = 192) 3x3 SparseConv2D, fp16,
     B2 x T80 x 14x14, clustered keep masks, fwd + bwd_in + bwd_w with bias (the
     autograd step of SparseDepthwiseConv2d), at every keep rate. Algorithmic
     bytes per step: the three passes each read their activation rows and the
@@ -346,7 +346,7 @@ def depthwise_measure(dev, reps):
 
 
 def large_channel_measure(dev, reps):
-    """BASELINE configs 4 and 5, the matrix-core path at large widths: the same
+    """Benchmark configs 4 and 5, the matrix-core path at large widths: the same
     autograd step as config 2 (weight pack, forward with fp32 bias, combined
     backward). Config 4: ViT-L adapter, C = 256 bf16, B2 x T96 x 16x16, top-k
     keeps 10 / 25 / 55 %. Config 5: C = 512 bf16, B4 x T128 x 16x16, ragged
@@ -682,7 +682,7 @@ def main():
         "vs_baseline": None,
         "dtype": dname,
         "data": "synthetic (seeded top-k keep masks, N(0,1) activations, uniform weights)",
-        "config": {"workload": "SparseConv2D fwd+bwd, ViT-B adapter bottleneck (BASELINE config 2)",
+        "config": {"workload": "SparseConv2D fwd+bwd, ViT-B adapter bottleneck (benchmark config 2)",
                    "grid": f"B{B} x T{T} x {H}x{W}", "channels": C, "keep": args.keep, "n_kept": n,
                    "hit_rate": round(prob.valid / (9 * n), 4), "bias": True},
         "hbm_frac": round(total_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
