@@ -28,12 +28,14 @@ The backward's weight gradients (sums over every token row) run on the
 split-row kernel of SparseConv2D's backward-weight pass with one offset
 (``opentad_sparse_ops.linear_wgrad``: deterministic, and a grid that fills the
 chip where a library GEMM with a 17k-long reduction gets a dozen workgroups);
-the input gradients use library GEMMs (``torch.matmul``) and PyTorch's own
-GELU backward. ``gamma``'s gradient needs ``z = cat(...) W_u^T + b_u``, which
-the fused forward never stores: ``sum(go * z) = <W_u, go^T c> + <b_u,
-sum(go)>``, and ``go^T c`` is the up-projection's weight-gradient reduction
-anyway. The bias gradients (column sums over the token rows) use
-``opentad_sparse_ops.column_sums``.
+the input gradients use library GEMMs (``torch.matmul``). The GELU backward
+reads the special-token and patch-token gradients in place of their
+concatenation (``opentad_sparse_ops.gelu_backward_split``). ``gamma``'s
+gradient needs ``z = cat(...) W_u^T + b_u``, which the fused forward never
+stores: ``sum(go * z) = <W_u, go^T c> + <b_u, sum(go)>``, and ``go^T c`` is
+the up-projection's weight-gradient reduction anyway; one launch adds both
+products (``opentad_sparse_ops.gamma_grad``). The bias gradients (column sums
+over the token rows) use ``opentad_sparse_ops.column_sums``.
 
 The fused path takes float16 / bfloat16 (the matrix-core dtypes) and raises
 otherwise; ``reference_forward`` runs the unfused chain in the reference's op
@@ -66,6 +68,25 @@ def _NO_ROWS(like):
     return torch.empty(0, dtype=torch.int32, device=like.device)
 
 
+_PATCH_ROWS = {}
+
+
+def _patch_rows(B, N, S, device):
+    """Row of ``go.reshape(B * N, -1)`` for each patch token in the order of
+    the SparseConv2D rows (``b * N + S + r``), cached per shape and device:
+    built on every backward it costs five small integer kernels."""
+    key = (B, N, S, device)
+    rows = _PATCH_ROWS.get(key)
+    if rows is None:
+        P = N - S
+        r = torch.arange(B * P, device=device, dtype=torch.int32)
+        rows = (r // P) * N + S + r % P
+        if len(_PATCH_ROWS) >= 64:
+            _PATCH_ROWS.clear()
+        _PATCH_ROWS[key] = rows
+    return rows
+
+
 class AdapterDownFunction(Function):
     """``(act_special, act_patch) = split(GELU(x W^T + b))``; x ``[B, N, k]``."""
 
@@ -80,18 +101,9 @@ class AdapterDownFunction(Function):
     @staticmethod
     def backward(ctx, g_sp, g_pa):
         x, weight, pre = ctx.saved_tensors
-        B, N, n = pre.shape
-        S = ctx.n_special
-        dg = torch.empty_like(pre)
-        if g_sp is None:
-            dg[:, :S].zero_()
-        else:
-            dg[:, :S] = g_sp
-        if g_pa is None:
-            dg[:, S:].zero_()
-        else:
-            dg[:, S:] = g_pa.reshape(B, N - S, n)
-        du = torch.ops.aten.gelu_backward(dg, pre)
+        n = pre.shape[-1]
+        # GELU backward straight from the two gradient buffers (no assembled dg)
+        du = _ops.gelu_backward_split(g_sp, g_pa, pre, ctx.n_special)
         du2 = du.reshape(-1, n)
         gx = torch.matmul(du, weight) if ctx.needs_input_grad[0] else None
         gw = _ops.linear_wgrad(du2, _NO_ROWS(du2), x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
@@ -120,20 +132,15 @@ class AdapterUpFunction(Function):
         # on the split-row kernel (rows of go picked by a row list), the few
         # special rows as a small GEMM
         if S > 0:
-            P = N - S
-            r = torch.arange(B * P, device=go.device, dtype=torch.int32)
-            rows = (r // P) * N + S + r % P
-            G = _ops.linear_wgrad(go2, rows, a_pa)
+            G = _ops.linear_wgrad(go2, _patch_rows(B, N, S, go.device), a_pa)
             G = G + torch.matmul(go[:, :S].reshape(-1, n).t(), a_sp.reshape(-1, k))
         else:
             G = _ops.linear_wgrad(go2, _NO_ROWS(go2), a_pa)
         gsum = _colsum(go2)
         g_gamma = None
         if ctx.needs_input_grad[4]:
-            s = (weight.float() * G.float()).sum()
-            if bias is not None:
-                s = s + (bias.float() * gsum.float()).sum()
-            g_gamma = s.reshape(1).to(gamma.dtype)
+            g_gamma = _ops.gamma_grad(weight, G, bias, gsum if bias is not None else None)
+            g_gamma = g_gamma.view(gamma.shape).to(gamma.dtype)
         g_sp = g_pa = None
         if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
             # (go * gamma) W = go (gamma W): gamma folded into the small weight

@@ -306,6 +306,84 @@ __global__ __launch_bounds__(256) void k_colsum_part(const T* __restrict__ a, fl
     }
 }
 
+// GELU backward (erf form) of the down projection, with the incoming gradient
+// read from the special-token and patch-token gradient buffers in place of
+// their concatenation (the dg assembly of the unfused chain):
+//   grad_pre[m][c] = g(m, c) * (Phi(u) + u * phi(u)),  u = pre[m][c],
+// evaluated in fp32 and rounded once, the derivative of x * Phi(x) that the
+// reference's nn.GELU backward takes (vit_sparse_adapter_poguise.py:305-306). A
+// missing gradient buffer counts as zeros. One thread per 8 elements.
+template <typename T>
+__global__ __launch_bounds__(256) void k_gelu_bwd_split(const T* __restrict__ g_sp, const T* __restrict__ g_pa,
+                                                        const T* __restrict__ pre, T* __restrict__ out,
+                                                        int total_chunks, int cpr, int n, RowMap rm) {
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    if (e >= total_chunks) return;
+    const int m = e / cpr, q = e - m * cpr;
+    bool special;
+    const int64_t r = rm.split(m, special);
+    const T* const gsrc = special ? g_sp : g_pa;
+    const u32x4 u = *(const u32x4*)(pre + (int64_t)m * n + q * 8);
+    const u32x4 gv = gsrc ? *(const u32x4*)(gsrc + r * n + q * 8) : u32x4{0u, 0u, 0u, 0u};
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        unsigned packed = 0;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const float x = (float)__builtin_bit_cast(T, (u16)(u[h] >> (16 * j)));
+            const float dy = (float)__builtin_bit_cast(T, (u16)(gv[h] >> (16 * j)));
+            const float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+            const float pdf = expf(-0.5f * x * x) * 0.39894228040143268f;  // 1 / sqrt(2 pi)
+            packed |= (unsigned)__builtin_bit_cast(u16, (T)(dy * (cdf + x * pdf))) << (16 * j);
+        }
+        o[h] = packed;
+    }
+    *(u32x4*)(out + (int64_t)m * n + q * 8) = o;
+}
+
+// out[0] = T(sum_i w[i] g[i] + sum_j b[j] gs[j]) in fp32: the gradient of
+// gamma in (c W^T + b) * gamma (vit_sparse_adapter_poguise.py:652-653), which is
+// sum(go * z) = <W, go^T c> + <b, column sums of go>. One workgroup; thread t
+// owns the 8-element chunks t, t + 1024, ... and the per-thread sums are
+// added by a fixed tree, so the result is deterministic.
+template <typename T>
+__global__ __launch_bounds__(1024) void k_gamma_grad(const T* __restrict__ w, const T* __restrict__ g,
+                                                     int64_t chunks, const T* __restrict__ b,
+                                                     const T* __restrict__ gs, int64_t chunks_b,
+                                                     T* __restrict__ out) {
+    __shared__ float red[1024];
+    const int tid = threadIdx.x;
+    float acc = 0.f;
+    auto dot8 = [&](const u32x4 a, const u32x4 c) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            acc += (float)__builtin_bit_cast(T, (u16)(a[h] & 0xffffu)) * (float)__builtin_bit_cast(T, (u16)(c[h] & 0xffffu));
+            acc += (float)__builtin_bit_cast(T, (u16)(a[h] >> 16)) * (float)__builtin_bit_cast(T, (u16)(c[h] >> 16));
+        }
+    };
+    int64_t c = tid;
+    for (; c + 3 * 1024 < chunks; c += 4 * 1024) {
+        u32x4 a[4], v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            a[u] = *(const u32x4*)(w + (c + u * 1024) * 8);
+            v[u] = *(const u32x4*)(g + (c + u * 1024) * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) dot8(a[u], v[u]);
+    }
+    for (; c < chunks; c += 1024) dot8(*(const u32x4*)(w + c * 8), *(const u32x4*)(g + c * 8));
+    for (int64_t cb = tid; cb < chunks_b; cb += 1024) dot8(*(const u32x4*)(b + cb * 8), *(const u32x4*)(gs + cb * 8));
+    red[tid] = acc;
+    __syncthreads();
+    for (int h = 512; h > 0; h >>= 1) {
+        if (tid < h) red[tid] += red[tid + h];
+        __syncthreads();
+    }
+    if (tid == 0) out[0] = (T)red[0];
+}
+
 }  // namespace svtad
 
 using namespace svtad;
@@ -414,5 +492,55 @@ extern "C" int svtad_column_sums(const void* a, void* out, void* workspace, size
         hipLaunchKernelGGL((k_colsum_part<bf16>), dim3((unsigned)(ncb * splits)), dim3(256), 0, s, (const bf16*)a,
                            (float*)workspace, rows, cols, ncb);
     split_reduce(dtype, workspace, cols, (int)splits, out, s);
+    return launch_status();
+}
+
+extern "C" int svtad_gelu_backward_split(const void* grad_special, const void* grad_patch, const void* pre_act,
+                                         void* grad_pre, int64_t batch, int64_t n_tokens, int64_t n_special,
+                                         int n, int dtype, void* stream) {
+    if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "gelu_backward_split: needs f16/bf16");
+    if (batch < 0 || n_tokens < 0 || n_special < 0 || n_special > n_tokens || n <= 0 || n % 8 != 0)
+        return set_error(SVTAD_ERR_INVALID, "gelu_backward_split: needs 0 <= n_special <= n_tokens and n % 8 == 0");
+    const int64_t rows = batch * n_tokens;
+    if (rows == 0) return SVTAD_OK;
+    if (rows * (int64_t)n >= (int64_t)INT32_MAX)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "gelu_backward_split: 2^31 elements or more");
+    if (!pre_act || !grad_pre) return set_error(SVTAD_ERR_INVALID, "gelu_backward_split: null pointer");
+    if (!al16(pre_act) || !al16(grad_pre) || (grad_special && !al16(grad_special)) ||
+        (grad_patch && !al16(grad_patch)))
+        return set_error(SVTAD_ERR_INVALID, "gelu_backward_split: buffers need 16-byte alignment");
+    const RowMap rm{n_tokens, n_special, n_tokens - n_special};
+    const int cpr = n / 8;
+    const int total = (int)(rows * cpr);
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid((unsigned)cdiv(total, 256));
+    if (dtype == SVTAD_F16)
+        hipLaunchKernelGGL((k_gelu_bwd_split<f16>), grid, dim3(256), 0, s, (const f16*)grad_special,
+                           (const f16*)grad_patch, (const f16*)pre_act, (f16*)grad_pre, total, cpr, n, rm);
+    else
+        hipLaunchKernelGGL((k_gelu_bwd_split<bf16>), grid, dim3(256), 0, s, (const bf16*)grad_special,
+                           (const bf16*)grad_patch, (const bf16*)pre_act, (bf16*)grad_pre, total, cpr, n, rm);
+    return launch_status();
+}
+
+extern "C" int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,
+                                int64_t count_b, void* out, int dtype, void* stream) {
+    if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "gamma_grad: needs f16/bf16");
+    if (count < 0 || count_b < 0 || count % 8 != 0 || count_b % 8 != 0 || (!b != !gs))
+        return set_error(SVTAD_ERR_INVALID, "gamma_grad: counts must be multiples of 8; b and gs go together");
+    if (!out || (count > 0 && (!w || !g)) || (count_b > 0 && !b))
+        return set_error(SVTAD_ERR_INVALID, "gamma_grad: null pointer");
+    if ((w && !al16(w)) || (g && !al16(g)) || (b && !al16(b)) || (gs && !al16(gs)))
+        return set_error(SVTAD_ERR_INVALID, "gamma_grad: inputs need 16-byte alignment");
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t nb = b ? count_b / 8 : 0;
+    if (dtype == SVTAD_F16)
+        hipLaunchKernelGGL((k_gamma_grad<f16>), dim3(1), dim3(1024), 0, s, (const f16*)w, (const f16*)g, count / 8,
+                           (const f16*)b, (const f16*)gs, nb, (f16*)out);
+    else
+        hipLaunchKernelGGL((k_gamma_grad<bf16>), dim3(1), dim3(1024), 0, s, (const bf16*)w, (const bf16*)g,
+                           count / 8, (const bf16*)b, (const bf16*)gs, nb, (bf16*)out);
     return launch_status();
 }

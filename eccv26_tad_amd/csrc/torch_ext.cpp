@@ -679,6 +679,68 @@ at::Tensor op_column_sums(const at::Tensor& a_in) {
     return out;
 }
 
+// gelu_backward_split(grad_special [B, S, n] or None, grad_patch [B * (N - S), n] or None,
+//                     pre_act [B, N, n], n_special) -> grad_pre [B, N, n]
+at::Tensor op_gelu_backward_split(const c10::optional<at::Tensor>& g_sp, const c10::optional<at::Tensor>& g_pa,
+                                  const at::Tensor& pre_in, int64_t n_special) {
+    check_gpu(pre_in, "pre_act");
+    TORCH_CHECK(pre_in.scalar_type() == at::kHalf || pre_in.scalar_type() == at::kBFloat16,
+                "gelu_backward_split takes float16 / bfloat16, got ", pre_in.scalar_type());
+    TORCH_CHECK(pre_in.dim() == 3, "pre_act must be [B, N, n]");
+    const int64_t B = pre_in.size(0), N = pre_in.size(1), n = pre_in.size(2);
+    TORCH_CHECK(n_special >= 0 && n_special <= N, "n_special out of range");
+    at::Tensor pre = pre_in.contiguous(), sp, pa;
+    if (g_sp.has_value() && g_sp->defined() && g_sp->numel() > 0) {
+        check_gpu(*g_sp, "grad_special");
+        TORCH_CHECK(g_sp->scalar_type() == pre.scalar_type() && g_sp->numel() == B * n_special * n,
+                    "grad_special must be [B, S, n] of the pre_act dtype");
+        sp = g_sp->contiguous();
+    }
+    if (g_pa.has_value() && g_pa->defined() && g_pa->numel() > 0) {
+        check_gpu(*g_pa, "grad_patch");
+        TORCH_CHECK(g_pa->scalar_type() == pre.scalar_type() && g_pa->numel() == B * (N - n_special) * n,
+                    "grad_patch must be [B * (N - S), n] of the pre_act dtype");
+        pa = g_pa->contiguous();
+    }
+    c10::DeviceGuard g(pre.device());
+    at::Tensor out = at::empty_like(pre);
+    check_status(svtad_gelu_backward_split(sp.defined() ? sp.data_ptr() : nullptr,
+                                           pa.defined() ? pa.data_ptr() : nullptr, pre.data_ptr(),
+                                           out.data_ptr(), B, N, n_special, (int)n, dtype_code(pre),
+                                           stream_of(pre)),
+                 "gelu_backward_split");
+    return out;
+}
+
+// gamma_grad(w, g, b or None, gs or None) -> [1]: sum(w * g) + sum(b * gs), fp32, ordered
+at::Tensor op_gamma_grad(const at::Tensor& w_in, const at::Tensor& g_in, const c10::optional<at::Tensor>& b_in,
+                         const c10::optional<at::Tensor>& gs_in) {
+    check_gpu(w_in, "w");
+    check_gpu(g_in, "g");
+    TORCH_CHECK(w_in.scalar_type() == g_in.scalar_type(), "w and g dtypes differ");
+    TORCH_CHECK(w_in.scalar_type() == at::kHalf || w_in.scalar_type() == at::kBFloat16,
+                "gamma_grad takes float16 / bfloat16, got ", w_in.scalar_type());
+    TORCH_CHECK(w_in.numel() == g_in.numel(), "w and g must have the same size");
+    at::Tensor w = w_in.contiguous(), g = g_in.contiguous(), b, gs;
+    if (bias_present(b_in)) {
+        TORCH_CHECK(gs_in.has_value() && gs_in->defined() && gs_in->numel() == b_in->numel(),
+                    "gs must match b");
+        check_gpu(*b_in, "b");
+        check_gpu(*gs_in, "gs");
+        TORCH_CHECK(b_in->scalar_type() == w.scalar_type() && gs_in->scalar_type() == w.scalar_type(),
+                    "b and gs must have the dtype of w");
+        b = b_in->contiguous();
+        gs = gs_in->contiguous();
+    }
+    c10::DeviceGuard guard(w.device());
+    at::Tensor out = at::empty({1}, w.options());
+    check_status(svtad_gamma_grad(w.data_ptr(), g.data_ptr(), w.numel(), b.defined() ? b.data_ptr() : nullptr,
+                                  gs.defined() ? gs.data_ptr() : nullptr, b.defined() ? b.numel() : 0,
+                                  out.data_ptr(), dtype_code(w), stream_of(w)),
+                 "gamma_grad");
+    return out;
+}
+
 PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.doc() = "MI355X (gfx950) SparseConv2D: drop-in for the reference opentad_sparse_ops";
     m.def("fwd", &op_fwd, "Forward", py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
@@ -743,5 +805,10 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("g"), py::arg("rows"), py::arg("x"));
     m.def("column_sums", &op_column_sums, "Column sums of a [rows, cols] matrix (ordered, fp32 accumulation)",
           py::arg("a"));
+    m.def("gelu_backward_split", &op_gelu_backward_split,
+          "GELU backward of the adapter's down projection from split special / patch gradients",
+          py::arg("grad_special"), py::arg("grad_patch"), py::arg("pre_act"), py::arg("n_special"));
+    m.def("gamma_grad", &op_gamma_grad, "sum(w * g) + sum(b * gs) in fp32 (the adapter's gamma gradient)",
+          py::arg("w"), py::arg("g"), py::arg("b"), py::arg("gs"));
     m.def("version", []() { return std::string(svtad_version()); });
 }

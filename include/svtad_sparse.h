@@ -311,6 +311,31 @@ size_t svtad_column_sums_workspace_bytes(int64_t rows, int cols, int dtype);
 int svtad_column_sums(const void* a, void* out, void* workspace, size_t workspace_bytes, int64_t rows, int cols,
                       int dtype, void* stream);
 
+/*
+ * GELU backward of the adapter's down projection, replacing the autograd of
+ * nn.GELU plus the special / patch split (vit_sparse_adapter_poguise.py:305-309):
+ *   grad_pre[m, c] = g(m, c) * (Phi(u) + u phi(u)),  u = pre_act[m, c],
+ * with g read from grad_special [batch, n_special, n] for the first n_special
+ * tokens of a sample and from grad_patch [batch * (n_tokens - n_special), n]
+ * for the rest (NULL: zeros). pre_act and grad_pre are [batch, n_tokens, n].
+ * fp32 evaluation, one rounding. f16 / bf16, n % 8 == 0, 16-byte aligned
+ * buffers. One launch on `stream`.
+ */
+int svtad_gelu_backward_split(const void* grad_special, const void* grad_patch, const void* pre_act,
+                              void* grad_pre, int64_t batch, int64_t n_tokens, int64_t n_special, int n,
+                              int dtype, void* stream);
+
+/*
+ * Gradient of the adapter's gamma, replacing the autograd of `* self.gamma`
+ * (vit_sparse_adapter_poguise.py:652-653): out[0] = sum_i w[i] g[i] +
+ * sum_j b[j] gs[j], with w the up projection's weight, g = go^T c its
+ * unscaled weight gradient, b its bias (NULL: none) and gs the column sums of
+ * go. fp32 accumulation in a fixed order, out (one element) in `dtype`.
+ * f16 / bf16; counts multiples of 8; 16-byte aligned. One launch on `stream`.
+ */
+int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,
+                     int64_t count_b, void* out, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

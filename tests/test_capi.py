@@ -149,6 +149,29 @@ def test_adapter_arguments_checked_on_host(lib):
                                   None) == 0
 
 
+def test_adapter_backward_arguments_checked_on_host(lib):
+    buf = ctypes.create_string_buffer(256)
+    # gelu_backward_split: f16/bf16 only, n % 8, n_special <= n_tokens, 2^31 elements
+    st = lib.svtad_gelu_backward_split(buf, buf, buf, buf, I64(1), I64(4), I64(1), 64, 0, None)
+    assert st == -3 and b"f16/bf16" in lib.svtad_last_error()
+    st = lib.svtad_gelu_backward_split(buf, buf, buf, buf, I64(1), I64(4), I64(1), 12, 1, None)
+    assert st == -1
+    st = lib.svtad_gelu_backward_split(buf, buf, buf, buf, I64(1), I64(4), I64(5), 64, 1, None)
+    assert st == -1
+    st = lib.svtad_gelu_backward_split(buf, buf, None, buf, I64(1), I64(4), I64(1), 64, 1, None)
+    assert st == -1 and b"null pointer" in lib.svtad_last_error()
+    st = lib.svtad_gelu_backward_split(buf, buf, buf, buf, I64(1 << 20), I64(1 << 12), I64(1), 1024, 1, None)
+    assert st == -3
+    assert lib.svtad_gelu_backward_split(None, None, None, None, I64(0), I64(4), I64(1), 64, 1, None) == 0
+    # gamma_grad: counts multiples of 8, b and gs together
+    st = lib.svtad_gamma_grad(buf, buf, I64(12), None, None, I64(0), buf, 1, None)
+    assert st == -1
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), buf, None, I64(8), buf, 1, None)
+    assert st == -1 and b"together" in lib.svtad_last_error()
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, 0, None)
+    assert st == -3
+
+
 def test_table_limits_rejected(lib):
     st = lib.svtad_table_scan(ctypes.create_string_buffer(8), I64(1), 200, 200,
                               ctypes.create_string_buffer(8), None)
@@ -164,7 +187,7 @@ def test_extension_module_api():
     for name in ("fwd_bias", "bwd_w_bias", "dw_fwd", "dw_bwd_in", "dw_bwd_w",
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
                  "validate_neighbor_table", "prune_tokens", "bwd_packed", "adapter_down",
-                 "adapter_up", "linear_wgrad", "column_sums"):
+                 "adapter_up", "linear_wgrad", "column_sums", "gelu_backward_split", "gamma_grad"):
         assert hasattr(ops, name)
     import torch
 

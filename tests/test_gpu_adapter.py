@@ -171,3 +171,61 @@ def test_column_sums(dev, dname, rows, cols):
     else:
         assert _err(out, ref) <= 1e-2
         assert torch.equal(out, sv.ops.column_sums(a))
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("B,N,S,n,missing", [
+    (2, 8625, 1, 256, None), (3, 50, 0, 64, None), (2, 40, 40, 128, None), (2, 33, 2, 256, "special"),
+    (2, 33, 2, 256, "patch"),
+])
+def test_gelu_backward_split(dev, dname, B, N, S, n, missing):
+    """GELU backward from split gradients against PyTorch's gelu_backward of
+    the assembled gradient (both fp32 evaluation, one rounding: bar 2e-3 for
+    float16, 1e-2 for bfloat16, max-scaled)."""
+    import eccv26_tad_amd as sv
+
+    dt = getattr(torch, dname)
+    g = torch.Generator().manual_seed(N + n)
+    pre = (torch.randn(B, N, n, generator=g) * 2).to(dev, dt)
+    g_sp = torch.randn(B, S, n, generator=g).to(dev, dt)
+    g_pa = torch.randn(B * (N - S), n, generator=g).to(dev, dt)
+    if missing == "special":
+        g_sp_arg, g_sp = None, torch.zeros_like(g_sp)
+    else:
+        g_sp_arg = g_sp
+    if missing == "patch":
+        g_pa_arg, g_pa = None, torch.zeros_like(g_pa)
+    else:
+        g_pa_arg = g_pa
+    print("gelu_backward_split", dname, B, N, S, n, missing, flush=True)
+    got = sv.ops.gelu_backward_split(g_sp_arg, g_pa_arg, pre, S)
+    dg = torch.cat([g_sp, g_pa.view(B, N - S, n)], dim=1)
+    ref = torch.ops.aten.gelu_backward(dg.float(), pre.float())
+    assert got.shape == pre.shape and got.dtype == dt
+    assert _err(got, ref) <= (2e-3 if dt == torch.float16 else 1e-2)
+    assert torch.equal(got, sv.ops.gelu_backward_split(g_sp_arg, g_pa_arg, pre, S))
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("count,count_b", [(768 * 256, 768), (64 * 128, 0), (8, 8), (0, 0)])
+def test_gamma_grad(dev, dname, count, count_b):
+    """sum(w * g) + sum(b * gs) against an fp64 sum (bar 1e-2 of the sum of
+    absolute products), deterministic."""
+    import eccv26_tad_amd as sv
+
+    dt = getattr(torch, dname)
+    gen = torch.Generator().manual_seed(count + count_b)
+    w = torch.randn(max(count, 1), generator=gen)[:count].to(dev, dt)
+    gm = torch.randn(max(count, 1), generator=gen)[:count].to(dev, dt)
+    b = torch.randn(count_b, generator=gen).to(dev, dt) if count_b else None
+    gs = torch.randn(count_b, generator=gen).to(dev, dt) if count_b else None
+    out = sv.ops.gamma_grad(w, gm, b, gs)
+    prod = w.double() * gm.double()
+    ref = prod.sum()
+    scale = prod.abs().sum()
+    if b is not None:
+        pb = b.double() * gs.double()
+        ref, scale = ref + pb.sum(), scale + pb.abs().sum()
+    assert out.shape == (1,) and out.dtype == dt
+    assert abs(float(out) - float(ref)) <= 1e-2 * max(float(scale), 1e-6) + 1e-3 * abs(float(ref))
+    assert torch.equal(out, sv.ops.gamma_grad(w, gm, b, gs))
