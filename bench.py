@@ -284,7 +284,9 @@ def blob_mask(keep: float, seed: int = SEED + 1):
 def depthwise_measure(dev, reps):
     """benchmark config 3: depthwise (groups = C = 192) 3x3 SparseConv2D, fp16,
     B2 x T80 x 14x14, clustered keep masks, fwd + bwd_in + bwd_w with bias (the
-    autograd step of SparseDepthwiseConv2d), at every keep rate. Algorithmic
+    autograd step of SparseDepthwiseConv2d: the forward, then the one-pass
+    backward), at every keep rate; the separate backward passes are timed
+    too (pass_us). Algorithmic
     bytes per step: the three passes each read their activation rows and the
     table once and write their output once, plus weights."""
     import torch
@@ -324,14 +326,14 @@ def depthwise_measure(dev, reps):
         go = torch.randn(n, C, generator=g).to(dev, torch.float16)
         hit = float((table >= 0).sum()) / (9 * n)
 
-        def step():
+        def step():  # the calls SparseDepthwiseConv2d's autograd makes
             y = ops.dw_fwd(x, table, w, b, 0)
-            gi = ops.dw_bwd_in(go, table, w, 0)
-            gw, gb = ops.dw_bwd_w(go, x, table, 0, True)
+            gi, gw, gb = ops.dw_bwd(go, x, table, w, 0, True)
             return y, gi, gw, gb
 
         t = time_events(step, reps)
-        parts = {"fwd": lambda: ops.dw_fwd(x, table, w, b, 0), "bwd_in": lambda: ops.dw_bwd_in(go, table, w, 0),
+        parts = {"fwd": lambda: ops.dw_fwd(x, table, w, b, 0), "bwd": lambda: ops.dw_bwd(go, x, table, w, 0, True),
+                 "bwd_in": lambda: ops.dw_bwd_in(go, table, w, 0),
                  "bwd_w": lambda: ops.dw_bwd_w(go, x, table, 0, True)}
         pt = {k2: round(time_events(f, reps) * 1e3, 2) for k2, f in parts.items()}
         # fwd: x, y, table; bwd_in: go, gi, table; bwd_w: go, x, table; weights and bias

@@ -323,6 +323,39 @@ extern "C" int svtad_dw_bwd_in(const void* grad_out, const int32_t* nbr, const v
     return launch_status();
 }
 
+// partials of the depthwise backward ([splits][10][c] in the accumulator
+// type), then one flag word per split, 16-byte aligned
+static size_t dw_bwd_ws(const BwPlan& p) { return cdiv(p.ws_bytes, 16) * 16 + (size_t)p.splits * 4; }
+
+extern "C" size_t svtad_dw_bwd_workspace_bytes(int64_t n, int c, int dtype) {
+    if (check_common("dw_bwd_workspace_bytes", n, c, c, 0, dtype)) return 0;
+    return dw_bwd_ws(plan_dw_bw(n, c, dtype));
+}
+
+extern "C" int svtad_dw_bwd(const void* grad_out, const void* x, const int32_t* nbr, const void* weight,
+                            void* grad_in, void* grad_w, void* grad_bias, void* workspace, size_t workspace_bytes,
+                            int64_t n, int c, int64_t tokens_per_batch, int dtype, void* stream) {
+    int st = check_common("dw_bwd", n, c, c, tokens_per_batch, dtype);
+    if (st) return st;
+    const BwPlan p = plan_dw_bw(n, c, dtype);
+    if (!grad_w || !workspace || !weight || (n > 0 && (!grad_out || !x || !nbr || !grad_in)))
+        return set_error(SVTAD_ERR_INVALID, "dw_bwd: null pointer");
+    if (workspace_bytes < dw_bwd_ws(p))
+        return set_error(SVTAD_ERR_WORKSPACE, "dw_bwd: workspace smaller than svtad_dw_bwd_workspace_bytes()");
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t* flags = (uint32_t*)((char*)workspace + cdiv(p.ws_bytes, 16) * 16);
+    if (n > 0 && dw_bwd_fused(dtype, p, grad_out, x, nbr, weight, grad_in, grad_w, grad_bias, workspace, flags, n,
+                              c, tokens_per_batch, s))
+        return launch_status();
+    // shapes / alignments the one-pass kernels do not take: the two passes
+    if (n > 0) {
+        dw_gather(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, grad_in, n, c, tokens_per_batch, s);
+        orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, nullptr, s);
+    }
+    dw_bw(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c, tokens_per_batch, s);
+    return launch_status();
+}
+
 extern "C" size_t svtad_dw_bwd_w_workspace_bytes(int64_t n, int c, int dtype) {
     if (check_common("dw_bwd_w_workspace_bytes", n, c, c, 0, dtype)) return 0;
     return plan_dw_bw(n, c, dtype).ws_bytes;

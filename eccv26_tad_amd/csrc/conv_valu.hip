@@ -472,6 +472,178 @@ __global__ __launch_bounds__(512) void k_dw_bw_vec(const T* __restrict__ go, con
     }
 }
 
+// Depthwise backward in one pass over the rows: the backward-weight partials
+// of k_dw_bw_vec and, for the same rows, the backward-input gather of
+// k_dw_vec<MODE_BWDIN>. Row i's table entries give both the gathered x rows
+// (weight gradient) and the candidates of its transposed entries: entry
+// (i, 8-k) -> j is row i's transposed source for offset k when (j, k) -> i.
+// Per chunk of rows, all threads first resolve both source rows of every
+// (row, offset) into LDS (the table reads and the partner check are one
+// parallel step, not a chain per row); then thread (row lane rl, chunk)
+// takes rows rl, rl + R, ... of the chunk with every gathered load of a row
+// in flight together. Chunks are a whole number of R rows, so a lane owns
+// the rows k_dw_bw_vec gives it, in the same order, and the partial sums
+// are bit-identical to k_dw_bw_vec's; each gi row is summed over k = 0 .. 8
+// in k_dw_vec's order (fp16 results can still differ by an ulp in a few
+// elements, where the compiler picks other multiply-add instructions). An
+// entry without its partner (possible only in a table not built from a keep
+// mask) is left to the orphan pass: the workgroup writes its flag word (0 or
+// 1, every launch, so it needs no clearing) and the reduction kernel runs
+// the pass when any word is set.
+constexpr int kDwChunkRows = 512;
+template <typename T>
+__global__ __launch_bounds__(512) void k_dw_bwd_vec(const T* __restrict__ go, const T* __restrict__ x,
+                                                    const int32_t* __restrict__ nbr, const T* __restrict__ w,
+                                                    T* __restrict__ gi, typename Acc<T>::type* __restrict__ ws,
+                                                    uint32_t* __restrict__ flags, int64_t n, int c, int64_t tpb,
+                                                    int64_t rows_per_split) {
+    constexpr int VEC = Vec16<T>::N;
+    typedef typename Acc<T>::type A;
+    __shared__ __align__(16) A red[5 * 512 * VEC];
+    __shared__ int sx[kDwChunkRows * 9], st[kDwChunkRows * 9];  // gathered x row / transposed go row, -1 none
+    const int cpr = c / VEC, R = 512 / cpr;
+    const int chunk = (kDwChunkRows / R) * R;
+    const int tid = threadIdx.x, rl = tid / cpr, ch = (tid - rl * cpr) * VEC;
+    const bool active = rl < R;
+    const int s = blockIdx.x;
+    const int64_t r_begin = (int64_t)s * rows_per_split;
+    const int64_t r_end = min(n, r_begin + rows_per_split);
+    const rsrc_t rs = make_rsrc(x, (uint32_t)(n * c * (int64_t)sizeof(T)));
+    const rsrc_t rg = make_rsrc(go, (uint32_t)(n * c * (int64_t)sizeof(T)));
+    A acc[10][VEC];
+#pragma unroll
+    for (int k = 0; k < 10; ++k)
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) acc[k][j] = (A)0;
+    Vec16<T> wk[9];
+    if (active) {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) wk[k] = __builtin_bit_cast(Vec16<T>, *(const u32x4*)(w + (int64_t)k * c + ch));
+    }
+    int orphan = 0;
+    for (int64_t c0 = r_begin; c0 < r_end; c0 += chunk) {
+        const int rows = (int)min<int64_t>(chunk, r_end - c0);
+        __syncthreads();  // the previous chunk's rows are consumed
+        for (int e = tid; e < rows * 9; e += 512) {
+            const int r = e / 9, k = e - r * 9;
+            const int64_t i = c0 + r;
+            sx[e] = (int)src_row(nbr, i, k, n, tpb);
+            const int64_t j = src_row(nbr, i, 8 - k, n, tpb);
+            const bool ok = j >= 0 && src_row(nbr, j, k, n, tpb) == i;
+            orphan |= (j >= 0 && !ok) ? 1 : 0;
+            st[e] = ok ? (int)j : -1;
+        }
+        __syncthreads();
+        if (!active) continue;
+        for (int r = rl; r < rows; r += R) {
+            const int64_t i = c0 + r;
+            const u32x4 gv = bload16(rg, (uint32_t)((i * c + ch) * (int64_t)sizeof(T)));
+            u32x4 v[9], t[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                const int jx = sx[r * 9 + k], jt = st[r * 9 + k];
+                v[k] = bload16(rs, jx >= 0 ? (uint32_t)(((int64_t)jx * c + ch) * (int64_t)sizeof(T)) : kOOB);
+                t[k] = bload16(rg, jt >= 0 ? (uint32_t)(((int64_t)jt * c + ch) * (int64_t)sizeof(T)) : kOOB);
+            }
+            const Vec16<T> g = __builtin_bit_cast(Vec16<T>, gv);
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) acc[9][j] += to_acc<A>(g.e[j]);
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                const Vec16<T> xv = __builtin_bit_cast(Vec16<T>, v[k]);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) acc[k][j] += to_acc<A>(g.e[j]) * to_acc<A>(xv.e[j]);
+            }
+            A gs[VEC];
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) gs[j] = (A)0;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) {
+                const Vec16<T> tv = __builtin_bit_cast(Vec16<T>, t[k]);
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) gs[j] += to_acc<A>(tv.e[j]) * to_acc<A>(wk[k].e[j]);
+            }
+            Vec16<T> o;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) o.e[j] = from_acc<T>(gs[j]);
+            *(u32x4*)(gi + i * c + ch) = __builtin_bit_cast(u32x4, o);
+        }
+    }
+    __syncthreads();  // red aliases nothing, but the last chunk's LDS readers finish first
+    // the weight / bias partials as in k_dw_bw_vec
+#pragma unroll
+    for (int k0 = 0; k0 < 10; k0 += 5) {
+        if (active) {
+#pragma unroll
+            for (int kk = 0; kk < 5; ++kk)
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) red[(kk * R + rl) * c + ch + j] = acc[k0 + kk][j];
+        }
+        __syncthreads();
+        for (int pi = tid; pi < 5 * c; pi += 512) {
+            const int kk = pi / c, tt = pi - kk * c;
+            const A* col = red + (int64_t)kk * R * c + tt;
+            A v = (A)0;
+            int q = 0;
+            for (; q + 8 <= R; q += 8) {
+                A u[8];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) u[h] = col[(q + h) * c];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) v += u[h];
+            }
+            for (; q < R; ++q) v += col[q * c];
+            ws[((int64_t)s * 10 + k0 + kk) * c + tt] = v;
+        }
+        __syncthreads();
+    }
+    const int any = __syncthreads_or(orphan);
+    if (tid == 0) flags[s] = any ? 1u : 0u;
+}
+
+// The split reduction of k_dw_bwd_vec's partials (as k_split_reduce, weight
+// then bias from one partial row of 10 c), then the depthwise orphan pass
+// over the whole table when any split's flag word is set.
+template <typename T, typename A>
+__global__ __launch_bounds__(1024) void k_dw_bwd_reduce(const A* __restrict__ ws, int64_t count, int splits,
+                                                        T* __restrict__ gw, int64_t stride, int64_t count0,
+                                                        T* __restrict__ gb, const uint32_t* __restrict__ flags,
+                                                        const T* __restrict__ go, const int32_t* __restrict__ nbr,
+                                                        const T* __restrict__ w, T* __restrict__ gi, int64_t n,
+                                                        int c, int64_t tpb) {
+    __shared__ A part[16][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+    const int spt = (splits + 15) / 16;
+    const int q0 = min(splits, g * spt), q1 = min(splits, q0 + spt);
+    A sum = 0;
+    if (e < count) {
+        int q = q0;
+        for (; q + 8 <= q1; q += 8) {
+            A v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)(q + u) * stride + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) sum += v[u];
+        }
+        for (; q < q1; ++q) sum += ws[(int64_t)q * stride + e];
+    }
+    part[g][lane] = sum;
+    __syncthreads();
+    if (g == 0 && e < count) {
+        A t = part[0][lane];
+#pragma unroll
+        for (int h = 1; h < 16; ++h) t += part[h][lane];
+        if (e < count0) gw[e] = from_acc<T>(t);
+        else gb[e - count0] = from_acc<T>(t);
+    }
+    int f = 0;
+    for (int q = threadIdx.x; q < splits; q += 1024) f |= flags[q] != 0u ? 1 : 0;
+    if (__syncthreads_or(f) == 0) return;
+    for (int64_t q = (int64_t)blockIdx.x * 1024 + threadIdx.x; q < n * 9; q += (int64_t)gridDim.x * 1024)
+        orphan_entry<T, true>(q, go, nbr, w, gi, n, c, c, tpb);
+}
+
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
@@ -640,6 +812,33 @@ static void launch_dw_bw(const BwPlan& p, const void* go, const void* x, const i
     }
     split_reduce(dtype_of<T>(), part, 9LL * c, p.splits, gw, s);
     if (gb) split_reduce(dtype_of<T>(), part_b, (int64_t)c, p.splits, gb, s);
+}
+
+template <typename T>
+static bool launch_dw_bwd(const BwPlan& p, const void* go, const void* x, const int32_t* nbr, const void* w,
+                          void* gi, void* gw, void* gb, void* ws, uint32_t* flags, int64_t n, int c, int64_t tpb,
+                          hipStream_t s) {
+    typedef typename Acc<T>::type A;
+    if (!dw_vec_ok<T>(n, c, go, x, gi) || !al16v(w)) return false;
+    hipLaunchKernelGGL((k_dw_bwd_vec<T>), dim3((unsigned)p.splits), dim3(512), 0, s, (const T*)go, (const T*)x,
+                       nbr, (const T*)w, (T*)gi, (A*)ws, flags, n, c, tpb, p.rows_per_split);
+    const int64_t count = gb ? 10LL * c : 9LL * c;
+    hipLaunchKernelGGL((k_dw_bwd_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, 64))), dim3(1024),
+                       0, s, (const A*)ws, count, p.splits, (T*)gw, 10LL * c, 9LL * c, (T*)gb, (const uint32_t*)flags,
+                       (const T*)go, nbr, (const T*)w, (T*)gi, n, c, tpb);
+    return true;
+}
+
+bool dw_bwd_fused(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, const void* w,
+                  void* gi, void* gw, void* gb, void* ws, uint32_t* flags, int64_t n, int c, int64_t tpb,
+                  hipStream_t s) {
+    switch (dtype) {
+        case SVTAD_F32: return launch_dw_bwd<float>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
+        case SVTAD_F16: return launch_dw_bwd<f16>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
+        case SVTAD_BF16: return launch_dw_bwd<bf16>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
+        case SVTAD_F64: return launch_dw_bwd<double>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
+    }
+    return false;
 }
 
 void dw_bw(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, void* gw,

@@ -39,6 +39,14 @@ void dw_gather(int dtype, int mode, const void* src, const int32_t* nbr, const v
                const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s);
 void dw_bw(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, void* gw,
            void* gb, void* ws, int64_t n, int c, int64_t tpb, hipStream_t s);
+// Depthwise backward-input and backward-weight / bias in one pass over the
+// rows plus one reduction launch (which also runs the orphan pass when a
+// split's flag word says so). ws holds the [splits][10][c] partials, flags
+// one word per split. Returns false (nothing launched) when the vectorized
+// kernels do not apply.
+bool dw_bwd_fused(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, const void* w,
+                  void* gi, void* gw, void* gb, void* ws, uint32_t* flags, int64_t n, int c, int64_t tpb,
+                  hipStream_t s);
 
 // out[e] = T(sum_s part[s][e]) for e < count; partials in the accumulator type.
 void split_reduce(int dtype, const void* part, int64_t count, int splits, void* out, hipStream_t s);

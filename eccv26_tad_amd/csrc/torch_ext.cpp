@@ -433,6 +433,37 @@ std::tuple<at::Tensor, at::Tensor> op_dw_bwd_w(const at::Tensor& go_in, const at
     return {gw, gb};
 }
 
+// dw_bwd(grad_output, x, table, weight, tpb, with_bias) -> (grad_in, grad_w, grad_bias):
+// dw_bwd_in and dw_bwd_w in one call (one pass over the rows + one reduction)
+std::tuple<at::Tensor, at::Tensor, at::Tensor> op_dw_bwd(const at::Tensor& go_in, const at::Tensor& x_in,
+                                                         const at::Tensor& nbr_in, const at::Tensor& w_in,
+                                                         int64_t tpb, bool with_bias) {
+    check_gpu(go_in, "grad_output");
+    at::Tensor go = rows_view(go_in);
+    at::Tensor x = rows_view(x_in);
+    const int64_t c = x.size(-1), n = n_rows(x);
+    TORCH_CHECK(go.size(-1) == c && n_rows(go) == n, "grad_output must match x's shape");
+    TORCH_CHECK(go.scalar_type() == x.scalar_type(), "grad_output and x dtypes differ");
+    TORCH_CHECK(w_in.dim() == 2 && w_in.size(0) == 9 && w_in.size(1) == c,
+                "depthwise weight must be (9, ", c, ")");
+    TORCH_CHECK(w_in.scalar_type() == x.scalar_type(), "x and weight dtypes differ");
+    at::Tensor w = w_in.contiguous();
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(x.device());
+    const int dt = dtype_code(x);
+    const size_t ws_bytes = svtad_dw_bwd_workspace_bytes(n, (int)c, dt);
+    TORCH_CHECK(ws_bytes > 0, "dw_bwd: ", svtad_last_error());
+    at::Tensor ws = at::empty({(int64_t)ws_bytes}, x.options().dtype(at::kByte));
+    at::Tensor gi = at::empty({n, c}, x.options());
+    at::Tensor gw = at::empty({9, c}, x.options());
+    at::Tensor gb = with_bias ? at::empty({c}, x.options()) : at::empty({0}, x.options());
+    const int st = svtad_dw_bwd(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(), gi.data_ptr(),
+                                gw.data_ptr(), with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
+                                (int)c, tpb, dt, stream_of(x));
+    check_status(st, "dw_bwd");
+    return {gi, gw, gb};
+}
+
 // ---------------------------------------------------------------------------
 // neighbor tables
 // ---------------------------------------------------------------------------
@@ -781,6 +812,9 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("weight"), py::arg("bias"), py::arg("tokens_per_batch"));
     m.def("dw_bwd_in", &op_dw_bwd_in, "Depthwise backward input", py::arg("grad_output"),
           py::arg("neighbor_indices"), py::arg("weight"), py::arg("tokens_per_batch"));
+    m.def("dw_bwd", &op_dw_bwd, "Depthwise backward input, weight and bias in one call",
+          py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
+          py::arg("tokens_per_batch"), py::arg("with_bias"));
     m.def("dw_bwd_w", &op_dw_bwd_w, "Depthwise backward weight and bias", py::arg("grad_output"),
           py::arg("x"), py::arg("neighbor_indices"), py::arg("tokens_per_batch"),
           py::arg("with_bias"));

@@ -183,9 +183,13 @@ class SparseDepthwiseConv2dFunction(Function):
         tpb = ctx.tokens_per_batch
         go = grad_output.contiguous()
         grad_input = grad_weight = grad_bias = None
+        need_b = bias is not None and ctx.needs_input_grad[3]
+        if ctx.needs_input_grad[0] and ctx.needs_input_grad[2]:
+            # all gradients in one pass over the rows plus one reduction
+            gi, gw, gb = _ops.dw_bwd(go, x, neighbor_indices, weight, tpb, need_b)
+            return gi.view(x.shape), None, gw, gb if need_b else None, None
         if ctx.needs_input_grad[0]:
             grad_input = _ops.dw_bwd_in(go, neighbor_indices, weight, tpb).view(x.shape)
-        need_b = bias is not None and ctx.needs_input_grad[3]
         if ctx.needs_input_grad[2] or need_b:
             gw, gb = _ops.dw_bwd_w(go, x, neighbor_indices, tpb, need_b)
             grad_weight = gw if ctx.needs_input_grad[2] else None

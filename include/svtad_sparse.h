@@ -177,6 +177,20 @@ size_t svtad_dw_bwd_w_workspace_bytes(int64_t n, int c, int dtype);
 int svtad_dw_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,
                    void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n, int c,
                    int64_t tokens_per_batch, int dtype, void* stream);
+/*
+ * Depthwise backward-input and backward-weight / bias in one call: one pass
+ * over the rows computes grad_in and the row-split weight / bias partials
+ * together (row i's table entries give both its gathered x rows and its
+ * transposed go sources), and one reduction launch adds the partials in a
+ * fixed order and runs the asymmetric-entry pass when the first pass met
+ * such an entry. Results equal svtad_dw_bwd_in followed by svtad_dw_bwd_w.
+ * grad_bias may be NULL. Workspace: svtad_dw_bwd_workspace_bytes(). Two
+ * launches on `stream` (the two separate calls take four).
+ */
+size_t svtad_dw_bwd_workspace_bytes(int64_t n, int c, int dtype);
+int svtad_dw_bwd(const void* grad_out, const void* x, const int32_t* nbr, const void* weight, void* grad_in,
+                 void* grad_w, void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n, int c,
+                 int64_t tokens_per_batch, int dtype, void* stream);
 
 /*
  * Neighbor table from a keep mask [n_frames, h, w] (uint8, nonzero = kept),

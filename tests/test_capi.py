@@ -187,7 +187,8 @@ def test_extension_module_api():
     for name in ("fwd_bias", "bwd_w_bias", "dw_fwd", "dw_bwd_in", "dw_bwd_w",
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
                  "validate_neighbor_table", "prune_tokens", "bwd_packed", "adapter_down",
-                 "adapter_up", "linear_wgrad", "column_sums", "gelu_backward_split", "gamma_grad"):
+                 "adapter_up", "linear_wgrad", "column_sums", "gelu_backward_split", "gamma_grad",
+                 "dw_bwd"):
         assert hasattr(ops, name)
     import torch
 

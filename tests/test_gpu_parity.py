@@ -522,6 +522,68 @@ def test_depthwise_module_grad(dev, oracle):
     assert oracle.rel_err(_np32(m.weight.grad), oracle.dw_bwd_w(gn, xn, t)) <= 1e-5
 
 
+@pytest.mark.parametrize("dname,c,tpb", [("float16", 192, 0), ("bfloat16", 64, 0), ("float32", 24, 0),
+                                          ("float64", 8, 0), ("float16", 192, 1)])
+def test_depthwise_one_pass_backward(dev, oracle, dname, c, tpb):
+    """dw_bwd (one pass over the rows + one reduction) against dw_bwd_in +
+    dw_bwd_w on mask-built tables, global and per-sample (tokens_per_batch)
+    indices: weight and bias gradients bit for bit (same row lanes, same
+    order); the input gradient bit for bit except float16, where the two
+    kernels' compiled multiply-adds leave a few elements 1 ulp apart; and the
+    oracle on a table with asymmetric entries (the reduction's orphan
+    pass)."""
+    import torch
+
+    import opentad_sparse_ops as ops
+
+    dt = _dt(dname)
+    rng = np.random.default_rng(c + tpb)
+    B, Tn = 2, 5
+    mask = topk_mask(rng, B, Tn, 14, 14, 0.55)
+    t = oracle.build_table(mask)
+    n = t.shape[0]
+    x = _rounded(rng.standard_normal((n, c)).astype(np.float32), dt)
+    w = _rounded(rng.standard_normal((9, c)).astype(np.float32) * 0.3, dt)
+    go = _rounded(rng.standard_normal((n, c)).astype(np.float32), dt)
+    X, W, G = (_t(a, dev, dt) for a in (x, w, go))
+    tab, tpb_v = t, 0
+    if tpb:  # per-sample indices: equal kept counts per sample
+        tpb_v = n // B
+        tab = t.copy()
+        tab[tab >= 0] %= tpb_v
+    T = _t(tab, dev, _dt("int32"))
+    _say("dw one-pass", dname, c, tpb_v)
+    gi, gw, gb = ops.dw_bwd(G, X, T, W, tpb_v, True)
+    gi2 = ops.dw_bwd_in(G, T, W, tpb_v)
+    gw2, gb2 = ops.dw_bwd_w(G, X, T, tpb_v, True)
+    assert torch.equal(gw, gw2) and torch.equal(gb, gb2)
+    if dt == torch.float16:
+        # the compiler's choice of fp16 multiply-add instructions differs
+        # between the two kernels: a few elements 1 ulp apart
+        d = (gi.double() - gi2.double()).abs()
+        assert float(d.max()) <= 2e-3 * float(gi2.double().abs().max())
+        assert int(torch.count_nonzero(d)) <= gi.numel() // 1000
+    else:
+        assert torch.equal(gi, gi2)
+    gi3, gw3, gb3 = ops.dw_bwd(G, X, T, W, tpb_v, False)
+    assert gb3.numel() == 0 and torch.equal(gi3, gi) and torch.equal(gw3, gw2)
+    tol = TOL[dname]
+    assert oracle.rel_err(gi.cpu().double().numpy(), oracle.dw_bwd_in(go, t, w)) <= tol
+    assert oracle.rel_err(gw.cpu().double().numpy(), oracle.dw_bwd_w(go, x, t)) <= tol
+    # asymmetric entries: every 7th row points one entry at a random row
+    asym = t.copy()
+    for i in range(0, n, 7):
+        asym[i, int(rng.integers(0, 9))] = int(rng.integers(0, n))
+    Ta = _t(asym, dev, _dt("int32"))
+    gia, gwa, gba = ops.dw_bwd(G, X, Ta, W, 0, True)
+    assert oracle.rel_err(gia.cpu().double().numpy(), oracle.dw_bwd_in(go, asym, w)) <= tol
+    assert oracle.rel_err(gwa.cpu().double().numpy(), oracle.dw_bwd_w(go, x, asym)) <= tol
+    assert oracle.rel_err(gba.cpu().double().numpy(), oracle.bias_grad(go)) <= tol
+    # a symmetric table again after the asymmetric one (flag words rewritten)
+    gi4, _, _ = ops.dw_bwd(G, X, T, W, tpb_v, True)
+    assert torch.equal(gi4, gi)
+
+
 # ---------------------------------------------------------------------------
 # determinism
 # ---------------------------------------------------------------------------
