@@ -42,7 +42,8 @@ from .neighbor import (  # noqa: E402
     transpose_neighbor_table,
     validate_neighbor_table,
 )
-from .adapter import AdapterDownFunction, AdapterUpFunction, SparseConvAdapter  # noqa: E402
+from .adapter import (AdapterDownFunction, AdapterUpFunction, SparseConvAdapter,  # noqa: E402
+                      SparseConvAdapterFunction)
 from .dense_path import (  # noqa: E402
     conv2d_weight_from_sparse,
     dense_conv_tokens,
@@ -65,6 +66,6 @@ __all__ = [
     "build_neighbor_table", "get_initial_neighbor_indices", "prune_tokens", "remap_neighbor_table",
     "transpose_neighbor_table", "validate_neighbor_table", "remap_legacy_sparse_conv_weights",
     "dense_conv_tokens", "keep_mask_from_indices", "sparse_weight_from_conv2d",
-    "conv2d_weight_from_sparse", "SparseConvAdapter", "AdapterDownFunction", "AdapterUpFunction",
+    "conv2d_weight_from_sparse", "SparseConvAdapter", "AdapterDownFunction", "AdapterUpFunction", "SparseConvAdapterFunction",
     "LIB_PATH",
 ]

@@ -11,8 +11,10 @@ module does not implement (it raises when asked for them):
     processed = sparse_conv(patches, neighbor_indices)
     y = up_proj(cat(special, processed)) * gamma + x
 
-The forward runs in three launches (``opentad_sparse_ops.adapter_down``, the
-SparseConv2D forward, ``opentad_sparse_ops.adapter_up``):
+The module runs as one autograd node (``SparseConvAdapterFunction``); its
+forward is the down GEMM (``opentad_sparse_ops.adapter_down``), the
+SparseConv2D forward (weight pack + gathered GEMM) and the up GEMM
+(``opentad_sparse_ops.adapter_up``):
 
 * the down GEMM's epilogue adds the bias, rounds the Linear output, applies
   GELU and writes the special tokens and the (contiguous) SparseConv2D input
@@ -37,6 +39,11 @@ the up-projection's weight-gradient reduction anyway; one launch adds both
 products (``opentad_sparse_ops.gamma_grad``). The bias gradients (column sums
 over the token rows) use ``opentad_sparse_ops.column_sums``.
 
+The input gradient is one GEMM with the residual's term as its addend
+(``addmm(go, du, W_d)``), which the single node makes possible.
+``AdapterDownFunction`` and ``AdapterUpFunction`` are the same kernels as two
+separate nodes around a ``SparseConv2d``.
+
 The fused path takes float16 / bfloat16 (the matrix-core dtypes) and raises
 otherwise; ``reference_forward`` runs the unfused chain in the reference's op
 order (for tests and the benchmark).
@@ -50,7 +57,7 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import opentad_sparse_ops as _ops
-from .sparse_conv_layer import SparseConv2d
+from .sparse_conv_layer import (BIAS_AFTER, BIAS_FP32, BIAS_NONE, IMPLICIT_GEMM_MIN_CIN, SparseConv2d)
 
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
@@ -152,6 +159,70 @@ class AdapterUpFunction(Function):
         return g_sp, g_pa, gw, gb, g_gamma, go
 
 
+class SparseConvAdapterFunction(Function):
+    """The whole adapter (down GEMM + GELU, SparseConv2D, up GEMM + gamma +
+    residual) as one autograd node, so that its backward can hand the input
+    gradient's two terms to one GEMM: ``grad_x = go + du W_d`` is
+    ``addmm(go, du, W_d)``, where the two-node chain computes ``du W_d`` and
+    then autograd adds ``go`` in a separate pass over the 768-wide tokens.
+    The kernels are those of ``AdapterDownFunction``, ``SparseConv2dFunction``
+    and ``AdapterUpFunction``."""
+
+    @staticmethod
+    def forward(ctx, x, w_d, b_d, w_c, b_c, w_u, b_u, gamma, nbr, n_special, tpb):
+        S = int(n_special)
+        pre, sp, pa = _ops.adapter_down(x, w_d, b_d, S)
+        c_in = w_c.shape[1]
+        if c_in % 4 != 0:
+            raise ValueError(f"C_in ({c_in}) must be divisible by 4 for optimized kernel.")
+        mode = BIAS_NONE if b_c is None else (BIAS_FP32 if c_in >= IMPLICIT_GEMM_MIN_CIN else BIAS_AFTER)
+        pf, pb = _ops.pack_weight(w_c, True, any(ctx.needs_input_grad))
+        processed = _ops.fwd_packed(pa, nbr, w_c, pf, b_c, tpb, mode)
+        out = _ops.adapter_up(sp, processed, w_u, b_u, gamma, x)
+        ctx.save_for_backward(x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma)
+        ctx.flags = (S, int(tpb), b_d is not None)
+        return out
+
+    @staticmethod
+    def backward(ctx, go):
+        x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma = ctx.saved_tensors
+        S, tpb, has_bd = ctx.flags
+        need = ctx.needs_input_grad
+        B, N, n = go.shape
+        k = w_u.shape[1]
+        go = go.contiguous()
+        go2 = go.reshape(-1, n)
+        # up projection: G = go^T cat(sp, processed) without the cat
+        if S > 0:
+            G = _ops.linear_wgrad(go2, _patch_rows(B, N, S, go.device), processed)
+            G = G + torch.matmul(go[:, :S].reshape(-1, n).t(), sp.reshape(-1, k))
+        else:
+            G = _ops.linear_wgrad(go2, _NO_ROWS(go2), processed)
+        gsum = _colsum(go2)
+        g_gamma = None
+        if need[7]:
+            g_gamma = _ops.gamma_grad(w_u, G, b_u, gsum if b_u is not None else None)
+            g_gamma = g_gamma.view(gamma.shape).to(gamma.dtype)
+        gw_u = G * gamma if need[5] else None
+        gb_u = gsum * gamma if b_u is not None and need[6] else None
+        dc = torch.matmul(go, w_u * gamma)  # [B, N, k]
+        g_sp = dc[:, :S]
+        g_pa = dc[:, S:].reshape(-1, k)
+        # SparseConv2D
+        need_bc = b_c is not None and need[4]
+        gi_pa, gw_c, gb_c = _ops.bwd_packed(g_pa, pa, nbr, w_c, pb, w_c.shape[1], tpb, need_bc)
+        # down projection: GELU backward from the two gradient buffers, then
+        # the input gradient with the residual's go in the same GEMM
+        du = _ops.gelu_backward_split(g_sp, gi_pa, pre, S)
+        du2 = du.reshape(-1, du.shape[-1])
+        x2 = x.reshape(-1, x.shape[-1])
+        gx = torch.addmm(go2, du2, w_d).view(x.shape) if need[0] else None
+        gw_d = _ops.linear_wgrad(du2, _NO_ROWS(du2), x2) if need[1] else None
+        gb_d = _colsum(du2) if has_bd and need[2] else None
+        return (gx, gw_d, gb_d, gw_c if need[3] else None, gb_c if need_bc else None, gw_u, gb_u, g_gamma,
+                None, None, None)
+
+
 class SparseConvAdapter(nn.Module):
     """The reference adapter with ``conv_type="sparse_conv"``, ``use_attn=0``
     and no heatmap injection, on fused HIP GEMM epilogues."""
@@ -191,13 +262,15 @@ class SparseConvAdapter(nn.Module):
         S = self._n_special(x, indices)
         if indices.shape[1] == 0:
             return self.reference_forward(x, h, w, indices, total_num_patches, neighbor_indices)
-        sp, pa = AdapterDownFunction.apply(x, self.down_proj.weight, self.down_proj.bias, S)
         nbr = neighbor_indices.reshape(-1, 9)
         if tokens_per_batch is None:
             tokens_per_batch = indices.shape[1] if int(nbr.max()) < indices.shape[1] else 0
-        processed = self.sparse_conv(pa, nbr, tokens_per_batch=tokens_per_batch)
-        return AdapterUpFunction.apply(sp, processed, self.up_proj.weight, self.up_proj.bias,
-                                       self.gamma, x)
+        if nbr.dtype != torch.int32:
+            nbr = nbr.to(torch.int32)
+        conv = self.sparse_conv
+        return SparseConvAdapterFunction.apply(x, self.down_proj.weight, self.down_proj.bias, conv.weight,
+                                               conv.bias, self.up_proj.weight, self.up_proj.bias, self.gamma,
+                                               nbr, S, tokens_per_batch)
 
     def reference_forward(self, x, h, w, indices, total_num_patches, neighbor_indices=None):
         """The unfused chain in the reference's op order

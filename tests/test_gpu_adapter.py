@@ -84,6 +84,32 @@ def test_fused_adapter_matches_unfused_chain(dev, dname, case):
 
 
 @pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+def test_two_node_chain_matches_single_node(dev, dname):
+    """AdapterDownFunction -> SparseConv2d -> AdapterUpFunction (three autograd
+    nodes) against the module's single node: same kernels, so the output is
+    identical; the gradients differ only where the single node adds the
+    residual's term inside the input-gradient GEMM (bar 1e-2, max-scaled)."""
+    import eccv26_tad_amd as sv
+
+    dt = getattr(torch, dname)
+    mod, _, idx, table, x, go = _setup(dev, dt, B=2, T=6, H=7, W=7, keep=0.4, embed=256, mlp_ratio=0.25,
+                                       S=1, seed=41)
+    H = W = 7
+    xa = x.detach().clone().requires_grad_(True)
+    ya = mod(xa, H, W, idx, 6 * H * W, table)
+    ga = torch.autograd.grad(ya, [xa] + list(mod.parameters()), go)
+    xb = x.detach().clone().requires_grad_(True)
+    S = xb.shape[1] - idx.shape[1]
+    sp, pa = sv.AdapterDownFunction.apply(xb, mod.down_proj.weight, mod.down_proj.bias, S)
+    processed = mod.sparse_conv(pa, table.reshape(-1, 9), tokens_per_batch=0)
+    yb = sv.AdapterUpFunction.apply(sp, processed, mod.up_proj.weight, mod.up_proj.bias, mod.gamma, xb)
+    gb = torch.autograd.grad(yb, [xb] + list(mod.parameters()), go)
+    assert torch.equal(ya, yb)
+    for a, b in zip(ga, gb):
+        assert _err(a, b) <= 1e-2
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
 def test_adapter_kernels_direct(dev, dname):
     import eccv26_tad_amd as sv
 
