@@ -584,6 +584,31 @@ def test_depthwise_one_pass_backward(dev, oracle, dname, c, tpb):
     assert torch.equal(gi4, gi)
 
 
+@pytest.mark.parametrize("dname,c", [("float32", 192), ("float32", 8), ("bfloat16", 64)])
+def test_depthwise_one_pass_backward_row_chunks(dev, dname, c):
+    """Splits longer than one LDS chunk of rows (141,120 rows, 552 per split):
+    the one-pass backward still equals the two separate calls bit for bit."""
+    import torch
+
+    import eccv26_tad_amd as sv
+    import opentad_sparse_ops as ops
+
+    dt = _dt(dname)
+    g = torch.Generator().manual_seed(c)
+    mask = torch.ones(1, 720, 14, 14, dtype=torch.uint8)
+    mask.view(-1)[torch.randperm(mask.numel(), generator=g)[:40]] = 0  # a few holes
+    T = sv.build_neighbor_table(mask.to(dev))
+    n = T.shape[0]
+    _say("dw one-pass chunks", dname, c, n)
+    x = torch.randn(n, c, generator=g).to(dev, dt)
+    go = torch.randn(n, c, generator=g).to(dev, dt)
+    w = (torch.randn(9, c, generator=g) * 0.3).to(dev, dt)
+    gi, gw, gb = ops.dw_bwd(go, x, T, w, 0, True)
+    gi2 = ops.dw_bwd_in(go, T, w, 0)
+    gw2, gb2 = ops.dw_bwd_w(go, x, T, 0, True)
+    assert torch.equal(gi, gi2) and torch.equal(gw, gw2) and torch.equal(gb, gb2)
+
+
 # ---------------------------------------------------------------------------
 # determinism
 # ---------------------------------------------------------------------------
