@@ -172,6 +172,22 @@ def test_adapter_backward_arguments_checked_on_host(lib):
     assert st == -3
 
 
+def test_dw_bwd_arguments_checked_on_host(lib):
+    lib.svtad_dw_bwd_workspace_bytes.restype = ctypes.c_size_t
+    buf = ctypes.create_string_buffer(256)
+    ws = lib.svtad_dw_bwd_workspace_bytes(I64(1000), 64, 1)
+    assert ws > lib.svtad_dw_bwd_w_workspace_bytes(I64(1000), 64, 1)  # plus the split flag words
+    st = lib.svtad_dw_bwd(buf, buf, buf, buf, buf, buf, None, buf, ctypes.c_size_t(16), I64(1000), 64, I64(0), 1,
+                          None)
+    assert st == -2 and b"workspace" in lib.svtad_last_error()
+    st = lib.svtad_dw_bwd(buf, buf, buf, None, buf, buf, None, buf, ctypes.c_size_t(ws), I64(1000), 64, I64(0), 1,
+                          None)
+    assert st == -1 and b"null pointer" in lib.svtad_last_error()
+    st = lib.svtad_dw_bwd(buf, buf, buf, buf, buf, buf, None, buf, ctypes.c_size_t(ws), I64(1000), 6, I64(0), 1,
+                          None)
+    assert st != 0
+
+
 def test_table_limits_rejected(lib):
     st = lib.svtad_table_scan(ctypes.create_string_buffer(8), I64(1), 200, 200,
                               ctypes.create_string_buffer(8), None)
