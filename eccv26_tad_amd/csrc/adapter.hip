@@ -342,18 +342,25 @@ __global__ __launch_bounds__(256) void k_gelu_bwd_split(const T* __restrict__ g_
     *(u32x4*)(out + (int64_t)m * n + q * 8) = o;
 }
 
-// out[0] = T(sum_i w[i] g[i] + sum_j b[j] gs[j]) in fp32: the gradient of
-// gamma in (c W^T + b) * gamma (vit_sparse_adapter_poguise.py:652-653), which is
-// sum(go * z) = <W, go^T c> + <b, column sums of go>. One workgroup; thread t
-// owns the 8-element chunks t, t + 1024, ... and the per-thread sums are
-// added by a fixed tree, so the result is deterministic.
+// part[p] = sum over the p-th slice of the 8-element chunks of
+// w[i] g[i] (then b[j] gs[j]) in fp32: the gradient of gamma in
+// (c W^T + b) * gamma (vit_sparse_adapter_poguise.py:652-653), which is
+// sum(go * z) = <W, go^T c> + <b, column sums of go>. kGammaParts
+// workgroups of 256 threads; the weight chunks and the bias chunks form one
+// index range, split into equal slices; each thread's strided sum and the
+// workgroup's fixed tree keep the order fixed, and split_reduce adds the
+// slices in order.
+constexpr int kGammaParts = 64;
 template <typename T>
-__global__ __launch_bounds__(1024) void k_gamma_grad(const T* __restrict__ w, const T* __restrict__ g,
-                                                     int64_t chunks, const T* __restrict__ b,
-                                                     const T* __restrict__ gs, int64_t chunks_b,
-                                                     T* __restrict__ out) {
-    __shared__ float red[1024];
+__global__ __launch_bounds__(256) void k_gamma_part(const T* __restrict__ w, const T* __restrict__ g,
+                                                    int64_t chunks, const T* __restrict__ b,
+                                                    const T* __restrict__ gs, int64_t chunks_b,
+                                                    float* __restrict__ part) {
+    __shared__ float red[256];
     const int tid = threadIdx.x;
+    const int64_t total = chunks + chunks_b;
+    const int64_t per = (total + kGammaParts - 1) / kGammaParts;
+    const int64_t c0 = (int64_t)blockIdx.x * per, c1 = min(total, c0 + per);
     float acc = 0.f;
     auto dot8 = [&](const u32x4 a, const u32x4 c) {
 #pragma unroll
@@ -362,26 +369,17 @@ __global__ __launch_bounds__(1024) void k_gamma_grad(const T* __restrict__ w, co
             acc += (float)__builtin_bit_cast(T, (u16)(a[h] >> 16)) * (float)__builtin_bit_cast(T, (u16)(c[h] >> 16));
         }
     };
-    int64_t c = tid;
-    for (; c + 3 * 1024 < chunks; c += 4 * 1024) {
-        u32x4 a[4], v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            a[u] = *(const u32x4*)(w + (c + u * 1024) * 8);
-            v[u] = *(const u32x4*)(g + (c + u * 1024) * 8);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) dot8(a[u], v[u]);
+    for (int64_t c = c0 + tid; c < c1; c += 256) {
+        if (c < chunks) dot8(*(const u32x4*)(w + c * 8), *(const u32x4*)(g + c * 8));
+        else dot8(*(const u32x4*)(b + (c - chunks) * 8), *(const u32x4*)(gs + (c - chunks) * 8));
     }
-    for (; c < chunks; c += 1024) dot8(*(const u32x4*)(w + c * 8), *(const u32x4*)(g + c * 8));
-    for (int64_t cb = tid; cb < chunks_b; cb += 1024) dot8(*(const u32x4*)(b + cb * 8), *(const u32x4*)(gs + cb * 8));
     red[tid] = acc;
     __syncthreads();
-    for (int h = 512; h > 0; h >>= 1) {
+    for (int h = 128; h > 0; h >>= 1) {
         if (tid < h) red[tid] += red[tid + h];
         __syncthreads();
     }
-    if (tid == 0) out[0] = (T)red[0];
+    if (tid == 0) part[blockIdx.x] = red[0];
 }
 
 }  // namespace svtad
@@ -524,23 +522,29 @@ extern "C" int svtad_gelu_backward_split(const void* grad_special, const void* g
     return launch_status();
 }
 
+extern "C" size_t svtad_gamma_grad_workspace_bytes(void) { return (size_t)kGammaParts * sizeof(float); }
+
 extern "C" int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,
-                                int64_t count_b, void* out, int dtype, void* stream) {
+                                int64_t count_b, void* out, void* workspace, size_t workspace_bytes, int dtype,
+                                void* stream) {
     if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
         return set_error(SVTAD_ERR_UNSUPPORTED, "gamma_grad: needs f16/bf16");
     if (count < 0 || count_b < 0 || count % 8 != 0 || count_b % 8 != 0 || (!b != !gs))
         return set_error(SVTAD_ERR_INVALID, "gamma_grad: counts must be multiples of 8; b and gs go together");
-    if (!out || (count > 0 && (!w || !g)) || (count_b > 0 && !b))
+    if (!out || !workspace || (count > 0 && (!w || !g)) || (count_b > 0 && !b))
         return set_error(SVTAD_ERR_INVALID, "gamma_grad: null pointer");
     if ((w && !al16(w)) || (g && !al16(g)) || (b && !al16(b)) || (gs && !al16(gs)))
         return set_error(SVTAD_ERR_INVALID, "gamma_grad: inputs need 16-byte alignment");
+    if (workspace_bytes < svtad_gamma_grad_workspace_bytes())
+        return set_error(SVTAD_ERR_WORKSPACE, "gamma_grad: workspace smaller than svtad_gamma_grad_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;
     const int64_t nb = b ? count_b / 8 : 0;
     if (dtype == SVTAD_F16)
-        hipLaunchKernelGGL((k_gamma_grad<f16>), dim3(1), dim3(1024), 0, s, (const f16*)w, (const f16*)g, count / 8,
-                           (const f16*)b, (const f16*)gs, nb, (f16*)out);
+        hipLaunchKernelGGL((k_gamma_part<f16>), dim3(kGammaParts), dim3(256), 0, s, (const f16*)w, (const f16*)g,
+                           count / 8, (const f16*)b, (const f16*)gs, nb, (float*)workspace);
     else
-        hipLaunchKernelGGL((k_gamma_grad<bf16>), dim3(1), dim3(1024), 0, s, (const bf16*)w, (const bf16*)g,
-                           count / 8, (const bf16*)b, (const bf16*)gs, nb, (bf16*)out);
+        hipLaunchKernelGGL((k_gamma_part<bf16>), dim3(kGammaParts), dim3(256), 0, s, (const bf16*)w, (const bf16*)g,
+                           count / 8, (const bf16*)b, (const bf16*)gs, nb, (float*)workspace);
+    split_reduce(dtype, workspace, 1, kGammaParts, out, s);
     return launch_status();
 }

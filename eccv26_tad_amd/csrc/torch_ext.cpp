@@ -765,9 +765,11 @@ at::Tensor op_gamma_grad(const at::Tensor& w_in, const at::Tensor& g_in, const c
     }
     c10::DeviceGuard guard(w.device());
     at::Tensor out = at::empty({1}, w.options());
+    const size_t wsb = svtad_gamma_grad_workspace_bytes();
+    at::Tensor work = at::empty({(int64_t)wsb}, w.options().dtype(at::kByte));
     check_status(svtad_gamma_grad(w.data_ptr(), g.data_ptr(), w.numel(), b.defined() ? b.data_ptr() : nullptr,
                                   gs.defined() ? gs.data_ptr() : nullptr, b.defined() ? b.numel() : 0,
-                                  out.data_ptr(), dtype_code(w), stream_of(w)),
+                                  out.data_ptr(), work.data_ptr(), wsb, dtype_code(w), stream_of(w)),
                  "gamma_grad");
     return out;
 }

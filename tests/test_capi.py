@@ -163,13 +163,18 @@ def test_adapter_backward_arguments_checked_on_host(lib):
     st = lib.svtad_gelu_backward_split(buf, buf, buf, buf, I64(1 << 20), I64(1 << 12), I64(1), 1024, 1, None)
     assert st == -3
     assert lib.svtad_gelu_backward_split(None, None, None, None, I64(0), I64(4), I64(1), 64, 1, None) == 0
-    # gamma_grad: counts multiples of 8, b and gs together
-    st = lib.svtad_gamma_grad(buf, buf, I64(12), None, None, I64(0), buf, 1, None)
+    # gamma_grad: counts multiples of 8, b and gs together, workspace size
+    lib.svtad_gamma_grad_workspace_bytes.restype = ctypes.c_size_t
+    wsb = ctypes.c_size_t(lib.svtad_gamma_grad_workspace_bytes())
+    assert wsb.value == 256
+    st = lib.svtad_gamma_grad(buf, buf, I64(12), None, None, I64(0), buf, buf, wsb, 1, None)
     assert st == -1
-    st = lib.svtad_gamma_grad(buf, buf, I64(16), buf, None, I64(8), buf, 1, None)
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), buf, None, I64(8), buf, buf, wsb, 1, None)
     assert st == -1 and b"together" in lib.svtad_last_error()
-    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, 0, None)
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, buf, wsb, 0, None)
     assert st == -3
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, buf, ctypes.c_size_t(8), 1, None)
+    assert st == -2
 
 
 def test_dw_bwd_arguments_checked_on_host(lib):
