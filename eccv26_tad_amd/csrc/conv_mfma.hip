@@ -1318,13 +1318,20 @@ static void launch_wide(const void* src, const int32_t* nbr, const void* wb, con
                        tpb, n_col, tiles, flag);
 }
 
-// Row fragments per workgroup: the smallest instantiated count that keeps the
-// grid within one workgroup per CU (a second wave of workgroups on a few CUs
-// would double the kernel time).
+// Row fragments per workgroup. The kernels hold one workgroup per CU
+// (registers), so the time is about (rounds of workgroups) x (one
+// workgroup's time), and the latter grows with FM. The largest instantiated
+// FM gives the fewest rounds; take the smallest FM that needs no more rounds
+// than that. With one round this is the smallest FM whose grid fits the CUs;
+// when none fits (C = 256 at 27k rows: 282 workgroups at FM 6, 423 at FM 4,
+// two rounds either way) it evens the rounds out instead of leaving a second
+// round of a few workgroups (measured 50.1 -> 39.8 us there).
 static int pick_fm(int64_t n, int n_col, const int* have, int count) {
-    const int64_t need = cdiv(cdiv(n, 16) * n_col, cu_count());
+    const int64_t cu = cu_count();
+    auto rounds = [&](int fm) { return cdiv(cdiv(n, 16 * fm) * n_col, cu); };
+    const int64_t r_min = rounds(have[count - 1]);
     for (int q = 0; q < count; ++q)
-        if (have[q] >= need) return have[q];
+        if (rounds(have[q]) <= r_min) return have[q];
     return have[count - 1];
 }
 
@@ -1346,6 +1353,14 @@ static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, 
             // (measured 10.8 -> 8.2 us at 3136 rows, 14.4 -> 11.5 us at 7840).
             if (fm <= 2) {
                 launch_wide<T, MODE, CR, 3, 1, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
+                return;
+            }
+        }
+        if constexpr (CR == 256 && FN == 4) {
+            // the same at C = 256: 128-column tiles of three row fragments
+            // (measured 14.4 -> 11.7 us at 4916 rows)
+            if (fm <= 2) {
+                launch_wide<T, MODE, CR, 3, 2, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
                 return;
             }
         }
