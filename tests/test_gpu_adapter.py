@@ -109,6 +109,27 @@ def test_two_node_chain_matches_single_node(dev, dname):
         assert _err(a, b) <= 1e-2
 
 
+def test_local_table_matches_global(dev):
+    """Per-sample (local) neighbor indices through the reference's max()
+    heuristic (tokens_per_batch=None) give the same output and gradients as
+    the global table, bit for bit."""
+    dt = torch.float16
+    mod, _, idx, table, x, go = _setup(dev, dt, B=2, T=5, H=7, W=7, keep=0.5, embed=128, mlp_ratio=0.5,
+                                       S=1, seed=43)
+    nk = idx.shape[1]
+    local = torch.where(table >= 0, table % nk, table)
+    assert int(local.max()) < nk <= int(table.max())
+    outs = []
+    for tab, tpb in ((table, 0), (local, None)):
+        xi = x.detach().clone().requires_grad_(True)
+        y = mod(xi, 7, 7, idx, 5 * 49, tab, tokens_per_batch=tpb)
+        grads = torch.autograd.grad(y, [xi] + list(mod.parameters()), go)
+        outs.append((y, grads))
+    assert torch.equal(outs[0][0], outs[1][0])
+    for a, b in zip(outs[0][1], outs[1][1]):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("dname", ["float16", "bfloat16"])
 def test_adapter_kernels_direct(dev, dname):
     import eccv26_tad_amd as sv
