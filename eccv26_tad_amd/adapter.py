@@ -199,13 +199,12 @@ class SparseConvAdapterFunction(Function):
         else:
             G = _ops.linear_wgrad(go2, _NO_ROWS(go2), processed)
         gsum = _colsum(go2)
-        g_gamma = None
-        if need[7]:
-            g_gamma = _ops.gamma_grad(w_u, G, b_u, gsum if b_u is not None else None)
-            g_gamma = g_gamma.view(gamma.shape).to(gamma.dtype)
-        gw_u = G * gamma if need[5] else None
-        gb_u = gsum * gamma if b_u is not None and need[6] else None
-        dc = torch.matmul(go, w_u * gamma)  # [B, N, k]
+        # gamma's gradient and the gamma-scaled W_u, G and sum(go) in one pass
+        g_gamma, w_u_g, gw_u, gb_u = _ops.up_proj_grads(w_u, G, b_u, gsum if b_u is not None else None, gamma)
+        g_gamma = g_gamma.view(gamma.shape) if need[7] else None
+        gw_u = gw_u if need[5] else None
+        gb_u = gb_u if b_u is not None and need[6] else None
+        dc = torch.matmul(go, w_u_g)  # [B, N, k]: (go * gamma) W_u
         g_sp = dc[:, :S]
         g_pa = dc[:, S:].reshape(-1, k)
         # SparseConv2D

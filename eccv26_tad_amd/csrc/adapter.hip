@@ -351,13 +351,30 @@ __global__ __launch_bounds__(256) void k_gelu_bwd_split(const T* __restrict__ g_
 // workgroup's fixed tree keep the order fixed, and split_reduce adds the
 // slices in order.
 constexpr int kGammaParts = 64;
+// With gamma, the pass also writes the scaled copies the backward needs
+// (NULL outputs are skipped): w_sc = T(w * gamma), g_sc = T(g * gamma),
+// gs_sc = T(gs * gamma), each product in fp32 and rounded once, as PyTorch's
+// elementwise multiply rounds it.
 template <typename T>
 __global__ __launch_bounds__(256) void k_gamma_part(const T* __restrict__ w, const T* __restrict__ g,
                                                     int64_t chunks, const T* __restrict__ b,
                                                     const T* __restrict__ gs, int64_t chunks_b,
-                                                    float* __restrict__ part) {
+                                                    float* __restrict__ part, const T* __restrict__ gamma,
+                                                    T* __restrict__ w_sc, T* __restrict__ g_sc,
+                                                    T* __restrict__ gs_sc) {
     __shared__ float red[256];
     const int tid = threadIdx.x;
+    const float gm = gamma ? (float)gamma[0] : 0.f;
+    auto scale8 = [&](const u32x4 a) {
+        u32x4 o;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const T lo = (T)((float)__builtin_bit_cast(T, (u16)(a[h] & 0xffffu)) * gm);
+            const T hi = (T)((float)__builtin_bit_cast(T, (u16)(a[h] >> 16)) * gm);
+            o[h] = (unsigned)__builtin_bit_cast(u16, lo) | ((unsigned)__builtin_bit_cast(u16, hi) << 16);
+        }
+        return o;
+    };
     const int64_t total = chunks + chunks_b;
     const int64_t per = (total + kGammaParts - 1) / kGammaParts;
     const int64_t c0 = (int64_t)blockIdx.x * per, c1 = min(total, c0 + per);
@@ -370,8 +387,16 @@ __global__ __launch_bounds__(256) void k_gamma_part(const T* __restrict__ w, con
         }
     };
     for (int64_t c = c0 + tid; c < c1; c += 256) {
-        if (c < chunks) dot8(*(const u32x4*)(w + c * 8), *(const u32x4*)(g + c * 8));
-        else dot8(*(const u32x4*)(b + (c - chunks) * 8), *(const u32x4*)(gs + (c - chunks) * 8));
+        if (c < chunks) {
+            const u32x4 wv = *(const u32x4*)(w + c * 8), gv = *(const u32x4*)(g + c * 8);
+            dot8(wv, gv);
+            if (w_sc) *(u32x4*)(w_sc + c * 8) = scale8(wv);
+            if (g_sc) *(u32x4*)(g_sc + c * 8) = scale8(gv);
+        } else {
+            const u32x4 bv = *(const u32x4*)(b + (c - chunks) * 8), sv = *(const u32x4*)(gs + (c - chunks) * 8);
+            dot8(bv, sv);
+            if (gs_sc) *(u32x4*)(gs_sc + (c - chunks) * 8) = scale8(sv);
+        }
     }
     red[tid] = acc;
     __syncthreads();
@@ -525,26 +550,32 @@ extern "C" int svtad_gelu_backward_split(const void* grad_special, const void* g
 extern "C" size_t svtad_gamma_grad_workspace_bytes(void) { return (size_t)kGammaParts * sizeof(float); }
 
 extern "C" int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,
-                                int64_t count_b, void* out, void* workspace, size_t workspace_bytes, int dtype,
-                                void* stream) {
+                                int64_t count_b, void* out, const void* gamma, void* w_scaled, void* g_scaled,
+                                void* gs_scaled, void* workspace, size_t workspace_bytes, int dtype, void* stream) {
     if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
         return set_error(SVTAD_ERR_UNSUPPORTED, "gamma_grad: needs f16/bf16");
     if (count < 0 || count_b < 0 || count % 8 != 0 || count_b % 8 != 0 || (!b != !gs))
         return set_error(SVTAD_ERR_INVALID, "gamma_grad: counts must be multiples of 8; b and gs go together");
     if (!out || !workspace || (count > 0 && (!w || !g)) || (count_b > 0 && !b))
         return set_error(SVTAD_ERR_INVALID, "gamma_grad: null pointer");
-    if ((w && !al16(w)) || (g && !al16(g)) || (b && !al16(b)) || (gs && !al16(gs)))
-        return set_error(SVTAD_ERR_INVALID, "gamma_grad: inputs need 16-byte alignment");
+    if ((w && !al16(w)) || (g && !al16(g)) || (b && !al16(b)) || (gs && !al16(gs)) ||
+        (w_scaled && !al16(w_scaled)) || (g_scaled && !al16(g_scaled)) || (gs_scaled && !al16(gs_scaled)))
+        return set_error(SVTAD_ERR_INVALID, "gamma_grad: buffers need 16-byte alignment");
+    if (!gamma && (w_scaled || g_scaled || gs_scaled))
+        return set_error(SVTAD_ERR_INVALID, "gamma_grad: scaled outputs need gamma");
+    if (gs_scaled && !b) return set_error(SVTAD_ERR_INVALID, "gamma_grad: gs_scaled needs b and gs");
     if (workspace_bytes < svtad_gamma_grad_workspace_bytes())
         return set_error(SVTAD_ERR_WORKSPACE, "gamma_grad: workspace smaller than svtad_gamma_grad_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;
     const int64_t nb = b ? count_b / 8 : 0;
     if (dtype == SVTAD_F16)
         hipLaunchKernelGGL((k_gamma_part<f16>), dim3(kGammaParts), dim3(256), 0, s, (const f16*)w, (const f16*)g,
-                           count / 8, (const f16*)b, (const f16*)gs, nb, (float*)workspace);
+                           count / 8, (const f16*)b, (const f16*)gs, nb, (float*)workspace, (const f16*)gamma,
+                           (f16*)w_scaled, (f16*)g_scaled, (f16*)gs_scaled);
     else
         hipLaunchKernelGGL((k_gamma_part<bf16>), dim3(kGammaParts), dim3(256), 0, s, (const bf16*)w, (const bf16*)g,
-                           count / 8, (const bf16*)b, (const bf16*)gs, nb, (float*)workspace);
+                           count / 8, (const bf16*)b, (const bf16*)gs, nb, (float*)workspace, (const bf16*)gamma,
+                           (bf16*)w_scaled, (bf16*)g_scaled, (bf16*)gs_scaled);
     split_reduce(dtype, workspace, 1, kGammaParts, out, s);
     return launch_status();
 }

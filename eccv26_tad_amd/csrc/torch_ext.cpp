@@ -769,9 +769,50 @@ at::Tensor op_gamma_grad(const at::Tensor& w_in, const at::Tensor& g_in, const c
     at::Tensor work = at::empty({(int64_t)wsb}, w.options().dtype(at::kByte));
     check_status(svtad_gamma_grad(w.data_ptr(), g.data_ptr(), w.numel(), b.defined() ? b.data_ptr() : nullptr,
                                   gs.defined() ? gs.data_ptr() : nullptr, b.defined() ? b.numel() : 0,
-                                  out.data_ptr(), work.data_ptr(), wsb, dtype_code(w), stream_of(w)),
+                                  out.data_ptr(), nullptr, nullptr, nullptr, nullptr, work.data_ptr(), wsb,
+                                  dtype_code(w), stream_of(w)),
                  "gamma_grad");
     return out;
+}
+
+// up_proj_grads(w, g, b or None, gs or None, gamma [1]) ->
+//   (grad_gamma [1], w * gamma, g * gamma, gs * gamma or empty): the gamma
+//   gradient and the gamma-scaled tensors of the adapter's up-projection
+//   backward in one pass
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> op_up_proj_grads(
+    const at::Tensor& w_in, const at::Tensor& g_in, const c10::optional<at::Tensor>& b_in,
+    const c10::optional<at::Tensor>& gs_in, const at::Tensor& gamma_in) {
+    check_gpu(w_in, "w");
+    check_gpu(g_in, "g");
+    check_gpu(gamma_in, "gamma");
+    TORCH_CHECK(w_in.scalar_type() == g_in.scalar_type() && gamma_in.scalar_type() == w_in.scalar_type(),
+                "w, g and gamma dtypes differ");
+    TORCH_CHECK(w_in.scalar_type() == at::kHalf || w_in.scalar_type() == at::kBFloat16,
+                "up_proj_grads takes float16 / bfloat16, got ", w_in.scalar_type());
+    TORCH_CHECK(w_in.numel() == g_in.numel() && gamma_in.numel() == 1, "w and g must match; gamma one element");
+    at::Tensor w = w_in.contiguous(), g = g_in.contiguous(), gm = gamma_in.contiguous(), b, gs;
+    if (bias_present(b_in)) {
+        TORCH_CHECK(gs_in.has_value() && gs_in->defined() && gs_in->numel() == b_in->numel(), "gs must match b");
+        check_gpu(*b_in, "b");
+        check_gpu(*gs_in, "gs");
+        TORCH_CHECK(b_in->scalar_type() == w.scalar_type() && gs_in->scalar_type() == w.scalar_type(),
+                    "b and gs must have the dtype of w");
+        b = b_in->contiguous();
+        gs = gs_in->contiguous();
+    }
+    c10::DeviceGuard guard(w.device());
+    at::Tensor out = at::empty({1}, w.options());
+    at::Tensor w_sc = at::empty_like(w), g_sc = at::empty_like(g);
+    at::Tensor gs_sc = b.defined() ? at::empty_like(gs) : at::empty({0}, w.options());
+    const size_t wsb = svtad_gamma_grad_workspace_bytes();
+    at::Tensor work = at::empty({(int64_t)wsb}, w.options().dtype(at::kByte));
+    check_status(svtad_gamma_grad(w.data_ptr(), g.data_ptr(), w.numel(), b.defined() ? b.data_ptr() : nullptr,
+                                  gs.defined() ? gs.data_ptr() : nullptr, b.defined() ? b.numel() : 0,
+                                  out.data_ptr(), gm.data_ptr(), w_sc.data_ptr(), g_sc.data_ptr(),
+                                  b.defined() ? gs_sc.data_ptr() : nullptr, work.data_ptr(), wsb, dtype_code(w),
+                                  stream_of(w)),
+                 "up_proj_grads");
+    return {out, w_sc, g_sc, gs_sc};
 }
 
 PYBIND11_MODULE(opentad_sparse_ops, m) {
@@ -844,6 +885,9 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.def("gelu_backward_split", &op_gelu_backward_split,
           "GELU backward of the adapter's down projection from split special / patch gradients",
           py::arg("grad_special"), py::arg("grad_patch"), py::arg("pre_act"), py::arg("n_special"));
+    m.def("up_proj_grads", &op_up_proj_grads,
+          "Adapter up projection: gamma gradient plus w, g, gs scaled by gamma, in one pass",
+          py::arg("w"), py::arg("g"), py::arg("b"), py::arg("gs"), py::arg("gamma"));
     m.def("gamma_grad", &op_gamma_grad, "sum(w * g) + sum(b * gs) in fp32 (the adapter's gamma gradient)",
           py::arg("w"), py::arg("g"), py::arg("b"), py::arg("gs"));
     m.def("version", []() { return std::string(svtad_version()); });

@@ -345,13 +345,18 @@ int svtad_gelu_backward_split(const void* grad_special, const void* grad_patch, 
  * sum_j b[j] gs[j], with w the up projection's weight, g = go^T c its
  * unscaled weight gradient, b its bias (NULL: none) and gs the column sums of
  * go. fp32 accumulation over 64 slices added in a fixed order, out (one
- * element) in `dtype`. f16 / bf16; counts multiples of 8; 16-byte aligned;
- * workspace of svtad_gamma_grad_workspace_bytes(). Two launches on `stream`.
+ * element) in `dtype`. With gamma (one element, device) the same pass writes
+ * the scaled copies the up projection's backward uses in place of three
+ * elementwise multiplies: w_scaled = w * gamma (for the input gradient),
+ * g_scaled = g * gamma (the weight gradient), gs_scaled = gs * gamma (the
+ * bias gradient); NULL skips one. f16 / bf16; counts multiples of 8; 16-byte
+ * aligned; workspace of svtad_gamma_grad_workspace_bytes(). Two launches on
+ * `stream`.
  */
 size_t svtad_gamma_grad_workspace_bytes(void);
 int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,
-                     int64_t count_b, void* out, void* workspace, size_t workspace_bytes, int dtype,
-                     void* stream);
+                     int64_t count_b, void* out, const void* gamma, void* w_scaled, void* g_scaled,
+                     void* gs_scaled, void* workspace, size_t workspace_bytes, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

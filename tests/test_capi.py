@@ -167,14 +167,18 @@ def test_adapter_backward_arguments_checked_on_host(lib):
     lib.svtad_gamma_grad_workspace_bytes.restype = ctypes.c_size_t
     wsb = ctypes.c_size_t(lib.svtad_gamma_grad_workspace_bytes())
     assert wsb.value == 256
-    st = lib.svtad_gamma_grad(buf, buf, I64(12), None, None, I64(0), buf, buf, wsb, 1, None)
+    N4 = (None, None, None, None)
+    st = lib.svtad_gamma_grad(buf, buf, I64(12), None, None, I64(0), buf, *N4, buf, wsb, 1, None)
     assert st == -1
-    st = lib.svtad_gamma_grad(buf, buf, I64(16), buf, None, I64(8), buf, buf, wsb, 1, None)
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), buf, None, I64(8), buf, *N4, buf, wsb, 1, None)
     assert st == -1 and b"together" in lib.svtad_last_error()
-    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, buf, wsb, 0, None)
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, *N4, buf, wsb, 0, None)
     assert st == -3
-    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, buf, ctypes.c_size_t(8), 1, None)
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, *N4, buf, ctypes.c_size_t(8), 1, None)
     assert st == -2
+    # scaled outputs need gamma
+    st = lib.svtad_gamma_grad(buf, buf, I64(16), None, None, I64(0), buf, None, buf, None, None, buf, wsb, 1, None)
+    assert st == -1 and b"gamma" in lib.svtad_last_error()
 
 
 def test_dw_bwd_arguments_checked_on_host(lib):
@@ -208,7 +212,7 @@ def test_extension_module_api():
     for name in ("fwd_bias", "bwd_w_bias", "dw_fwd", "dw_bwd_in", "dw_bwd_w",
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
                  "validate_neighbor_table", "prune_tokens", "bwd_packed", "adapter_down",
-                 "adapter_up", "linear_wgrad", "column_sums", "gelu_backward_split", "gamma_grad",
+                 "adapter_up", "linear_wgrad", "column_sums", "gelu_backward_split", "gamma_grad", "up_proj_grads",
                  "dw_bwd"):
         assert hasattr(ops, name)
     import torch

@@ -276,3 +276,27 @@ def test_gamma_grad(dev, dname, count, count_b):
     assert out.shape == (1,) and out.dtype == dt
     assert abs(float(out) - float(ref)) <= 1e-2 * max(float(scale), 1e-6) + 1e-3 * abs(float(ref))
     assert torch.equal(out, sv.ops.gamma_grad(w, gm, b, gs))
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_up_proj_grads(dev, dname, with_bias):
+    """The gamma gradient equals gamma_grad, and the scaled copies equal
+    PyTorch's elementwise multiplies bit for bit (one fp32 product, one
+    rounding)."""
+    import eccv26_tad_amd as sv
+
+    dt = getattr(torch, dname)
+    gen = torch.Generator().manual_seed(5 + with_bias)
+    w = torch.randn(768, 256, generator=gen).to(dev, dt)
+    g = torch.randn(768, 256, generator=gen).to(dev, dt)
+    b = torch.randn(768, generator=gen).to(dev, dt) if with_bias else None
+    gs = torch.randn(768, generator=gen).to(dev, dt) if with_bias else None
+    gamma = torch.tensor([0.37], device=dev, dtype=dt)
+    gg, w_s, g_s, gs_s = sv.ops.up_proj_grads(w, g, b, gs, gamma)
+    assert torch.equal(gg, sv.ops.gamma_grad(w, g, b, gs))
+    assert torch.equal(w_s, w * gamma) and torch.equal(g_s, g * gamma)
+    if with_bias:
+        assert torch.equal(gs_s, gs * gamma)
+    else:
+        assert gs_s.numel() == 0
