@@ -1,5 +1,5 @@
-"""SparseConv2D at the full benchmark sizes (configs c2, c4, c5 of the
-benchmark plan): the neighbor table bit-exact against the oracle's closed
+"""SparseConv2D at the full benchmark sizes (configs c2, c4 at 25 % and
+55 % keep, c5 of the benchmark plan; the depthwise c3 at the end): the neighbor table bit-exact against the oracle's closed
 form, forward and backward-input on a seeded 2048-row subsample against the
 fp64 oracle (run on the compacted sub-problem those rows need), and the
 weight / bias gradients (sums over every row) against an fp64 gather +
@@ -133,3 +133,40 @@ def test_c5_full_size_ragged(dev, oracle):
     _say("c5 full size")
     mask = _ragged_mask(np.random.default_rng(1005), 4, 128, 16, 16)
     _run(dev, oracle, mask, 512, "bfloat16", 2005)
+
+
+def test_c4_full_size_keep055(dev, oracle):
+    """c4 at 55 % keep (N = 27034): the gathered GEMMs run four row fragments
+    per workgroup in two even rounds (no single round fits)."""
+    _say("c4 full size 55 %")
+    mask = topk_mask(np.random.default_rng(1014), 2, 96, 16, 16, 0.55)
+    _run(dev, oracle, mask, 256, "bfloat16", 2014)
+
+
+def test_c3_depthwise_full_size(dev, oracle):
+    """c3: depthwise C=192 fp16 on B2 x T80 x 14x14 at 55 % keep: forward and
+    the one-pass backward (input, weight, bias gradients) against the fp64
+    oracle at full size."""
+    import torch
+
+    import opentad_sparse_ops as ops
+
+    _say("c3 depthwise full size")
+    rng = np.random.default_rng(1003)
+    mask = topk_mask(rng, 2, 80, 14, 14, 0.55)
+    t = oracle.build_table(mask)
+    n, c = t.shape[0], 192
+    dt = torch.float16
+    x = torch.from_numpy(rng.standard_normal((n, c)).astype(np.float32)).to(dt)
+    w = torch.from_numpy((rng.standard_normal((9, c)) * 0.3).astype(np.float32)).to(dt)
+    b = torch.from_numpy((rng.standard_normal(c) * 0.1).astype(np.float32)).to(dt)
+    go = torch.from_numpy(rng.standard_normal((n, c)).astype(np.float32)).to(dt)
+    xn, wn, bn, gn = (a.float().numpy() for a in (x, w, b, go))
+    T = torch.from_numpy(t).to(dev)
+    y = ops.dw_fwd(x.to(dev), T, w.to(dev), b.to(dev), 0)
+    gi, gw, gb = ops.dw_bwd(go.to(dev), x.to(dev), T, w.to(dev), 0, True)
+    tol = TOL["float16"]
+    assert oracle.rel_err(y.cpu().double().numpy(), oracle.dw_fwd(xn, t, wn, bn)) <= tol
+    assert oracle.rel_err(gi.cpu().double().numpy(), oracle.dw_bwd_in(gn, t, wn)) <= tol
+    assert oracle.rel_err(gw.cpu().double().numpy(), oracle.dw_bwd_w(gn, xn, t)) <= tol
+    assert oracle.rel_err(gb.cpu().double().numpy(), oracle.bias_grad(gn)) <= tol
