@@ -484,7 +484,9 @@ extern "C" int svtad_linear_wgrad(const void* g, const int32_t* rows, const void
         return set_error(SVTAD_ERR_INVALID, "linear_wgrad: g and x need 16-byte alignment");
     if (workspace_bytes < p.ws_bytes)
         return set_error(SVTAD_ERR_WORKSPACE, "linear_wgrad: workspace smaller than svtad_linear_wgrad_workspace_bytes()");
-    wgrad_mfma(dtype, p, g, rows, x, out, workspace, n, rows ? n_g_rows : n, c_g, c_x, (hipStream_t)stream);
+    const int st = wgrad_mfma(dtype, p, g, rows, x, out, workspace, workspace_bytes, n, rows ? n_g_rows : n, c_g,
+                              c_x, (hipStream_t)stream);
+    if (st) return st;
     return launch_status();
 }
 
@@ -547,6 +549,13 @@ extern "C" int svtad_gelu_backward_split(const void* grad_special, const void* g
     return launch_status();
 }
 
+// Heatmap injection of the adapter (vit_sparse_adapter_poguise.py:311-355):
+// patch[i] = T(patch[i] + T(special[src[i]] * gate)), in place, with src[i]
+// the flattened special-token row (b * S + 1 + heatmap cell) patch row i
+// samples. A thread owns 8 channels (16 bytes) of one row; rows whose source
+// is outside [0, n_special_rows) are left unchanged. The patch rows gather
+// special rows that other workgroups of the down GEMM produce, so the add
+// is a launch of its own after that GEMM.
 extern "C" size_t svtad_gamma_grad_workspace_bytes(void) { return (size_t)kGammaParts * sizeof(float); }
 
 extern "C" int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,

@@ -40,9 +40,10 @@ static int check_common(const char* who, int64_t n, int c_in, int c_out, int64_t
 }
 
 // Full conv plan. Rows are split so that the partial-tile workgroups fill the
-// chip's compute units at most once (a second round of workgroups on a few
+// chip's compute units in whole rounds (a second round of workgroups on a few
 // units would nearly double the kernel time), without splits shorter than 256
-// rows, and so that no split is longer than 2048 rows.
+// rows where n allows, and so that no split is longer than kMaxSplitRows - 128
+// rows.
 static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     BwPlan p;
     p.path = bw_mfma_supported(dtype, n, c_in, c_out) ? 1 : 0;
@@ -248,10 +249,12 @@ extern "C" int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* n
     if (workspace_bytes < p.ws_bytes)
         return set_error(SVTAD_ERR_WORKSPACE, "bwd_w: workspace smaller than svtad_bwd_w_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;
-    if (p.path == 1)
-        bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
-                tokens_per_batch, nullptr, s);
-    else
+    if (p.path == 1) {
+        bool unused;
+        st = bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, workspace_bytes, n, c_in, c_out,
+                     tokens_per_batch, nullptr, &unused, s);
+        if (st) return st;
+    } else
         bw_valu(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
                 tokens_per_batch, s);
     return launch_status();
@@ -287,10 +290,11 @@ extern "C" int svtad_bwd_packed(const void* grad_out, const void* x, const int32
     // 2. grad_w / grad_bias; the reduction also runs the orphan pass of step 1
     const OrphanJob job{grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, flag};
     bool taken = false;
-    if (p.path == 1)
-        taken = bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
-                        tokens_per_batch, n > 0 ? &job : nullptr, s);
-    else
+    if (p.path == 1) {
+        st = bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, workspace_bytes, n, c_in, c_out,
+                     tokens_per_batch, n > 0 ? &job : nullptr, &taken, s);
+        if (st) return st;
+    } else
         bw_valu(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
                 tokens_per_batch, s);
     if (n > 0 && !taken)

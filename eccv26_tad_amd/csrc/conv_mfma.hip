@@ -20,8 +20,11 @@
 // mapping, so the pairing of reduction values matches by construction.
 #include <type_traits>
 
+#include <stdio.h>
+
 #include "sv_common.h"
 #include "sv_conv.h"
+#include "sv_internal.h"
 #include "sv_mfma.h"
 
 namespace svtad {
@@ -1063,7 +1066,12 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     const int steps = (rows + KR - 1) / KR;
     const bool do_bias = ws_bias != nullptr && k == (n_off == 9 ? 4 : 0) && ci0 == 0;  // uniform
 
-    for (int r = tid; r < (steps + 2) * KR; r += NT) {
+    // The staging waves read the list two stages at a time up to stage
+    // steps_even + 1 (steps rounded up to even), so it is filled that far;
+    // with rows_per_split <= kMaxSplitRows (checked on the host) that is at
+    // most TROWS entries.
+    const int steps_even = (steps + 1) & ~1;
+    for (int r = tid; r < (steps_even + 2) * KR; r += NT) {
         int64_t sr = -1;
         if (r < rows) {
             if (n_off == 9) {
@@ -1454,16 +1462,42 @@ bool bw_mfma_supported(int dtype, int64_t n, int c_in, int c_out) {
 // Tile edge for a bwd-weight dimension: 96 when it divides, else 64, else 32.
 int bw_mfma_tile(int c) { return c % 96 == 0 ? 96 : (c % 64 == 0 ? 64 : 32); }
 
+// Host checks of a row-split plan against what the backward-weight partial
+// kernels assume before any launch: splits of whole pairs of 64-row stages,
+// each within the split's LDS row list (kMaxSplitRows), every row in some
+// split, and a workspace that holds every workgroup's partial tile (part_bytes).
+static int check_split_plan(const char* who, const BwPlan& p, int64_t n, size_t part_bytes,
+                            size_t ws_bytes) {
+    static thread_local char buf[256];
+    if (p.splits < 1 || p.rows_per_split <= 0 || p.rows_per_split % (2 * KR) != 0 ||
+        p.rows_per_split > kMaxSplitRows || (int64_t)p.splits * p.rows_per_split < n) {
+        snprintf(buf, sizeof(buf), "%s: bad row-split plan (splits=%d rows_per_split=%lld n=%lld)", who,
+                 p.splits, (long long)p.rows_per_split, (long long)n);
+        return set_error(SVTAD_ERR_INVALID, buf);
+    }
+    if (part_bytes > ws_bytes) {
+        snprintf(buf, sizeof(buf), "%s: %zu partial bytes exceed the %zu-byte workspace", who, part_bytes,
+                 ws_bytes);
+        return set_error(SVTAD_ERR_WORKSPACE, buf);
+    }
+    return SVTAD_OK;
+}
+
 template <typename T, int FM, int FN>
-static void launch_bw(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
-                      float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
-                      hipStream_t s) {
+static int launch_bw(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                     float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
+                     size_t ws_bytes, hipStream_t s) {
     constexpr int BM = 2 * FM * 16, BN = 2 * FN * 16;
     const int nci = (int)cdiv(c_in, BM), nco = (int)cdiv(c_out, BN);
     const int64_t blocks = (int64_t)9 * nci * nco * p.splits;
+    // ws[s][k][ci][co] for ci < c_in, co < c_out, then the bias partials
+    const size_t need = (size_t)p.splits * 9 * c_in * c_out * 4 + (part_b ? (size_t)p.splits * c_out * 4 : 0);
+    const int st = check_split_plan("bwd_w", p, n, need, ws_bytes);
+    if (st) return st;
     hipLaunchKernelGGL((k_bw_mfma<T, FM, FN>), dim3((unsigned)blocks), dim3(256), 0, s,
                        (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
                        p.rows_per_split, nci, nco, blocks);
+    return SVTAD_OK;
 }
 
 // Large-tile backward-weight configurations: WGM x WGN waves, each with
@@ -1495,29 +1529,34 @@ void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn) {
 }
 
 template <typename T, int FM, int FN, int WGM, int WGN>
-static void launch_big(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
-                       float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
-                       hipStream_t s) {
+static int launch_big(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                      float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
+                      size_t ws_bytes, hipStream_t s) {
     constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
-    const int nci = (int)cdiv(c_in, BM), nco = (int)cdiv(c_out, BN);
+    if (c_in % BM != 0 || c_out % BN != 0) return set_error(SVTAD_ERR_INVALID, "bwd_w: widths are not whole tiles");
+    const int nci = c_in / BM, nco = c_out / BN;
     const int64_t blocks = (int64_t)9 * nci * nco * p.splits;
+    // one BM x BN tile per workgroup (splits x 9 x nci x nco of them), then
+    // the bias partials
+    const size_t need = (size_t)blocks * BM * BN * 4 + (part_b ? (size_t)p.splits * c_out * 4 : 0);
+    const int st = check_split_plan("bwd_w", p, n, need, ws_bytes);
+    if (st) return st;
     hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks),
                        dim3(bw_big_threads(FM, FN, WGM, WGN)),
                        0, s, (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
                        p.rows_per_split, nci, nco, blocks, 9, n);
+    return SVTAD_OK;
 }
 
 template <typename T>
-static void bw_dispatch(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
-                        float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
-                        hipStream_t s) {
+static int bw_dispatch(const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+                       float* part, float* part_b, int64_t n, int c_in, int c_out, int64_t tpb,
+                       size_t ws_bytes, hipStream_t s) {
     BigCfg bc;
     if (big_cfg(c_in, c_out, &bc)) {
-#define SVTAD_BIG_CASE(M, N, WM, WN)                                                          \
-    if (bc.fm == M && bc.fn == N && bc.wgm == WM && bc.wgn == WN) {                           \
-        launch_big<T, M, N, WM, WN>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);    \
-        return;                                                                               \
-    }
+#define SVTAD_BIG_CASE(M, N, WM, WN)                                                                   \
+    if (bc.fm == M && bc.fn == N && bc.wgm == WM && bc.wgn == WN)                                      \
+        return launch_big<T, M, N, WM, WN>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, ws_bytes, s);
         SVTAD_BIG_CASE(6, 3, 2, 4)
         SVTAD_BIG_CASE(4, 4, 2, 4)
         SVTAD_BIG_CASE(4, 2, 2, 4)
@@ -1526,11 +1565,9 @@ static void bw_dispatch(const BwPlan& p, const void* go, const void* x, const in
 #undef SVTAD_BIG_CASE
     }
     const int tm = bw_mfma_tile(c_in), tn = bw_mfma_tile(c_out);
-#define SVTAD_BW_CASE(M, N)                                                                 \
-    if (tm == M && tn == N) {                                                               \
-        launch_bw<T, M / 32, N / 32>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s); \
-        return;                                                                             \
-    }
+#define SVTAD_BW_CASE(M, N)                                                                              \
+    if (tm == M && tn == N)                                                                              \
+        return launch_bw<T, M / 32, N / 32>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, ws_bytes, s);
     SVTAD_BW_CASE(96, 96)
     SVTAD_BW_CASE(96, 64)
     SVTAD_BW_CASE(64, 96)
@@ -1541,16 +1578,20 @@ static void bw_dispatch(const BwPlan& p, const void* go, const void* x, const in
     SVTAD_BW_CASE(32, 64)
     SVTAD_BW_CASE(32, 32)
 #undef SVTAD_BW_CASE
+    return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_w: no tile configuration for these widths");
 }
 
-bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
-             void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
-             const OrphanJob* oj, hipStream_t s) {
+int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+            void* gw, void* gb, void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb,
+            const OrphanJob* oj, bool* oj_taken, hipStream_t s) {
+    *oj_taken = false;
     float* part = (float*)ws;
     float* part_b = gb ? part + (int64_t)p.splits * 9 * c_in * c_out : nullptr;
-    if (dtype == SVTAD_F16) bw_dispatch<f16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
-    else bw_dispatch<bf16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, s);
-    if (!gw) return false;  // partials only
+    const int st = dtype == SVTAD_F16
+                       ? bw_dispatch<f16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, ws_bytes, s)
+                       : bw_dispatch<bf16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, ws_bytes, s);
+    if (st) return st;
+    if (!gw) return SVTAD_OK;  // partials only
     BigCfg bc;
     if (big_cfg(c_in, c_out, &bc)) {
         const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
@@ -1565,11 +1606,12 @@ bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const in
             hipLaunchKernelGGL((k_bw_reduce<bf16>), grid, dim3(256), 0, s, (const float*)part,
                                (const float*)part_b, p.splits, 9, c_in, c_out, bc.fm, bc.fn, bc.wgm,
                                bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb, job);
-        return oj != nullptr;
+        *oj_taken = oj != nullptr;
+        return SVTAD_OK;
     }
     split_reduce(dtype, part, 9LL * c_in * c_out, p.splits, gw, s);
     if (gb) split_reduce(dtype, part_b, (int64_t)c_out, p.splits, gb, s);
-    return false;
+    return SVTAD_OK;
 }
 
 // Row-split plan of a linear layer's weight gradient (one offset): splits
@@ -1592,11 +1634,16 @@ BwPlan plan_wgrad(int64_t n, int c_in, int c_out) {
 }
 
 template <typename T, int FM, int FN, int WGM, int WGN>
-static void launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
-                         float* part, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s) {
+static int launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
+                        float* part, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out,
+                        hipStream_t s) {
     constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
+    if (c_in % BM != 0 || c_out % BN != 0)
+        return set_error(SVTAD_ERR_INVALID, "linear_wgrad: widths are not whole tiles");
     const int nci = c_in / BM, nco = c_out / BN;
     const int64_t blocks = (int64_t)nci * nco * p.splits;
+    const int st = check_split_plan("linear_wgrad", p, n, (size_t)blocks * BM * BN * 4, ws_bytes);
+    if (st) return st;
     // the kernel's "x" (gathered, ci) is g and its "go" (linear, co) is x
     hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks),
                        dim3(bw_big_threads(FM, FN, WGM, WGN)), 0, s, (const T*)x, (const T*)g, rows,
@@ -1606,26 +1653,26 @@ static void launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, co
     const OrphanJob none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
     hipLaunchKernelGGL((k_bw_reduce<T>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
                        p.splits, 1, c_in, c_out, FM, FN, WGM, WGN, nci, nco, (T*)out, (T*)nullptr, none);
+    return SVTAD_OK;
 }
 
-bool wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
-                void* ws, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s) {
+int wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
+               void* ws, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s) {
     BigCfg bc;
-    if (!p.path || !big_cfg(c_in, c_out, &bc)) return false;
-#define SVTAD_WG_CASE(M, N, WM, WN)                                                                   \
-    if (bc.fm == M && bc.fn == N && bc.wgm == WM && bc.wgn == WN) {                                   \
-        if (dtype == SVTAD_F16) launch_wgrad<f16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, n, n_src, c_in, c_out, s); \
-        else launch_wgrad<bf16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, n, n_src, c_in, c_out, s);  \
-        found = true;                                                                                 \
-    }
-    bool found = false;
+    if (!p.path || !big_cfg(c_in, c_out, &bc))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: no tile configuration for these widths");
+#define SVTAD_WG_CASE(M, N, WM, WN)                                                                           \
+    if (bc.fm == M && bc.fn == N && bc.wgm == WM && bc.wgn == WN)                                             \
+        return dtype == SVTAD_F16                                                                             \
+                   ? launch_wgrad<f16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, ws_bytes, n, n_src, c_in, c_out, s) \
+                   : launch_wgrad<bf16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, ws_bytes, n, n_src, c_in, c_out, s);
     SVTAD_WG_CASE(6, 3, 2, 4)
-    else SVTAD_WG_CASE(4, 4, 2, 4)
-    else SVTAD_WG_CASE(4, 2, 2, 4)
-    else SVTAD_WG_CASE(3, 3, 2, 2)
-    else SVTAD_WG_CASE(2, 2, 2, 2)
+    SVTAD_WG_CASE(4, 4, 2, 4)
+    SVTAD_WG_CASE(4, 2, 2, 4)
+    SVTAD_WG_CASE(3, 3, 2, 2)
+    SVTAD_WG_CASE(2, 2, 2, 2)
 #undef SVTAD_WG_CASE
-    return found;
+    return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: no tile configuration for these widths");
 }
 
 }  // namespace svtad

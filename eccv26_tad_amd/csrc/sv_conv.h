@@ -96,18 +96,23 @@ struct OrphanJob {
     int64_t tpb;
     const uint32_t* flag;
 };
-// Returns true when oj (may be NULL) was run by the reduction; false leaves
-// it to the caller (gw NULL or a shape without the large-tile reduction).
-bool bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
-             void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
-             const OrphanJob* oj, hipStream_t s);
+// Returns SVTAD_OK, or an SVTAD_ERR_* (message set, nothing launched) when
+// the plan or the workspace (ws_bytes) does not fit what the kernels assume.
+// *oj_taken says whether oj (may be NULL) was run by the reduction; false
+// leaves it to the caller (gw NULL or a shape without the large-tile
+// reduction).
+int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
+            void* gw, void* gb, void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb,
+            const OrphanJob* oj, bool* oj_taken, hipStream_t s);
 
 // A linear layer's weight gradient out[ci][co] = sum_i g[rows[i]][ci] x[i][co]
 // (rows NULL: row i of g), i < n, on the backward-weight partial kernel with
 // one offset and its ordered reduction. path 0 in the plan: no large-tile
-// configuration for (c_in, c_out); wgrad_mfma then returns false.
+// configuration for (c_in, c_out); wgrad_mfma then returns
+// SVTAD_ERR_UNSUPPORTED. Returns SVTAD_OK or an SVTAD_ERR_* (nothing
+// launched) as bw_mfma.
 BwPlan plan_wgrad(int64_t n, int c_in, int c_out);
-bool wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
-                void* ws, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s);
+int wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
+               void* ws, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s);
 
 }  // namespace svtad
