@@ -2,19 +2,27 @@
 
 Reference: the ``conv_type == "sparse_conv"`` adapter of
 ``opentad/models/backbones/vit_sparse_adapter_poguise.py`` (constructor
-``:95-111,163-166``, forward ``:290-362`` and ``:652-653``), without the
-optional heatmap injection (``:316-355``) and attention branch, which this
-module does not implement (it raises when asked for them):
+``:78-166``, forward ``:288-362`` and ``:511-653``), every variant of it:
 
     x_proj = GELU(down_proj(x))                      # [B, N, hidden]
     special, patches = x_proj[:, :S], x_proj[:, S:]  # S = N - indices.shape[1]
+    patches += heatmap_gate * special[1 + cell(i)]   # heatmap injection (:311-355)
     processed = sparse_conv(patches, neighbor_indices)
-    y = up_proj(cat(special, processed)) * gamma + x
+    c = cat(special, processed)
+    c = attention_branch(c)                          # use_attn >= 1 (:511-650)
+    y = up_proj(c) * gamma + x
 
-The module runs as one autograd node (``SparseConvAdapterFunction``); its
-forward is the down GEMM (``opentad_sparse_ops.adapter_down``), the
-SparseConv2D forward (weight pack + gathered GEMM) and the up GEMM
-(``opentad_sparse_ops.adapter_up``):
+The heatmap injection runs when ``n_key_tokens > 1``, ``heatmap_grid_size``
+is set and ``use_attn == 0``; ``use_attn`` 1-3 adds the attention over the
+adapter tokens (1: all tokens, 2: visual tokens attend to the key tokens,
+3: key tokens attend to the visual tokens; ``shortcut + attn_proj(.) *
+attn_gamma``), 4 and above the temporal attention over frame-pooled tokens.
+
+Without attention the module runs as one autograd node
+(``SparseConvAdapterFunction``); its forward is the down GEMM
+(``opentad_sparse_ops.adapter_down``), the heatmap gather-add when it
+applies (``heatmap_add_``), the SparseConv2D forward (weight pack +
+gathered GEMM) and the up GEMM (``opentad_sparse_ops.adapter_up``):
 
 * the down GEMM's epilogue adds the bias, rounds the Linear output, applies
   GELU and writes the special tokens and the (contiguous) SparseConv2D input
@@ -25,6 +33,14 @@ SparseConv2D forward (weight pack + gathered GEMM) and the up GEMM
 * ``tokens_per_batch`` defaults to 0 (the tables the backbone builds are
   global), so there is no host sync; ``None`` restores the reference's
   ``max()`` heuristic (``sparse_conv_layer.py:174-177``).
+
+With attention the adapter is a chain of nodes: the fused down GEMM
+(``AdapterDownFunction``), SparseConv2D, the concatenation and the
+reference's attention ops (LayerNorm, Linear, attention), then the same up
+GEMM epilogue for both ``shortcut + attn_proj(.) * attn_gamma`` and
+``up_proj(c) * gamma + x`` (``AdapterUpFunction`` with no special tokens: the
+A rows are the ``[B, N, .]`` input itself). The attention is evaluated in
+float32 (``_attention``).
 
 The backward's weight gradients (sums over every token row) run on the
 split-row kernel of SparseConv2D's backward-weight pass with one offset
@@ -37,16 +53,22 @@ gradient needs ``z = cat(...) W_u^T + b_u``, which the fused forward never
 stores: ``sum(go * z) = <W_u, go^T c> + <b_u, sum(go)>``, and ``go^T c`` is
 the up-projection's weight-gradient reduction anyway; one launch adds both
 products (``opentad_sparse_ops.gamma_grad``). The bias gradients (column sums
-over the token rows) use ``opentad_sparse_ops.column_sums``.
+over the token rows) use ``opentad_sparse_ops.column_sums``. The heatmap
+injection's backward is the gather's: a scatter-add of ``g * gate`` into the
+special-token gradient and ``sum(g * sampled)`` for the gate, in PyTorch.
 
 The input gradient is one GEMM with the residual's term as its addend
 (``addmm(go, du, W_d)``), which the single node makes possible.
 ``AdapterDownFunction`` and ``AdapterUpFunction`` are the same kernels as two
 separate nodes around a ``SparseConv2d``.
 
-The fused path takes float16 / bfloat16 (the matrix-core dtypes) and raises
-otherwise; ``reference_forward`` runs the unfused chain in the reference's op
-order (for tests and the benchmark).
+The fused path takes float16 / bfloat16 GPU tensors with parameters of the
+same dtype, outside autocast. Any other call (float32 input, autocast with
+float32 parameters as in the reference's training loop, CPU tensors, no
+kept tokens) runs ``reference_forward``: the unfused chain in the
+reference's op order, whose SparseConv2d applies the reference's autocast
+casts, so the output dtype is the reference's (float32 under autocast with
+a float32 ``gamma``).
 """
 from __future__ import annotations
 
@@ -73,6 +95,16 @@ def _colsum(a):
 def _NO_ROWS(like):
     """Empty row list: the weight-gradient kernel then takes rows in order."""
     return torch.empty(0, dtype=torch.int32, device=like.device)
+
+
+def _wgrad(g, rows, x):
+    """A Linear layer's weight gradient ``g[rows]^T x`` (``rows`` empty: the
+    first ``len(x)`` rows of g) on the split-row kernel; widths that are not
+    multiples of 64 (no tile configuration there) take a library GEMM."""
+    if g.shape[1] % 64 == 0 and x.shape[1] % 64 == 0:
+        return _ops.linear_wgrad(g, rows, x)
+    gr = g.index_select(0, rows) if rows.numel() else g[: x.shape[0]]
+    return torch.matmul(gr.t(), x)
 
 
 _PATCH_ROWS = {}
@@ -113,7 +145,7 @@ class AdapterDownFunction(Function):
         du = _ops.gelu_backward_split(g_sp, g_pa, pre, ctx.n_special)
         du2 = du.reshape(-1, n)
         gx = torch.matmul(du, weight) if ctx.needs_input_grad[0] else None
-        gw = _ops.linear_wgrad(du2, _NO_ROWS(du2), x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
+        gw = _wgrad(du2, _NO_ROWS(du2), x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
         gb = _colsum(du2) if ctx.has_bias and ctx.needs_input_grad[2] else None
         return gx, gw, gb, None
 
@@ -139,10 +171,10 @@ class AdapterUpFunction(Function):
         # on the split-row kernel (rows of go picked by a row list), the few
         # special rows as a small GEMM
         if S > 0:
-            G = _ops.linear_wgrad(go2, _patch_rows(B, N, S, go.device), a_pa)
+            G = _wgrad(go2, _patch_rows(B, N, S, go.device), a_pa)
             G = G + torch.matmul(go[:, :S].reshape(-1, n).t(), a_sp.reshape(-1, k))
         else:
-            G = _ops.linear_wgrad(go2, _NO_ROWS(go2), a_pa)
+            G = _wgrad(go2, _NO_ROWS(go2), a_pa)
         gsum = _colsum(go2)
         g_gamma = None
         if ctx.needs_input_grad[4]:
@@ -169,9 +201,12 @@ class SparseConvAdapterFunction(Function):
     and ``AdapterUpFunction``."""
 
     @staticmethod
-    def forward(ctx, x, w_d, b_d, w_c, b_c, w_u, b_u, gamma, nbr, n_special, tpb):
+    def forward(ctx, x, w_d, b_d, w_c, b_c, w_u, b_u, gamma, nbr, n_special, tpb, hm_rows=None, hm_gate=None):
         S = int(n_special)
         pre, sp, pa = _ops.adapter_down(x, w_d, b_d, S)
+        if hm_rows is not None:
+            # heatmap injection on the SparseConv2D input (in place)
+            _ops.heatmap_add_(pa, sp, hm_rows, hm_gate)
         c_in = w_c.shape[1]
         if c_in % 4 != 0:
             raise ValueError(f"C_in ({c_in}) must be divisible by 4 for optimized kernel.")
@@ -179,13 +214,13 @@ class SparseConvAdapterFunction(Function):
         pf, pb = _ops.pack_weight(w_c, True, any(ctx.needs_input_grad))
         processed = _ops.fwd_packed(pa, nbr, w_c, pf, b_c, tpb, mode)
         out = _ops.adapter_up(sp, processed, w_u, b_u, gamma, x)
-        ctx.save_for_backward(x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma)
+        ctx.save_for_backward(x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma, hm_rows, hm_gate)
         ctx.flags = (S, int(tpb), b_d is not None)
         return out
 
     @staticmethod
     def backward(ctx, go):
-        x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma = ctx.saved_tensors
+        x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma, hm_rows, hm_gate = ctx.saved_tensors
         S, tpb, has_bd = ctx.flags
         need = ctx.needs_input_grad
         B, N, n = go.shape
@@ -194,10 +229,10 @@ class SparseConvAdapterFunction(Function):
         go2 = go.reshape(-1, n)
         # up projection: G = go^T cat(sp, processed) without the cat
         if S > 0:
-            G = _ops.linear_wgrad(go2, _patch_rows(B, N, S, go.device), processed)
+            G = _wgrad(go2, _patch_rows(B, N, S, go.device), processed)
             G = G + torch.matmul(go[:, :S].reshape(-1, n).t(), sp.reshape(-1, k))
         else:
-            G = _ops.linear_wgrad(go2, _NO_ROWS(go2), processed)
+            G = _wgrad(go2, _NO_ROWS(go2), processed)
         gsum = _colsum(go2)
         # gamma's gradient and the gamma-scaled W_u, G and sum(go) in one pass
         g_gamma, w_u_g, gw_u, gb_u = _ops.up_proj_grads(w_u, G, b_u, gsum if b_u is not None else None, gamma)
@@ -210,78 +245,227 @@ class SparseConvAdapterFunction(Function):
         # SparseConv2D
         need_bc = b_c is not None and need[4]
         gi_pa, gw_c, gb_c = _ops.bwd_packed(g_pa, pa, nbr, w_c, pb, w_c.shape[1], tpb, need_bc)
+        g_gate = None
+        if hm_rows is not None:
+            # backward of patches + special[hm_rows] * gate: the gather's
+            # scatter-add into the special-token gradient, and the gate's sum
+            hidden = sp.shape[-1]
+            sp_rows = sp.reshape(-1, hidden)
+            if need[12]:
+                g_gate = (gi_pa.float() * sp_rows.index_select(0, hm_rows).float()).sum().view(hm_gate.shape)
+                g_gate = g_gate.to(hm_gate.dtype)
+            g_sp = g_sp.reshape(-1, hidden).index_add(0, hm_rows, gi_pa * hm_gate).view(sp.shape)
         # down projection: GELU backward from the two gradient buffers, then
         # the input gradient with the residual's go in the same GEMM
         du = _ops.gelu_backward_split(g_sp, gi_pa, pre, S)
         du2 = du.reshape(-1, du.shape[-1])
         x2 = x.reshape(-1, x.shape[-1])
         gx = torch.addmm(go2, du2, w_d).view(x.shape) if need[0] else None
-        gw_d = _ops.linear_wgrad(du2, _NO_ROWS(du2), x2) if need[1] else None
+        gw_d = _wgrad(du2, _NO_ROWS(du2), x2) if need[1] else None
         gb_d = _colsum(du2) if has_bd and need[2] else None
         return (gx, gw_d, gb_d, gw_c if need[3] else None, gb_c if need_bc else None, gw_u, gb_u, g_gamma,
-                None, None, None)
+                None, None, None, None, g_gate)
+
+
+def _trunc_normal_init(layer, std):
+    """mmengine's trunc_normal_init(layer, std=std, bias=0) as the reference calls
+    it: weight ~ N(0, std) truncated to [-2, 2], bias 0."""
+    nn.init.trunc_normal_(layer.weight, mean=0.0, std=std, a=-2.0, b=2.0)
+    if getattr(layer, "bias", None) is not None:
+        nn.init.zeros_(layer.bias)
+
+
+def _attention(q, k, v):
+    """Scaled dot-product attention ``softmax(q k^T / sqrt(d)) v`` evaluated in
+    float32 with the operands made contiguous, result in q's dtype (the
+    reference calls F.scaled_dot_product_attention in the module dtype)."""
+    qf, kf, vf = q.float(), k.float(), v.float()
+    s = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * (1.0 / math.sqrt(q.shape[-1]))
+    return torch.matmul(torch.softmax(s, dim=-1), vf.contiguous()).to(q.dtype)
 
 
 class SparseConvAdapter(nn.Module):
-    """The reference adapter with ``conv_type="sparse_conv"``, ``use_attn=0``
-    and no heatmap injection, on fused HIP GEMM epilogues."""
+    """The reference adapter with ``conv_type="sparse_conv"``
+    (vit_sparse_adapter_poguise.py:78-166,288-653): every ``use_attn`` variant
+    and the heatmap injection, with the same parameter names, shapes and
+    initialisation, on fused HIP GEMM epilogues."""
 
-    def __init__(self, embed_dims: int, mlp_ratio: float = 0.25, n_key_tokens: int = 1,
-                 heatmap_grid_size=None):
+    def __init__(self, embed_dims: int, mlp_ratio: float = 0.25, conv_type: str = "sparse_conv",
+                 use_attn=0, n_key_tokens: int = 1, heatmap_grid_size=None, **kwargs):
         super().__init__()
-        if n_key_tokens > 1 and heatmap_grid_size is not None:
-            raise NotImplementedError("SparseConvAdapter: heatmap injection is not implemented")
+        if conv_type != "sparse_conv":
+            raise NotImplementedError(f"SparseConvAdapter: conv_type {conv_type!r} (only 'sparse_conv')")
+        self.conv_type = conv_type
+        self.use_attn = int(use_attn)
+        self.n_key_tokens = n_key_tokens
+        self.heatmap_grid_size = heatmap_grid_size
         self.embed_dims = embed_dims
         hidden = int(embed_dims * mlp_ratio)
         hidden = int(2 ** round(math.log2(hidden)))  # power of two, as the reference rounds
         self.hidden_dims = hidden
         self.down_proj = nn.Linear(embed_dims, hidden)
-        nn.init.trunc_normal_(self.down_proj.weight, std=0.02)
-        nn.init.zeros_(self.down_proj.bias)
+        _trunc_normal_init(self.down_proj, 0.02)
         self.act = nn.GELU()
         self.up_proj = nn.Linear(hidden, embed_dims)
         nn.init.zeros_(self.up_proj.weight)
         nn.init.zeros_(self.up_proj.bias)
         self.gamma = nn.Parameter(torch.ones(1))
+        if self.n_key_tokens > 1 and self.use_attn == 0:
+            self.heatmap_gate = nn.Parameter(torch.zeros(1))
+        if self.use_attn:
+            self.attn_norm = nn.LayerNorm(hidden)
+            self.attn_gamma = nn.Parameter(torch.ones(1))
+            if self.use_attn >= 4:
+                self.num_heads = max(1, hidden // 64)
+                self.qkv = nn.Linear(hidden, hidden * 3, bias=False)
+                _trunc_normal_init(self.qkv, 0.02)
+                self.attn_proj = nn.Linear(hidden, hidden)
+                _trunc_normal_init(self.attn_proj, 0.02)
+                self.attn_mlp = nn.Sequential(nn.LayerNorm(hidden), nn.Linear(hidden, hidden), nn.GELU(),
+                                              nn.Linear(hidden, hidden))
+                _trunc_normal_init(self.attn_mlp[1], 0.02)
+                nn.init.zeros_(self.attn_mlp[3].weight)
+                nn.init.zeros_(self.attn_mlp[3].bias)
+            else:
+                attn_dim = hidden // 2
+                self.num_heads = 4
+                self.down_attn = nn.Linear(hidden, attn_dim)
+                _trunc_normal_init(self.down_attn, 0.02)
+                self.qkv = nn.Linear(attn_dim, attn_dim * 3)
+                self.q_norm = nn.LayerNorm(attn_dim // self.num_heads)
+                self.k_norm = nn.LayerNorm(attn_dim // self.num_heads)
+                _trunc_normal_init(self.qkv, 0.02)
+                self.attn_proj = nn.Linear(attn_dim, hidden)
+                _trunc_normal_init(self.attn_proj, 0.02)
         self.sparse_conv = SparseConv2d(hidden, hidden)
 
     @staticmethod
     def _n_special(x, indices):
         return x.shape[1] - indices.shape[1]
 
+    def _uses_heatmap(self):
+        return self.n_key_tokens > 1 and self.heatmap_grid_size is not None and self.use_attn == 0
+
+    def _heatmap_cells(self, indices, h, w):
+        """Heatmap cell each kept token samples (vit_sparse_adapter_poguise.py:
+        321-339): its spatial position, mapped to the heatmap grid by nearest
+        index when the grids differ."""
+        H_hm, W_hm = self.heatmap_grid_size
+        spatial = indices % (h * w)
+        if H_hm != h or W_hm != w:
+            y = spatial // w
+            xc = spatial % w
+            return ((y * H_hm) // h) * W_hm + (xc * W_hm) // w
+        return spatial
+
+    def _fusable(self, x):
+        return (x.is_cuda and x.dtype in _FUSED_DTYPES and not torch.is_autocast_enabled("cuda")
+                and self.down_proj.weight.dtype == x.dtype)
+
     def forward(self, x, h, w, indices, total_num_patches, neighbor_indices=None, tokens_per_batch=0):
-        """``x [B, N, embed]``; ``indices [B, N_kept]``; ``neighbor_indices``
-        ``[B, N_kept, 9]`` or ``[B * N_kept, 9]``. ``h``, ``w`` and
-        ``total_num_patches`` are accepted for signature compatibility."""
-        if x.dtype not in _FUSED_DTYPES or not x.is_cuda:
-            raise RuntimeError(f"SparseConvAdapter: the fused path takes float16 / bfloat16 GPU "
-                               f"tensors, got {x.dtype} on {x.device}")
-        if self.down_proj.weight.dtype != x.dtype:
-            raise RuntimeError("SparseConvAdapter: convert the module to the input dtype first")
-        S = self._n_special(x, indices)
-        if indices.shape[1] == 0:
+        """``x [B, N, embed]``; ``indices [B, N_kept]`` (flattened ``t*h*w + y*w
+        + x`` positions of the kept tokens); ``neighbor_indices`` ``[B, N_kept,
+        9]`` or ``[B * N_kept, 9]``. ``total_num_patches`` is ``T*h*w``."""
+        if not self._fusable(x) or indices.shape[1] == 0:
             return self.reference_forward(x, h, w, indices, total_num_patches, neighbor_indices)
+        B, N, _ = x.shape
+        S = self._n_special(x, indices)
         nbr = neighbor_indices.reshape(-1, 9)
         if tokens_per_batch is None:
             tokens_per_batch = indices.shape[1] if int(nbr.max()) < indices.shape[1] else 0
         if nbr.dtype != torch.int32:
             nbr = nbr.to(torch.int32)
         conv = self.sparse_conv
-        return SparseConvAdapterFunction.apply(x, self.down_proj.weight, self.down_proj.bias, conv.weight,
-                                               conv.bias, self.up_proj.weight, self.up_proj.bias, self.gamma,
-                                               nbr, S, tokens_per_batch)
+        if not self.use_attn:
+            hm_rows = hm_gate = None
+            if self._uses_heatmap():
+                H_hm, W_hm = self.heatmap_grid_size
+                if S < 1 + H_hm * W_hm:
+                    raise ValueError(f"SparseConvAdapter: {S} special tokens hold no {H_hm}x{W_hm} heatmap after CLS")
+                cells = self._heatmap_cells(indices, h, w)
+                base = torch.arange(B, device=x.device).view(B, 1) * S + 1
+                hm_rows = (base + cells).reshape(-1).to(torch.int32)
+                hm_gate = self.heatmap_gate
+            return SparseConvAdapterFunction.apply(x, self.down_proj.weight, self.down_proj.bias, conv.weight,
+                                                   conv.bias, self.up_proj.weight, self.up_proj.bias, self.gamma,
+                                                   nbr, S, tokens_per_batch, hm_rows, hm_gate)
+        sp, pa = AdapterDownFunction.apply(x, self.down_proj.weight, self.down_proj.bias, S)
+        processed = conv(pa, nbr, tokens_per_batch=tokens_per_batch)
+        x_comb = torch.cat([sp, processed.view(B, N - S, -1)], dim=1)
+        x_comb = self._attention_branch(x_comb, S, indices, h, w, total_num_patches, fused=True)
+        empty = x_comb.new_empty(B, 0, x_comb.shape[-1])
+        return AdapterUpFunction.apply(empty, x_comb.reshape(B * N, -1), self.up_proj.weight, self.up_proj.bias,
+                                       self.gamma, x)
+
+    def _attention_branch(self, x_comb, S, indices, h, w, total_num_patches, fused):
+        """The ``use_attn`` branch on ``x_combined`` (vit_sparse_adapter_poguise.py:
+        511-650). With ``fused`` the ``shortcut + attn_proj(.) * attn_gamma`` of
+        variants 1-3 runs on the up GEMM's epilogue."""
+        shortcut = x_comb
+        B, N, C = x_comb.shape
+        if self.use_attn >= 4:
+            # temporal attention over frame-pooled tokens (:513-596)
+            special = x_comb[:, :S]
+            patches = x_comb[:, S:]
+            hw = h * w
+            frame = indices // hw
+            n_frames = total_num_patches // hw
+            idx = frame.unsqueeze(-1).expand(-1, -1, C)
+            feats = patches.new_zeros(B, n_frames, C).scatter_add(1, idx, patches)
+            counts = patches.new_zeros(B, n_frames, 1).scatter_add(
+                1, frame.unsqueeze(-1), torch.ones_like(frame, dtype=patches.dtype).unsqueeze(-1))
+            feats = feats / (counts + 1e-6)
+            attn_in = torch.cat([special, feats], dim=1)
+            xa = self.attn_norm(attn_in)
+            qkv = self.qkv(xa).reshape(B, -1, 3, self.num_heads, C // self.num_heads).permute(2, 0, 3, 1, 4)
+            xa = _attention(qkv[0], qkv[1], qkv[2]).transpose(1, 2).reshape(B, -1, C)
+            xa = self.attn_proj(xa)
+            coarse = xa + self.attn_mlp(xa)
+            sp_out = coarse[:, :S]
+            fr_out = coarse[:, S:]
+            pa_out = torch.gather(fr_out, 1, idx)
+            return shortcut + torch.cat([sp_out, pa_out], dim=1)
+        xa = self.down_attn(self.attn_norm(x_comb))
+        A = xa.shape[-1]
+        hd = A // self.num_heads
+        q, k, v = self.qkv(xa).reshape(B, N, 3, self.num_heads, hd).permute(2, 0, 3, 1, 4)
+        q = self.q_norm(q)
+        k = self.k_norm(k)
+        nk = self.n_key_tokens
+        if self.use_attn == 2:  # visual tokens attend to the key tokens (:608-620)
+            vis = _attention(q[:, :, nk:], k[:, :, :nk], v[:, :, :nk])
+            xa = torch.cat([torch.zeros_like(q[:, :, :nk]), vis], dim=2)
+        elif self.use_attn == 3:  # key tokens attend to the visual tokens (:621-634)
+            key = _attention(q[:, :, :nk], k[:, :, nk:], v[:, :, nk:])
+            xa = torch.cat([key, torch.zeros_like(q[:, :, nk:])], dim=2)
+        else:
+            xa = _attention(q, k, v)
+        xa = xa.transpose(1, 2).reshape(B, N, A)
+        if fused:
+            empty = xa.new_empty(B, 0, A)
+            return AdapterUpFunction.apply(empty, xa.reshape(B * N, A), self.attn_proj.weight, self.attn_proj.bias,
+                                           self.attn_gamma, shortcut)
+        return shortcut + self.attn_proj(xa) * self.attn_gamma
 
     def reference_forward(self, x, h, w, indices, total_num_patches, neighbor_indices=None):
         """The unfused chain in the reference's op order
-        (vit_sparse_adapter_poguise.py:305-362,652-653), including its
-        ``.max()`` heuristic inside SparseConv2d."""
+        (vit_sparse_adapter_poguise.py:288-362,511-653), including its
+        ``.max()`` heuristic inside SparseConv2d and its autocast casts."""
         inputs = x
         x_proj = self.act(self.down_proj(x))
         S = self._n_special(x, indices)
         special = x_proj[:, :S, :]
         patches = x_proj[:, S:, :]
+        if self._uses_heatmap():
+            heat = special[:, 1:, :]
+            cells = self._heatmap_cells(indices, h, w)
+            sampled = torch.gather(heat, 1, cells.unsqueeze(-1).expand(-1, -1, self.hidden_dims))
+            patches = patches + sampled * self.heatmap_gate
         if patches.shape[1] == 0:
             # the reference applies the activation a second time here (:356-358)
             return self.up_proj(self.act(x_proj)) * self.gamma + inputs
         processed = self.sparse_conv(patches, neighbor_indices)
-        return self.up_proj(torch.cat([special, processed], dim=1)) * self.gamma + inputs
+        x_comb = torch.cat([special, processed], dim=1)
+        if self.use_attn:
+            x_comb = self._attention_branch(x_comb, S, indices, h, w, total_num_patches, fused=False)
+        return self.up_proj(x_comb) * self.gamma + inputs

@@ -556,6 +556,65 @@ extern "C" int svtad_gelu_backward_split(const void* grad_special, const void* g
 // is outside [0, n_special_rows) are left unchanged. The patch rows gather
 // special rows that other workgroups of the down GEMM produce, so the add
 // is a launch of its own after that GEMM.
+namespace svtad {
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_heatmap_add(T* __restrict__ patch, const T* __restrict__ special,
+                                                     const int32_t* __restrict__ src, const T* __restrict__ gate,
+                                                     int64_t rows, int64_t n_special_rows, int cols) {
+    // two roundings, as the unfused chain: no fused multiply-add
+#pragma clang fp contract(off)
+    const int cpr = cols / 8;
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= rows * cpr) return;
+    const int64_t i = e / cpr;
+    const int c = (int)(e - i * cpr) * 8;
+    const int32_t r = src[i];
+    if (r < 0 || r >= n_special_rows) return;
+    const float g = (float)gate[0];
+    u32x4* const pp = (u32x4*)(patch + i * cols + c);
+    const u32x4 pv = *pp;
+    const u32x4 hv = *(const u32x4*)(special + (int64_t)r * cols + c);
+    u32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        unsigned w = 0;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const T pt = __builtin_bit_cast(T, (u16)(pv[q] >> (16 * h)));
+            const T ht = __builtin_bit_cast(T, (u16)(hv[q] >> (16 * h)));
+            const T prod = (T)((float)ht * g);
+            w |= (unsigned)__builtin_bit_cast(u16, (T)((float)pt + (float)prod)) << (16 * h);
+        }
+        o[q] = w;
+    }
+    *pp = o;
+}
+
+}  // namespace svtad
+
+extern "C" int svtad_heatmap_add(void* patch, const void* special, const int32_t* src_rows, const void* gate,
+                                 int64_t rows, int64_t n_special_rows, int cols, int dtype, void* stream) {
+    if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "heatmap_add: needs f16/bf16");
+    if (rows < 0 || n_special_rows < 0 || cols <= 0 || cols % 8 != 0)
+        return set_error(SVTAD_ERR_INVALID, "heatmap_add: needs rows >= 0 and cols a positive multiple of 8");
+    if (rows == 0) return SVTAD_OK;
+    if (!patch || !src_rows || !gate || (n_special_rows > 0 && !special))
+        return set_error(SVTAD_ERR_INVALID, "heatmap_add: null pointer");
+    if (!al16(patch) || (special && !al16(special)))
+        return set_error(SVTAD_ERR_INVALID, "heatmap_add: patch and special need 16-byte alignment");
+    const int64_t threads = rows * (cols / 8);
+    const dim3 grid((unsigned)cdiv(threads, 256));
+    if (dtype == SVTAD_F16)
+        hipLaunchKernelGGL(k_heatmap_add<f16>, grid, dim3(256), 0, (hipStream_t)stream, (f16*)patch,
+                           (const f16*)special, src_rows, (const f16*)gate, rows, n_special_rows, cols);
+    else
+        hipLaunchKernelGGL(k_heatmap_add<bf16>, grid, dim3(256), 0, (hipStream_t)stream, (bf16*)patch,
+                           (const bf16*)special, src_rows, (const bf16*)gate, rows, n_special_rows, cols);
+    return launch_status();
+}
+
 extern "C" size_t svtad_gamma_grad_workspace_bytes(void) { return (size_t)kGammaParts * sizeof(float); }
 
 extern "C" int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,

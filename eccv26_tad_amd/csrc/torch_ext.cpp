@@ -666,6 +666,29 @@ at::Tensor op_adapter_up(const at::Tensor& sp_in, const at::Tensor& pa_in, const
     return out;
 }
 
+// heatmap_add_(patch [R, C], special [*, C], src_rows int32 [R], gate [1]) -> patch,
+// in place: patch[i] += special[src_rows[i]] * gate (rounded as the unfused chain)
+at::Tensor op_heatmap_add_(at::Tensor patch, const at::Tensor& special_in, const at::Tensor& src_in,
+                           const at::Tensor& gate_in) {
+    adapter_common(patch, patch, "patch");
+    TORCH_CHECK(patch.dim() == 2 && patch.is_contiguous(), "patch must be a contiguous [rows, cols] tensor");
+    check_gpu(special_in, "special");
+    check_gpu(src_in, "src_rows");
+    check_gpu(gate_in, "gate");
+    TORCH_CHECK(special_in.scalar_type() == patch.scalar_type() && gate_in.scalar_type() == patch.scalar_type(),
+                "special, gate and patch must share the dtype");
+    const int64_t rows = patch.size(0), cols = patch.size(1);
+    TORCH_CHECK(special_in.size(-1) == cols, "special must have ", cols, " columns");
+    TORCH_CHECK(src_in.scalar_type() == at::kInt && src_in.numel() == rows, "src_rows must be int32 [rows]");
+    TORCH_CHECK(gate_in.numel() == 1, "gate must be one element");
+    at::Tensor sp = special_in.contiguous(), src = src_in.contiguous(), gate = gate_in.contiguous();
+    c10::DeviceGuard g(patch.device());
+    check_status(svtad_heatmap_add(patch.data_ptr(), sp.numel() ? sp.data_ptr() : nullptr, src.data_ptr<int32_t>(),
+                                   gate.data_ptr(), rows, n_rows(sp), (int)cols, dtype_code(patch), stream_of(patch)),
+                 "heatmap_add_");
+    return patch;
+}
+
 // linear_wgrad(g [*, c_g], rows int32 [n] or empty, x [n, c_x]) -> out [c_g, c_x]
 // (out = g[rows]^T x, or g^T x with the first n rows of g when rows is empty)
 at::Tensor op_linear_wgrad(const at::Tensor& g_in, const at::Tensor& rows_in, const at::Tensor& x_in) {
@@ -878,6 +901,8 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.def("adapter_up", &op_adapter_up, "Adapter up_proj on cat(special, patch) * gamma + residual",
           py::arg("a_special"), py::arg("a_patch"), py::arg("weight"), py::arg("bias"), py::arg("gamma"),
           py::arg("residual"));
+    m.def("heatmap_add_", &op_heatmap_add_, "In place: patch[i] += special[src_rows[i]] * gate (adapter heatmap injection)",
+          py::arg("patch"), py::arg("special"), py::arg("src_rows"), py::arg("gate"));
     m.def("linear_wgrad", &op_linear_wgrad, "Linear-layer weight gradient g[rows]^T x (split rows, ordered sum)",
           py::arg("g"), py::arg("rows"), py::arg("x"));
     m.def("column_sums", &op_column_sums, "Column sums of a [rows, cols] matrix (ordered, fp32 accumulation)",

@@ -340,6 +340,22 @@ int svtad_gelu_backward_split(const void* grad_special, const void* grad_patch, 
                               int dtype, void* stream);
 
 /*
+ * Heatmap injection of the adapter, the forward of
+ *   patch_tokens_proj + gather(heatmap_tokens, cell) * heatmap_gate
+ * (vit_sparse_adapter_poguise.py:311-355), in place on the SparseConv2D input:
+ *   patch[i, c] = T(patch[i, c] + T(special[src_rows[i], c] * gate[0]))
+ * patch [rows, cols] (the patch tokens after down_proj + GELU), special
+ * [n_special_rows, cols] (the special tokens of every sample, flattened),
+ * src_rows int32 [rows]: the special row of the heatmap cell each patch token
+ * samples (b * S + 1 + cell); rows whose entry is outside [0, n_special_rows)
+ * are left unchanged. gate: one element (device). The products and sums are
+ * rounded to `dtype` as in the unfused chain. f16 / bf16, cols % 8 == 0,
+ * patch and special 16-byte aligned. One launch on `stream`.
+ */
+int svtad_heatmap_add(void* patch, const void* special, const int32_t* src_rows, const void* gate,
+                      int64_t rows, int64_t n_special_rows, int cols, int dtype, void* stream);
+
+/*
  * Gradient of the adapter's gamma, replacing the autograd of `* self.gamma`
  * (vit_sparse_adapter_poguise.py:652-653): out[0] = sum_i w[i] g[i] +
  * sum_j b[j] gs[j], with w the up projection's weight, g = go^T c its

@@ -181,6 +181,50 @@ def test_adapter_backward_arguments_checked_on_host(lib):
     assert st == -1 and b"gamma" in lib.svtad_last_error()
 
 
+def test_heatmap_add_arguments_checked_on_host(lib):
+    buf = ctypes.create_string_buffer(256)
+    st = lib.svtad_heatmap_add(buf, buf, buf, buf, I64(4), I64(4), 64, 0, None)
+    assert st == -3 and b"f16/bf16" in lib.svtad_last_error()
+    st = lib.svtad_heatmap_add(buf, buf, buf, buf, I64(4), I64(4), 12, 1, None)
+    assert st == -1
+    st = lib.svtad_heatmap_add(buf, buf, None, buf, I64(4), I64(4), 64, 2, None)
+    assert st == -1 and b"null pointer" in lib.svtad_last_error()
+    assert lib.svtad_heatmap_add(None, None, None, None, I64(0), I64(4), 64, 1, None) == 0
+
+
+def test_adapter_variants_have_the_reference_parameters():
+    """Parameter names and shapes of every adapter variant match the reference
+    module's (vit_sparse_adapter_poguise.py:93-166), so its state dicts load."""
+    from eccv26_tad_amd import SparseConvAdapter
+
+    def shapes(m):
+        return {k: tuple(v.shape) for k, v in m.state_dict().items()}
+
+    base = {"down_proj.weight": (256, 768), "down_proj.bias": (256,), "up_proj.weight": (768, 256),
+            "up_proj.bias": (768,), "gamma": (1,), "sparse_conv.weight": (9, 256, 256), "sparse_conv.bias": (256,)}
+    assert shapes(SparseConvAdapter(768, 0.25)) == base
+    assert shapes(SparseConvAdapter(768, 0.25, n_key_tokens=197, heatmap_grid_size=(14, 14))) == {
+        **base, "heatmap_gate": (1,)}
+    attn = {"attn_norm.weight": (256,), "attn_norm.bias": (256,), "attn_gamma": (1,),
+            "down_attn.weight": (128, 256), "down_attn.bias": (128,), "qkv.weight": (384, 128), "qkv.bias": (384,),
+            "q_norm.weight": (32,), "q_norm.bias": (32,), "k_norm.weight": (32,), "k_norm.bias": (32,),
+            "attn_proj.weight": (256, 128), "attn_proj.bias": (256,)}
+    for v in (1, 2, 3):
+        m = SparseConvAdapter(768, 0.25, use_attn=v, n_key_tokens=197, heatmap_grid_size=(14, 14))
+        assert shapes(m) == {**base, **attn} and m.num_heads == 4
+    m = SparseConvAdapter(768, 0.25, use_attn=4)
+    t = {"attn_norm.weight": (256,), "attn_norm.bias": (256,), "attn_gamma": (1,), "qkv.weight": (768, 256),
+         "attn_proj.weight": (256, 256), "attn_proj.bias": (256,), "attn_mlp.0.weight": (256,),
+         "attn_mlp.0.bias": (256,), "attn_mlp.1.weight": (256, 256), "attn_mlp.1.bias": (256,),
+         "attn_mlp.3.weight": (256, 256), "attn_mlp.3.bias": (256,)}
+    assert shapes(m) == {**base, **t} and m.num_heads == 4
+    # the reference's zero-initialised layers and unit gains
+    assert float(m.attn_mlp[3].weight.detach().abs().max()) == 0 and float(m.up_proj.weight.detach().abs().max()) == 0
+    assert float(m.gamma.detach()) == 1 and float(m.attn_gamma.detach()) == 1
+    # hidden width rounds to a power of two (768 * 0.25 -> 256, 384 * 0.25 -> 128, 1024 / 4 -> 256)
+    assert SparseConvAdapter(384, 0.25).hidden_dims == 128 and SparseConvAdapter(1024, 0.25).hidden_dims == 256
+
+
 def test_dw_bwd_arguments_checked_on_host(lib):
     lib.svtad_dw_bwd_workspace_bytes.restype = ctypes.c_size_t
     buf = ctypes.create_string_buffer(256)
@@ -213,7 +257,7 @@ def test_extension_module_api():
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
                  "validate_neighbor_table", "prune_tokens", "bwd_packed", "adapter_down",
                  "adapter_up", "linear_wgrad", "column_sums", "gelu_backward_split", "gamma_grad", "up_proj_grads",
-                 "dw_bwd"):
+                 "dw_bwd", "heatmap_add_"):
         assert hasattr(ops, name)
     import torch
 
