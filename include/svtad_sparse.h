@@ -132,6 +132,23 @@ int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* we
                         int64_t tokens_per_batch, int dtype, void* stream);
 
 /*
+ * Allocation-free forward. No counterpart in the reference: for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Computes exactly what svtad_fwd computes,
+ * with its workspace (the packed weight) in a static device array of
+ * svtad_fwd_noalloc_max_workspace_bytes() (8 MiB) that every GPU the library
+ * runs on holds until the process ends; shapes whose svtad_fwd_workspace_bytes()
+ * exceed it are rejected with SVTAD_ERR_UNSUPPORTED (square weights up to
+ * C = 512 fit). Calls no hipMalloc/hipFree. All calls on one GPU share its
+ * array: calls that overlap on one GPU (different streams, or host threads
+ * without ordering) race.
+ */
+size_t svtad_fwd_noalloc_max_workspace_bytes(void);
+int svtad_fwd_noalloc(const void* x, const int32_t* nbr, const void* weight, const void* bias,
+                      int bias_mode, void* out, int64_t n, int c_in, int c_out, int64_t tokens_per_batch,
+                      int dtype, void* stream);
+
+/*
  * The whole backward in one call: grad_in as svtad_bwd_in_packed computes it
  * and grad_w / grad_bias as svtad_bwd_w computes them (same kernels, same
  * results), with the pass for table entries without a symmetric partner run
