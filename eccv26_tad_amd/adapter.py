@@ -79,6 +79,7 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import opentad_sparse_ops as _ops
+from .neighbor import global_neighbor_table
 from .sparse_conv_layer import (BIAS_AFTER, BIAS_FP32, BIAS_NONE, IMPLICIT_GEMM_MIN_CIN, SparseConv2d)
 
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
@@ -370,11 +371,13 @@ class SparseConvAdapter(nn.Module):
             return self.reference_forward(x, h, w, indices, total_num_patches, neighbor_indices)
         B, N, _ = x.shape
         S = self._n_special(x, indices)
-        nbr = neighbor_indices.reshape(-1, 9)
         if tokens_per_batch is None:
-            tokens_per_batch = indices.shape[1] if int(nbr.max()) < indices.shape[1] else 0
-        if nbr.dtype != torch.int32:
-            nbr = nbr.to(torch.int32)
+            # the reference's max() < N rule, on the device (no host sync)
+            nbr, tokens_per_batch = global_neighbor_table(neighbor_indices, indices.shape[1]), 0
+        else:
+            nbr = neighbor_indices.reshape(-1, 9)
+            if nbr.dtype != torch.int32:
+                nbr = nbr.to(torch.int32)
         conv = self.sparse_conv
         if not self.use_attn:
             hm_rows = hm_gate = None

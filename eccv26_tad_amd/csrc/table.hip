@@ -1,6 +1,8 @@
 // Neighbor-index table kernels: build from a keep mask, remap after a prune,
 // transpose, validate. Integer work; every output is bit-exact with the
 // reference procedures (see the citations at each entry point).
+#include <algorithm>
+
 #include "sv_common.h"
 #include "sv_internal.h"
 
@@ -240,6 +242,131 @@ __global__ __launch_bounds__(256) void k_validate(const int32_t* __restrict__ t,
     }
 }
 
+// ---------------------------------------------------------------------------
+// one-launch builds: the table from a mask with a known row count (no host
+// synchronisation), the full-grid table in closed form, and the
+// local -> global conversion behind the tokens_per_batch heuristic
+// ---------------------------------------------------------------------------
+
+// Nonzero bytes of a 32-bit word: bit 7 of each byte is set iff the byte is
+// nonzero ((b & 0x7f) + 0x7f carries into bit 7 unless b & 0x7f == 0; OR b
+// adds b's own bit 7).
+__device__ __forceinline__ int nonzero_bytes(uint32_t v) {
+    return __popc((((v & 0x7f7f7f7fu) + 0x7f7f7f7fu) | v) & 0x80808080u);
+}
+
+// Workgroup g owns frames [g * fpw, (g + 1) * fpw). It counts the kept cells
+// of every frame before its range itself (16-byte reads of the mask; mask is
+// 16-byte aligned), which gives the rank of its first row without a scan
+// launch; then per frame it ranks the cells in LDS (rank of each cell,
+// cell of each rank) and writes the frame's rows entry by entry, so that
+// consecutive threads store consecutive table entries. Rows at or past n_rows
+// are not written; the workgroup that owns the last frame fills rows
+// [total, n_rows) with -1 when the mask keeps fewer than n_rows cells.
+template <typename I>
+__global__ __launch_bounds__(256) void k_table_build(const uint8_t* __restrict__ mask, int64_t n_frames, int h,
+                                                     int w, int fpw, int64_t n_rows, I* __restrict__ table) {
+    extern __shared__ int16_t lds16[];
+    int16_t* const rank_s = lds16;              // cells entries: rank of the cell in its frame, -1 if dropped
+    int16_t* const cell_of = lds16 + h * w;     // cells entries: cell of each rank
+    __shared__ int32_t wsum[4];
+    __shared__ int32_t base_s;
+    const int cells = h * w;
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int64_t f0 = (int64_t)blockIdx.x * fpw;
+    const int64_t f1 = min<int64_t>(n_frames, f0 + fpw);
+
+    // kept cells before the range
+    const int64_t pre_bytes = f0 * cells;
+    int cnt = 0;  // < 2^31: the host limits the mask to 4 MiB
+    for (int64_t c = tid; c < pre_bytes / 16; c += 256) {
+        const uint4 v = *(const uint4*)(mask + c * 16);
+        cnt += nonzero_bytes(v.x) + nonzero_bytes(v.y) + nonzero_bytes(v.z) + nonzero_bytes(v.w);
+    }
+    for (int64_t b = (pre_bytes / 16) * 16 + tid; b < pre_bytes; b += 256) cnt += mask[b] != 0;
+    for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+    if (tid == 0) base_s = 0;
+    __syncthreads();
+    if (lane == 0) atomicAdd(&base_s, cnt);
+    __syncthreads();
+    int64_t base = base_s;
+
+    for (int64_t f = f0; f < f1; ++f) {
+        const uint8_t* m = mask + f * cells;
+        int kept_total = 0;
+        for (int b0 = 0; b0 < cells; b0 += 256) {
+            const int p = b0 + tid;
+            const bool kept = p < cells && m[p] != 0;
+            const uint64_t bal = __ballot(kept);
+            const int before = __popcll(bal & ((1ull << lane) - 1ull));
+            if (lane == 0) wsum[wid] = __popcll(bal);
+            __syncthreads();
+            int pre = kept_total;
+            for (int q = 0; q < wid; ++q) pre += wsum[q];
+            if (p < cells) {
+                rank_s[p] = (int16_t)(kept ? pre + before : -1);
+                if (kept) cell_of[pre + before] = (int16_t)p;
+            }
+            kept_total += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+            __syncthreads();
+        }
+        for (int e = tid; e < kept_total * 9; e += 256) {
+            const int r = e / 9, k = e - r * 9;
+            const int64_t row = base + r;
+            if (row >= n_rows) break;  // rows grow with e
+            const int p = cell_of[r];
+            const int y = p / w, x = p - y * w;
+            const int yy = y + k / 3 - 1, xx = x + k % 3 - 1;
+            I v = -1;
+            if (yy >= 0 && yy < h && xx >= 0 && xx < w) {
+                const int rq = rank_s[yy * w + xx];
+                if (rq >= 0) v = (I)(base + rq);
+            }
+            table[row * 9 + k] = v;
+        }
+        base += kept_total;
+        __syncthreads();  // the next frame overwrites the rank arrays
+    }
+    if (f1 >= n_frames)
+        for (int64_t e = base * 9 + tid; e < n_rows * 9; e += 256) table[e] = (I)-1;
+}
+
+// Full-grid table (every cell kept) in closed form: row i = f * h * w + y * w
+// + x, entry k -> i + (dy * w + dx) when (y + dy, x + dx) is in the frame,
+// else -1 (get_initial_neighbor_indices, vit_sparse_adapter_poguise.py:
+// 1623-1670). One thread per entry, consecutive entries per thread block.
+template <typename I>
+__global__ __launch_bounds__(256) void k_table_grid(int64_t n_entries, int h, int w, I* __restrict__ table) {
+    const int cells = h * w;
+    for (int64_t e = blockIdx.x * (int64_t)256 + threadIdx.x; e < n_entries; e += (int64_t)gridDim.x * 256) {
+        const int64_t row = e / 9;
+        const int k = (int)(e - row * 9);
+        const int p = (int)(row % cells);
+        const int y = p / w, x = p - y * w;
+        const int dy = k / 3 - 1, dx = k % 3 - 1;
+        const int yy = y + dy, xx = x + dx;
+        table[e] = (yy >= 0 && yy < h && xx >= 0 && xx < w) ? (I)(row + dy * w + dx) : (I)-1;
+    }
+}
+
+// The reference wrapper's heuristic (sparse_conv_layer.py:170-177) without the
+// host sync: with *vmax (the table's max, on the device) < tpb the entries are
+// local to their batch and get the row's batch offset (i / tpb) * tpb, else
+// they are global already. Negative entries and values past the int32 range
+// become -1 (missing). Output int32.
+template <typename I>
+__global__ __launch_bounds__(256) void k_table_to_global(const I* __restrict__ in, int64_t n_entries,
+                                                         int64_t tpb, const I* __restrict__ vmax,
+                                                         int32_t* __restrict__ out) {
+    const bool local = (int64_t)*vmax < tpb;
+    for (int64_t e = blockIdx.x * (int64_t)256 + threadIdx.x; e < n_entries; e += (int64_t)gridDim.x * 256) {
+        const int64_t v = (int64_t)in[e];
+        int64_t o = v;
+        if (v >= 0 && local) o += ((e / 9) / tpb) * tpb;
+        out[e] = (v < 0 || o > (int64_t)INT32_MAX) ? -1 : (int32_t)o;
+    }
+}
+
 static inline unsigned grid_for(int64_t work, int threads) {
     int64_t g = cdiv(work, threads);
     if (g < 1) g = 1;
@@ -376,5 +503,70 @@ extern "C" int svtad_validate_table(const int32_t* table, int64_t n_entries, int
     if (n_entries > 0)
         hipLaunchKernelGGL(k_validate, dim3(grid_for(n_entries, 256 * 8)), dim3(256), 0, s, table,
                            n_entries, bound, stats);
+    return launch_status();
+}
+
+// the largest mask the one-launch build reads as prefix counts (each
+// workgroup re-reads the mask before its frames); larger masks take the
+// scan + fill launches
+constexpr int64_t kBuildOneLaunchMaskBytes = (int64_t)4 << 20;
+
+extern "C" int svtad_table_build(const uint8_t* mask, int64_t n_frames, int h, int w, int64_t n_rows, void* table,
+                                 int index_bits, void* stream) {
+    if (n_frames < 0 || h <= 0 || w <= 0 || n_rows < 0 || (index_bits != 32 && index_bits != 64))
+        return set_error(SVTAD_ERR_INVALID, "table_build: bad arguments");
+    if ((int64_t)h * w > kMaxFrameCells)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "table_build: h*w exceeds 16384 cells");
+    if (n_frames * (int64_t)h * w >= (int64_t)INT32_MAX || n_rows >= (int64_t)INT32_MAX)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "table_build: more than 2^31-1 cells or rows");
+    if (n_frames * (int64_t)h * w > kBuildOneLaunchMaskBytes)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "table_build: mask larger than 4 MiB (use svtad_table_scan / svtad_table_fill)");
+    if (n_rows == 0) return SVTAD_OK;
+    if (!table || (n_frames > 0 && !mask)) return set_error(SVTAD_ERR_INVALID, "table_build: null pointer");
+    if (((uintptr_t)mask & 15) != 0) return set_error(SVTAD_ERR_INVALID, "table_build: mask must be 16-byte aligned");
+    const int64_t groups_max = 256;
+    const int fpw = (int)std::max<int64_t>(1, cdiv(n_frames, groups_max));
+    const int64_t groups = std::max<int64_t>(1, cdiv(n_frames, fpw));
+    const size_t lds = 2 * sizeof(int16_t) * (size_t)h * w;
+    hipStream_t s = (hipStream_t)stream;
+    if (index_bits == 32)
+        hipLaunchKernelGGL(k_table_build<int32_t>, dim3((unsigned)groups), dim3(256), lds, s, mask, n_frames, h, w,
+                           fpw, n_rows, (int32_t*)table);
+    else
+        hipLaunchKernelGGL(k_table_build<int64_t>, dim3((unsigned)groups), dim3(256), lds, s, mask, n_frames, h, w,
+                           fpw, n_rows, (int64_t*)table);
+    return launch_status();
+}
+
+extern "C" int svtad_table_grid(int64_t n_frames, int h, int w, void* table, int index_bits, void* stream) {
+    if (n_frames < 0 || h <= 0 || w <= 0 || (index_bits != 32 && index_bits != 64))
+        return set_error(SVTAD_ERR_INVALID, "table_grid: bad arguments");
+    const int64_t rows = n_frames * (int64_t)h * w;
+    if (rows >= (int64_t)INT32_MAX) return set_error(SVTAD_ERR_UNSUPPORTED, "table_grid: more than 2^31-1 rows");
+    if (rows == 0) return SVTAD_OK;
+    if (!table) return set_error(SVTAD_ERR_INVALID, "table_grid: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(grid_for(rows * 9, 256));
+    if (index_bits == 32)
+        hipLaunchKernelGGL(k_table_grid<int32_t>, grid, dim3(256), 0, s, rows * 9, h, w, (int32_t*)table);
+    else
+        hipLaunchKernelGGL(k_table_grid<int64_t>, grid, dim3(256), 0, s, rows * 9, h, w, (int64_t*)table);
+    return launch_status();
+}
+
+extern "C" int svtad_table_to_global(const void* table, int index_bits, int64_t n_rows, int64_t tokens_per_batch,
+                                     const void* table_max, int32_t* out, void* stream) {
+    if (n_rows < 0 || tokens_per_batch < 0 || (index_bits != 32 && index_bits != 64))
+        return set_error(SVTAD_ERR_INVALID, "table_to_global: bad arguments");
+    if (n_rows == 0) return SVTAD_OK;
+    if (!table || !table_max || !out) return set_error(SVTAD_ERR_INVALID, "table_to_global: null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(grid_for(n_rows * 9, 256));
+    if (index_bits == 32)
+        hipLaunchKernelGGL(k_table_to_global<int32_t>, grid, dim3(256), 0, s, (const int32_t*)table, n_rows * 9,
+                           tokens_per_batch, (const int32_t*)table_max, out);
+    else
+        hipLaunchKernelGGL(k_table_to_global<int64_t>, grid, dim3(256), 0, s, (const int64_t*)table, n_rows * 9,
+                           tokens_per_batch, (const int64_t*)table_max, out);
     return launch_status();
 }

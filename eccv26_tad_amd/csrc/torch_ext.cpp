@@ -493,6 +493,74 @@ at::Tensor op_build_neighbor_table(const at::Tensor& mask_in) {
     return table;
 }
 
+// build_neighbor_table_n(mask [..., H, W], n_rows, int64_out) -> [n_rows, 9]: no host sync
+// (the caller knows the kept count); masks past 4 MiB take scan + fill without a sync
+at::Tensor op_build_neighbor_table_n(const at::Tensor& mask_in, int64_t n_rows, bool int64_out) {
+    check_gpu(mask_in, "mask");
+    TORCH_CHECK(mask_in.dim() >= 2, "mask must be [..., H, W]");
+    TORCH_CHECK(mask_in.scalar_type() == at::kBool || mask_in.scalar_type() == at::kByte,
+                "mask must be bool or uint8");
+    TORCH_CHECK(n_rows >= 0, "n_rows must be >= 0");
+    at::Tensor mask = mask_in.contiguous();
+    if (mask.scalar_type() == at::kBool) mask = mask.view(at::kByte);
+    if (((uintptr_t)mask.data_ptr() & 15) != 0) mask = mask.clone();
+    const int64_t h = mask.size(-2), w = mask.size(-1);
+    const int64_t frames = h * w == 0 ? 0 : mask.numel() / (h * w);
+    c10::DeviceGuard g(mask.device());
+    const auto idx_t = int64_out ? at::kLong : at::kInt;
+    void* s = stream_of(mask);
+    if (frames * h * w <= ((int64_t)4 << 20)) {
+        at::Tensor table = at::empty({n_rows, 9}, mask.options().dtype(idx_t));
+        check_status(svtad_table_build(mask.data_ptr<uint8_t>(), frames, (int)h, (int)w, n_rows, table.data_ptr(),
+                                       int64_out ? 64 : 32, s),
+                     "build_neighbor_table");
+        return table;
+    }
+    // large masks: the scan + fill launches, into a buffer with a row for
+    // every cell (the fill writes every kept cell, whatever n_rows says),
+    // cut to n_rows
+    at::Tensor offs = at::empty({frames + 1}, mask.options().dtype(at::kInt));
+    check_status(svtad_table_scan(mask.data_ptr<uint8_t>(), frames, (int)h, (int)w, offs.data_ptr<int32_t>(), s),
+                 "build_neighbor_table");
+    at::Tensor t32 = at::full({std::max(n_rows, frames * h * w), 9}, -1, mask.options().dtype(at::kInt));
+    check_status(svtad_table_fill(mask.data_ptr<uint8_t>(), offs.data_ptr<int32_t>(), frames, (int)h, (int)w,
+                                  t32.data_ptr<int32_t>(), s),
+                 "build_neighbor_table");
+    t32 = t32.narrow(0, 0, n_rows).contiguous();
+    return int64_out ? t32.to(at::kLong) : t32;
+}
+
+// grid_neighbor_table(frames, h, w, int64_out, like) -> [frames * h * w, 9] on like's device
+at::Tensor op_grid_neighbor_table(int64_t frames, int64_t h, int64_t w, bool int64_out, const at::Tensor& like) {
+    check_gpu(like, "like");
+    TORCH_CHECK(frames >= 0 && h > 0 && w > 0, "bad grid");
+    c10::DeviceGuard g(like.device());
+    at::Tensor table = at::empty({frames * h * w, 9}, like.options().dtype(int64_out ? at::kLong : at::kInt));
+    check_status(svtad_table_grid(frames, (int)h, (int)w, table.data_ptr(), int64_out ? 64 : 32, stream_of(like)),
+                 "grid_neighbor_table");
+    return table;
+}
+
+// table_to_global(table [..., 9] int32/int64, tokens_per_batch) -> int32 [rows, 9]: the
+// max() < N heuristic on the device (no host sync)
+at::Tensor op_table_to_global(const at::Tensor& table_in, int64_t tokens_per_batch) {
+    check_gpu(table_in, "neighbor_indices");
+    TORCH_CHECK(table_in.scalar_type() == at::kInt || table_in.scalar_type() == at::kLong,
+                "neighbor_indices must be int32 or int64");
+    TORCH_CHECK(table_in.numel() % 9 == 0, "neighbor_indices must have 9 entries per row");
+    TORCH_CHECK(tokens_per_batch >= 0, "tokens_per_batch must be >= 0");
+    at::Tensor table = table_in.contiguous();
+    const int64_t rows = table.numel() / 9;
+    c10::DeviceGuard g(table.device());
+    at::Tensor out = at::empty({rows, 9}, table.options().dtype(at::kInt));
+    if (rows == 0) return out;
+    at::Tensor vmax = table.max();  // device scalar, no sync
+    check_status(svtad_table_to_global(table.data_ptr(), table.scalar_type() == at::kLong ? 64 : 32, rows,
+                                       tokens_per_batch, vmax.data_ptr(), out.data_ptr<int32_t>(), stream_of(table)),
+                 "table_to_global");
+    return out;
+}
+
 // remap_neighbor_table(table [B, N_prev, 9] int32, keep_idx [B, N_new] int64) -> [B, N_new, 9]
 at::Tensor op_remap_neighbor_table(const at::Tensor& table_in, const at::Tensor& keep_in) {
     check_gpu(table_in, "table");
@@ -886,6 +954,14 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("with_bias"));
     m.def("build_neighbor_table", &op_build_neighbor_table, "Neighbor table from a keep mask",
           py::arg("mask"));
+    m.def("build_neighbor_table_n", &op_build_neighbor_table_n,
+          "Neighbor table from a keep mask with a known row count (one launch, no host sync)",
+          py::arg("mask"), py::arg("n_rows"), py::arg("int64_out") = false);
+    m.def("grid_neighbor_table", &op_grid_neighbor_table, "Full-grid neighbor table in closed form (one launch)",
+          py::arg("frames"), py::arg("h"), py::arg("w"), py::arg("int64_out"), py::arg("like"));
+    m.def("table_to_global", &op_table_to_global,
+          "int32 global table from a local or global one by the max() < N rule, on the device",
+          py::arg("neighbor_indices"), py::arg("tokens_per_batch"));
     m.def("remap_neighbor_table", &op_remap_neighbor_table, "Neighbor table remap after a prune",
           py::arg("table"), py::arg("keep_idx"));
     m.def("prune_tokens", &op_prune_tokens,

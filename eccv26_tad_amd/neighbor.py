@@ -7,19 +7,42 @@ integer kernels with bit-identical output.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import opentad_sparse_ops as _ops
 
+# Debug validation of the table after every prune step, as the reference's
+# OPENTAD_DEBUG_SPARSE=1 (internvideo_next.py:32-70, called at :454, :1387,
+# :1426). Off by default: the check synchronises with the host.
+DEBUG_SPARSE = os.environ.get("OPENTAD_DEBUG_SPARSE", "0") == "1"
 
-def build_neighbor_table(mask: torch.Tensor, batched: bool = False) -> torch.Tensor:
+
+def set_debug_sparse(enabled: bool) -> None:
+    """Switch the prune-step table validation on or off at run time."""
+    global DEBUG_SPARSE
+    DEBUG_SPARSE = bool(enabled)
+
+
+def build_neighbor_table(mask: torch.Tensor, batched: bool = False, n: int | None = None,
+                         dtype: torch.dtype = torch.int32) -> torch.Tensor:
     """Table from a keep mask ``[B, T, H, W]`` (or any ``[..., H, W]``).
 
-    Returns int32 ``[N, 9]`` of global indices (-1 = missing) with
-    k = (dy+1)*3 + (dx+1), rows in flattened mask order. With ``batched=True``
-    and a 4-D mask whose samples keep equal counts, returns ``[B, N/B, 9]``.
+    Returns ``[N, 9]`` of global indices (-1 = missing) with
+    k = (dy+1)*3 + (dx+1), rows in flattened mask order, int32 or int64
+    (``dtype``). With ``n``, the number of kept cells the caller knows (the
+    backbone's top-k count), the build is one launch with no host
+    synchronisation; rows past the mask's count are -1. Without it, the table
+    is sized by reading the count back. With ``batched=True`` and a 4-D mask
+    whose samples keep equal counts, returns ``[B, N/B, 9]``.
     """
-    table = _ops.build_neighbor_table(mask)
+    if n is None:
+        table = _ops.build_neighbor_table(mask)
+        if dtype != torch.int32:
+            table = table.to(dtype)
+    else:
+        table = _ops.build_neighbor_table_n(mask, int(n), dtype == torch.int64)
     if batched:
         B = mask.shape[0]
         if table.shape[0] % B:
@@ -32,10 +55,21 @@ def get_initial_neighbor_indices(h: int, w: int, T: int, device, B: int,
                                  dtype: torch.dtype = torch.int32) -> torch.Tensor:
     """Full-grid table ``(B, T*h*w, 9)`` of global indices, as
     ``get_initial_neighbor_indices`` (vit_sparse_adapter_poguise.py:1623-1670 with
-    int32; internvideo_next.py:1896-1945 with int64)."""
-    mask = torch.ones((B, T, h, w), dtype=torch.uint8, device=device)
-    table = _ops.build_neighbor_table(mask).view(B, T * h * w, 9)
-    return table if dtype == torch.int32 else table.to(dtype)
+    int32; internvideo_next.py:1896-1945 with int64): one launch of the closed
+    form, no mask, no host synchronisation."""
+    like = torch.empty(0, device=device)
+    table = _ops.grid_neighbor_table(B * T, h, w, dtype == torch.int64, like)
+    return table.view(B, T * h * w, 9)
+
+
+def global_neighbor_table(neighbor_indices: torch.Tensor, tokens_per_batch: int) -> torch.Tensor:
+    """int32 ``[rows, 9]`` global table from ``neighbor_indices`` ``[..., 9]``
+    (int32 / int64): the reference wrapper's rule (sparse_conv_layer.py:170-177)
+    evaluated on the device. When the table's maximum is below
+    ``tokens_per_batch`` (N of a ``[B, N, C]`` input) the entries are
+    per-sample indices and row i's valid entries get ``(i // N) * N`` added;
+    otherwise they are global already. No host synchronisation."""
+    return _ops.table_to_global(neighbor_indices, int(tokens_per_batch))
 
 
 def remap_neighbor_table(neighbor_indices: torch.Tensor, keep_idx: torch.Tensor) -> torch.Tensor:
@@ -46,6 +80,8 @@ def remap_neighbor_table(neighbor_indices: torch.Tensor, keep_idx: torch.Tensor)
     dt = neighbor_indices.dtype
     t = neighbor_indices if dt == torch.int32 else neighbor_indices.to(torch.int32)
     out = _ops.remap_neighbor_table(t, keep_idx)
+    if DEBUG_SPARSE:
+        validate_neighbor_table(out, keep_idx.shape[1], "remap_neighbor_table")
     return out if dt == torch.int32 else out.to(dt)
 
 
@@ -78,8 +114,11 @@ def prune_tokens(x: torch.Tensor, keep_idx: torch.Tensor, last_idx=None, neighbo
         idx_new = idx_new.to(last_idx.dtype)
     if neighbor_indices is None:
         t_new = None
-    elif dt != torch.int32:
-        t_new = t_new.to(dt)
+    else:
+        if DEBUG_SPARSE:
+            validate_neighbor_table(t_new, keep_idx.shape[1], "prune_tokens")
+        if dt != torch.int32:
+            t_new = t_new.to(dt)
     return x_new, idx_new, t_new
 
 

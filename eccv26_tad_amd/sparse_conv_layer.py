@@ -15,6 +15,7 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import opentad_sparse_ops as _ops
+from .neighbor import global_neighbor_table
 
 try:  # torch >= 2.4
     from torch.amp import custom_bwd as _custom_bwd, custom_fwd as _custom_fwd
@@ -87,13 +88,21 @@ class SparseConv2dFunction(Function):
         return grad_input, None, grad_weight, grad_bias, None, None
 
 
-def _local_tokens_per_batch(x, neighbor_indices):
-    """The reference heuristic (sparse_conv_layer.py:170-177): for 3D input, the
-    table holds local (per-sample) indices when its max is < N."""
-    B, N, _ = x.shape
-    if neighbor_indices.numel() > 0 and int(neighbor_indices.max()) < N:
-        return N
-    return 0
+def _table_and_tpb(x, neighbor_indices, tokens_per_batch):
+    """The int32 ``[rows, 9]`` table and tokens_per_batch for the kernels.
+
+    For a 3D input without an explicit ``tokens_per_batch`` this is the
+    reference heuristic (sparse_conv_layer.py:170-177: local per-sample
+    indices when the table's max is < N), evaluated on the device by
+    ``global_neighbor_table``: the table comes back global, so the kernels run
+    with tokens_per_batch = 0, and there is no host synchronisation (the
+    reference reads ``max()`` back)."""
+    if x.dim() == 3 and tokens_per_batch is None:
+        return global_neighbor_table(neighbor_indices, x.shape[1]), 0
+    nbr = neighbor_indices.reshape(-1, 9)
+    if nbr.dtype != torch.int32:
+        nbr = nbr.to(torch.int32)
+    return nbr, (tokens_per_batch or 0)
 
 
 def _autocast_cast(x, weight, bias):
@@ -118,8 +127,8 @@ class SparseConv2d(nn.Module):
 
     ``forward(x, neighbor_indices)``: x is ``[N, C_in]`` or ``[B, N, C_in]``;
     neighbor_indices ``[N, 9]`` / ``[B, N, 9]`` (int32 or int64, -1 = missing).
-    ``tokens_per_batch`` may be passed to skip the reference's host-side
-    ``max()`` heuristic; ``None`` keeps it.
+    ``tokens_per_batch`` may be passed to skip the reference's ``max()``
+    heuristic; ``None`` keeps it, evaluated on the device (no host sync).
     """
 
     def __init__(self, in_channels, out_channels, bias=True, chunk_size=4096):
@@ -148,18 +157,12 @@ class SparseConv2d(nn.Module):
 
     def forward(self, x, neighbor_indices, tokens_per_batch=None):
         is_batched = x.dim() == 3
-        tpb = 0
+        nbr, tpb = _table_and_tpb(x, neighbor_indices, tokens_per_batch)
         if is_batched:
             B, N, C = x.shape
-            tpb = _local_tokens_per_batch(x, neighbor_indices) if tokens_per_batch is None else tokens_per_batch
             x = x.reshape(-1, C)
-            neighbor_indices = neighbor_indices.reshape(-1, 9)
-        elif tokens_per_batch is not None:
-            tpb = tokens_per_batch
-        if neighbor_indices.dtype != torch.int32:
-            neighbor_indices = neighbor_indices.to(torch.int32)
         x, weight, bias = _autocast_cast(x, self.weight, self.bias)
-        out = SparseConv2dFunction.apply(x, neighbor_indices, weight, bias, tpb, self.chunk_size)
+        out = SparseConv2dFunction.apply(x, nbr, weight, bias, tpb, self.chunk_size)
         if is_batched:
             out = out.view(B, N, -1)
         return out
@@ -221,18 +224,12 @@ class SparseDepthwiseConv2d(nn.Module):
 
     def forward(self, x, neighbor_indices, tokens_per_batch=None):
         is_batched = x.dim() == 3
-        tpb = 0
+        nbr, tpb = _table_and_tpb(x, neighbor_indices, tokens_per_batch)
         if is_batched:
             B, N, C = x.shape
-            tpb = _local_tokens_per_batch(x, neighbor_indices) if tokens_per_batch is None else tokens_per_batch
             x = x.reshape(-1, C)
-            neighbor_indices = neighbor_indices.reshape(-1, 9)
-        elif tokens_per_batch is not None:
-            tpb = tokens_per_batch
-        if neighbor_indices.dtype != torch.int32:
-            neighbor_indices = neighbor_indices.to(torch.int32)
         x, weight, bias = _autocast_cast(x, self.weight, self.bias)
-        out = SparseDepthwiseConv2dFunction.apply(x, neighbor_indices, weight, bias, tpb)
+        out = SparseDepthwiseConv2dFunction.apply(x, nbr, weight, bias, tpb)
         if is_batched:
             out = out.view(B, N, -1)
         return out

@@ -229,6 +229,37 @@ int svtad_table_fill(const uint8_t* mask, const int32_t* frame_offsets, int64_t 
                      int w, int32_t* table, void* stream);
 
 /*
+ * One-launch table builds, with no host synchronisation.
+ *
+ * svtad_table_build: the table svtad_table_scan + svtad_table_fill write,
+ * for a caller that knows the row count N (the backbone's kept-token count,
+ * e.g. B * ceil(r * T * h * w) after a top-k prune) and allocates
+ * table [n_rows, 9] itself. Rows past the mask's kept count are -1; kept cells
+ * past n_rows are not written. index_bits 32 (int32 entries,
+ * vit_sparse_adapter_poguise.py) or 64 (int64, internvideo_next.py:1896-1945).
+ * mask 16-byte aligned, at most 4 MiB (larger masks: scan + fill). One launch.
+ *
+ * svtad_table_grid: the full-grid table (every cell kept) in closed form,
+ * table [n_frames * h * w, 9], as get_initial_neighbor_indices
+ * (vit_sparse_adapter_poguise.py:1623-1670; int64 in internvideo_next.py).
+ * One launch, no mask.
+ *
+ * svtad_table_to_global: the reference wrapper's tokens_per_batch heuristic
+ * (sparse_conv_layer.py:170-177) on the device: with table_max (the table's
+ * maximum entry, a device scalar of the table's type) < tokens_per_batch the
+ * entries are per-sample (local) indices and each valid entry of row i gets
+ * (i / tokens_per_batch) * tokens_per_batch added; otherwise they are copied.
+ * Writes int32 out [n_rows, 9] (-1 for negative entries and values past the
+ * int32 range), which every kernel then reads with tokens_per_batch = 0, the
+ * same sources as the reference's tokens_per_batch = N. One launch.
+ */
+int svtad_table_build(const uint8_t* mask, int64_t n_frames, int h, int w, int64_t n_rows, void* table,
+                      int index_bits, void* stream);
+int svtad_table_grid(int64_t n_frames, int h, int w, void* table, int index_bits, void* stream);
+int svtad_table_to_global(const void* table, int index_bits, int64_t n_rows, int64_t tokens_per_batch,
+                          const void* table_max, int32_t* out, void* stream);
+
+/*
  * Table remap after a prune (poguise.py:913-977; internvideo_next.py:1447-1492):
  * out[b*n_new+j, k] = mapping[table[b*n_prev + keep_idx[b,j], k]] for valid
  * entries, where mapping[b*n_prev + keep_idx[b,j]] = b*n_new + j and -1

@@ -241,6 +241,26 @@ def test_dw_bwd_arguments_checked_on_host(lib):
     assert st != 0
 
 
+def test_one_launch_table_arguments_checked_on_host(lib):
+    buf = ctypes.create_string_buffer(64)
+    aligned = ctypes.c_void_p((ctypes.addressof(buf) + 15) & ~15)
+    # index width 32 or 64; h*w <= 16384; at most 4 MiB of mask; 16-byte aligned mask
+    assert lib.svtad_table_build(aligned, I64(1), 2, 2, I64(4), aligned, 16, None) == -1
+    assert lib.svtad_table_build(aligned, I64(1), 200, 200, I64(4), aligned, 32, None) == -3
+    st = lib.svtad_table_build(aligned, I64(300), 128, 128, I64(4), aligned, 32, None)
+    assert st == -3 and b"4 MiB" in lib.svtad_last_error()
+    unaligned = ctypes.c_void_p(aligned.value + 1)
+    st = lib.svtad_table_build(unaligned, I64(1), 2, 2, I64(4), aligned, 32, None)
+    assert st == -1 and b"aligned" in lib.svtad_last_error()
+    assert lib.svtad_table_build(None, I64(1), 2, 2, I64(0), None, 64, None) == 0  # no rows: nothing to do
+    assert lib.svtad_table_grid(I64(1), 0, 3, aligned, 32, None) == -1
+    assert lib.svtad_table_grid(I64(0), 3, 3, None, 64, None) == 0
+    assert lib.svtad_table_to_global(aligned, 32, I64(-1), I64(4), aligned, aligned, None) == -1
+    st = lib.svtad_table_to_global(None, 64, I64(3), I64(4), aligned, aligned, None)
+    assert st == -1 and b"null pointer" in lib.svtad_last_error()
+    assert lib.svtad_table_to_global(None, 32, I64(0), I64(4), None, None, None) == 0
+
+
 def test_table_limits_rejected(lib):
     st = lib.svtad_table_scan(ctypes.create_string_buffer(8), I64(1), 200, 200,
                               ctypes.create_string_buffer(8), None)
@@ -257,7 +277,7 @@ def test_extension_module_api():
                  "build_neighbor_table", "remap_neighbor_table", "transpose_neighbor_table",
                  "validate_neighbor_table", "prune_tokens", "bwd_packed", "adapter_down",
                  "adapter_up", "linear_wgrad", "column_sums", "gelu_backward_split", "gamma_grad", "up_proj_grads",
-                 "dw_bwd", "heatmap_add_"):
+                 "dw_bwd", "heatmap_add_", "build_neighbor_table_n", "grid_neighbor_table", "table_to_global"):
         assert hasattr(ops, name)
     import torch
 
