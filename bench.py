@@ -484,14 +484,29 @@ def cpu_baseline(budget_s: float):
     per = el / steps
     by = sum(op_bytes(n, C, C, 4).values())
     cpu = "unknown"
+    phys = set()
     try:
         with open("/proc/cpuinfo") as f:
+            pid = None
             for line in f:
-                if line.startswith("model name"):
+                if line.startswith("model name") and cpu == "unknown":
                     cpu = line.split(":", 1)[1].strip()
-                    break
+                elif line.startswith("physical id"):
+                    pid = line.split(":", 1)[1].strip()
+                elif line.startswith("core id"):
+                    phys.add((pid, line.split(":", 1)[1].strip()))
     except OSError:
         pass
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    # the fp64 torch oracle of the test suite (dense conv2d on the zero-filled
+    # grid and its autograd) on the same workload, torch's CPU threads
+    import torch
+
+    from tests.helpers import dense_reference
+
+    t1 = time.perf_counter()
+    dense_reference(mask, x, w, b, go)
+    fp64_s = time.perf_counter() - t1
     return {
         "value": round(by / per / 1e9, 3), "unit": "GB/s",
         "cores": sv_oracle.num_threads(), "kind": "port",
@@ -499,19 +514,23 @@ def cpu_baseline(budget_s: float):
                    f"{steps} step(s) in {el:.1f} s, {per * 1e3:.1f} ms/step; "
                    f"host {cpu} ({platform.machine()})"),
         "ms_per_step": round(per * 1e3, 3),
+        "host": {"cpu": cpu, "logical_cpus_available": avail, "logical_cpus": os.cpu_count(),
+                 "physical_cores": len(phys) or None, "omp_threads": sv_oracle.num_threads()},
+        "torch_fp64_oracle": {"ms_per_step": round(fp64_s * 1e3, 1), "threads": torch.get_num_threads(),
+                              "what": "dense float64 conv2d on the zero-filled grid + autograd (tests/helpers.py)"},
     }
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--keep", type=float, default=0.55, help="headline keep rate")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
@@ -562,10 +581,15 @@ def main():
     flops_9n = 3 * 2 * 9 * n * C * C
     flops_useful = 3 * 2 * prob.valid * C * C
 
-    # table build (mask already resident): scan + fill
+    # table build (mask already resident): one launch with the kept count the
+    # caller knows (no host sync), and the full-grid table of the backbone's
+    # first block (closed form, one launch)
     import eccv26_tad_amd as sv
 
-    table_ms = time_events(lambda: sv.build_neighbor_table(prob.mask), 20)
+    table_ms = time_events(lambda: sv.build_neighbor_table(prob.mask, n=n), 50)
+    grid_ms = time_events(lambda: sv.get_initial_neighbor_indices(H, W, T, dev, B), 50)
+    if not torch.equal(sv.build_neighbor_table(prob.mask, n=n), prob.table):
+        raise RuntimeError("one-launch table differs from the scan + fill table")
 
     # timed fwd+bwd steps
     log(f"bench: N={n}, warmup {args.warmup}, steps {args.steps}")
@@ -573,15 +597,19 @@ def main():
         prob.step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s_ev.record()
-    for _ in range(args.steps):
+    # one event before every step and one after the last: the mean over the K
+    # steps (ms_per_step) and the per-step median
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    evs[0].record()
+    for i in range(args.steps):
         prob.step()
-    e_ev.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = s_ev.elapsed_time(e_ev) / args.steps
-    log(f"bench: {ms * 1e3:.1f} us/step (wall {wall / args.steps * 1e3:.1f} us/step)")
+    ms = evs[0].elapsed_time(evs[-1]) / args.steps
+    per_step = sorted(evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps))
+    med_ms = per_step[len(per_step) // 2]
+    log(f"bench: {ms * 1e3:.1f} us/step mean, {med_ms * 1e3:.1f} median (wall {wall / args.steps * 1e3:.1f} us/step)")
 
     # HIP graph replay of the same step
     graph_ms = None
@@ -679,6 +707,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
         "us_per_step": round(ms * 1e3, 2),
+        "median_us_per_step": round(med_ms * 1e3, 2),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -695,6 +724,9 @@ def main():
         "graph_us_per_step": round(graph_ms * 1e3, 2) if graph_ms else None,
         "pass_us": {k: round(v * 1e3, 2) for k, v in phases.items()},
         "table_build_us": round(table_ms * 1e3, 2),
+        "table_build_bytes": int(prob.mask.numel() + 36 * n),
+        "table_build_gbs": round((prob.mask.numel() + 36 * n) / (table_ms * 1e-3) / 1e9, 1),
+        "grid_table_us": round(grid_ms * 1e3, 2),
         "dense_us": round(dense * 1e3, 2) if dense is not None else None,
         "speedup_vs_dense": round(dense / ms, 3) if dense is not None else None,
         "roofline": roof,
