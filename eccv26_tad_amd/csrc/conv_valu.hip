@@ -375,6 +375,48 @@ __global__ __launch_bounds__(256) void k_dw_vec(const T* __restrict__ src, const
     *(u32x4*)(out + i * c + ch) = __builtin_bit_cast(u32x4, o);
 }
 
+// The row lanes' sums of a depthwise backward-weight workgroup: thread (row
+// lane rl, chunk q) holds acc[k][j] for channel q * VEC + j, k < 9 the
+// offsets and k = 9 the bias. Each (k, channel) sum is added over the R row
+// lanes in order 0 .. R-1 through LDS, five offsets at a time, eight LDS reads
+// in flight, and stored at ws_split[k * c + channel]. LDS layout
+// [kk][rl][j][q]: the 64 lanes of a store instruction write 64 consecutive
+// words and a read instruction's lanes read consecutive (j, q) positions, so
+// neither has bank conflicts (a [kk][rl][channel] layout, each lane storing
+// its VEC consecutive channels, makes lanes 32 bytes apart collide 8 ways).
+template <typename A, int VEC>
+__device__ __forceinline__ void dw_row_lane_sums(const A (&acc)[10][VEC], A* __restrict__ red, bool active, int rl,
+                                                 int q, int R, int c, int cpr, A* __restrict__ ws_split, int tid,
+                                                 int nthreads) {
+#pragma unroll
+    for (int k0 = 0; k0 < 10; k0 += 5) {
+        if (active) {
+#pragma unroll
+            for (int kk = 0; kk < 5; ++kk)
+#pragma unroll
+                for (int j = 0; j < VEC; ++j) red[((kk * R + rl) * VEC + j) * cpr + q] = acc[k0 + kk][j];
+        }
+        __syncthreads();
+        for (int pi = tid; pi < 5 * c; pi += nthreads) {
+            const int kk = pi / c, u = pi - kk * c;  // u = j * cpr + chunk
+            const int j = u / cpr, qq = u - j * cpr;
+            const A* col = red + (int64_t)kk * R * c + u;  // row lane stride VEC * cpr = c
+            A v = (A)0;
+            int h0 = 0;
+            for (; h0 + 8 <= R; h0 += 8) {
+                A t[8];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) t[h] = col[(h0 + h) * c];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) v += t[h];
+            }
+            for (; h0 < R; ++h0) v += col[h0 * c];
+            ws_split[(int64_t)(k0 + kk) * c + qq * VEC + j] = v;
+        }
+        __syncthreads();
+    }
+}
+
 // ws[s][k][c] = sum over the rows i of split s of go[i,c] x[src(i,k),c] for
 // k < 9 and ws[s][9][c] = sum of go[i,c] (the bias; one partial row of 10 c
 // per split, reduced in one launch): one workgroup of 512 threads per split,
@@ -439,37 +481,8 @@ __global__ __launch_bounds__(512) void k_dw_bw_vec(const T* __restrict__ go, con
             add(g2, v2);
         }
     }
-    // two rounds of five offsets (the bias is offset 9): row lane rl's sums
-    // of offset k0 + kk at red[(kk * R + rl) * c + channel]
-#pragma unroll
-    for (int k0 = 0; k0 < 10; k0 += 5) {
-        if (active) {
-#pragma unroll
-            for (int kk = 0; kk < 5; ++kk)
-#pragma unroll
-                for (int j = 0; j < VEC; ++j) red[(kk * R + rl) * c + ch + j] = acc[k0 + kk][j];
-        }
-        __syncthreads();
-        // (offset, channel) pair p summed over the row lanes in order 0 .. R-1,
-        // eight LDS reads in flight at a time
-        for (int pi = tid; pi < 5 * c; pi += 512) {
-            const int kk = pi / c, t = pi - kk * c;
-            const A* col = red + (int64_t)kk * R * c + t;
-            A v = (A)0;
-            int q = 0;
-            for (; q + 8 <= R; q += 8) {
-                A u[8];
-#pragma unroll
-                for (int h = 0; h < 8; ++h) u[h] = col[(q + h) * c];
-#pragma unroll
-                for (int h = 0; h < 8; ++h) v += u[h];
-            }
-            for (; q < R; ++q) v += col[q * c];
-            const int k = k0 + kk;
-            ws[((int64_t)s * 10 + k) * c + t] = v;
-        }
-        __syncthreads();
-    }
+    // the 10 sums per channel over the row lanes, in order
+    dw_row_lane_sums<A, VEC>(acc, red, active, rl, ch / VEC, R, c, cpr, ws + (int64_t)s * 10 * c, tid, 512);
 }
 
 // Depthwise backward in one pass over the rows: the backward-weight partials
@@ -569,34 +582,9 @@ __global__ __launch_bounds__(512) void k_dw_bwd_vec(const T* __restrict__ go, co
             *(u32x4*)(gi + i * c + ch) = __builtin_bit_cast(u32x4, o);
         }
     }
-    __syncthreads();  // red aliases nothing, but the last chunk's LDS readers finish first
-    // the weight / bias partials as in k_dw_bw_vec
-#pragma unroll
-    for (int k0 = 0; k0 < 10; k0 += 5) {
-        if (active) {
-#pragma unroll
-            for (int kk = 0; kk < 5; ++kk)
-#pragma unroll
-                for (int j = 0; j < VEC; ++j) red[(kk * R + rl) * c + ch + j] = acc[k0 + kk][j];
-        }
-        __syncthreads();
-        for (int pi = tid; pi < 5 * c; pi += 512) {
-            const int kk = pi / c, tt = pi - kk * c;
-            const A* col = red + (int64_t)kk * R * c + tt;
-            A v = (A)0;
-            int q = 0;
-            for (; q + 8 <= R; q += 8) {
-                A u[8];
-#pragma unroll
-                for (int h = 0; h < 8; ++h) u[h] = col[(q + h) * c];
-#pragma unroll
-                for (int h = 0; h < 8; ++h) v += u[h];
-            }
-            for (; q < R; ++q) v += col[q * c];
-            ws[((int64_t)s * 10 + k0 + kk) * c + tt] = v;
-        }
-        __syncthreads();
-    }
+    // the weight / bias partials as in k_dw_bw_vec (red aliases nothing the
+    // row loop uses)
+    dw_row_lane_sums<A, VEC>(acc, red, active, rl, ch / VEC, R, c, cpr, ws + (int64_t)s * 10 * c, tid, 512);
     const int any = __syncthreads_or(orphan);
     if (tid == 0) flags[s] = any ? 1u : 0u;
 }

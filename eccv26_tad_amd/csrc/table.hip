@@ -334,18 +334,21 @@ __global__ __launch_bounds__(256) void k_table_build(const uint8_t* __restrict__
 // Full-grid table (every cell kept) in closed form: row i = f * h * w + y * w
 // + x, entry k -> i + (dy * w + dx) when (y + dy, x + dx) is in the frame,
 // else -1 (get_initial_neighbor_indices, vit_sparse_adapter_poguise.py:
-// 1623-1670). One thread per entry, consecutive entries per thread block.
-template <typename I>
-__global__ __launch_bounds__(256) void k_table_grid(int64_t n_entries, int h, int w, I* __restrict__ table) {
-    const int cells = h * w;
-    for (int64_t e = blockIdx.x * (int64_t)256 + threadIdx.x; e < n_entries; e += (int64_t)gridDim.x * 256) {
-        const int64_t row = e / 9;
+// 1623-1670). One thread per entry, consecutive entries per thread block;
+// the entry index and the divisions by 9, h * w and w in E (uint32_t when
+// the table has fewer than 2^32 entries: a 64-bit division is a long
+// software sequence on the GPU).
+template <typename I, typename E>
+__global__ __launch_bounds__(256) void k_table_grid(E n_entries, E h, E w, I* __restrict__ table) {
+    const E cells = h * w;
+    for (E e = blockIdx.x * (E)256 + threadIdx.x; e < n_entries; e += (E)gridDim.x * 256) {
+        const E row = e / 9;
         const int k = (int)(e - row * 9);
-        const int p = (int)(row % cells);
-        const int y = p / w, x = p - y * w;
+        const E p = row % cells;
+        const E y = p / w, x = p - y * w;
         const int dy = k / 3 - 1, dx = k % 3 - 1;
-        const int yy = y + dy, xx = x + dx;
-        table[e] = (yy >= 0 && yy < h && xx >= 0 && xx < w) ? (I)(row + dy * w + dx) : (I)-1;
+        const bool in = (dy >= 0 || y > 0) && (dy <= 0 || y + 1 < h) && (dx >= 0 || x > 0) && (dx <= 0 || x + 1 < w);
+        table[e] = in ? (I)((int64_t)row + dy * (int64_t)w + dx) : (I)-1;
     }
 }
 
@@ -546,11 +549,22 @@ extern "C" int svtad_table_grid(int64_t n_frames, int h, int w, void* table, int
     if (rows == 0) return SVTAD_OK;
     if (!table) return set_error(SVTAD_ERR_INVALID, "table_grid: null pointer");
     hipStream_t s = (hipStream_t)stream;
-    const dim3 grid(grid_for(rows * 9, 256));
-    if (index_bits == 32)
-        hipLaunchKernelGGL(k_table_grid<int32_t>, grid, dim3(256), 0, s, rows * 9, h, w, (int32_t*)table);
-    else
-        hipLaunchKernelGGL(k_table_grid<int64_t>, grid, dim3(256), 0, s, rows * 9, h, w, (int64_t*)table);
+    const int64_t entries = rows * 9;
+    const dim3 grid(grid_for(entries, 256));
+    if (entries <= (int64_t)UINT32_MAX - (int64_t)grid.x * 256) {  // the loop's e + stride stays in 32 bits
+        const uint32_t ne = (uint32_t)entries, hh = (uint32_t)h, ww = (uint32_t)w;
+        if (index_bits == 32)
+            hipLaunchKernelGGL((k_table_grid<int32_t, uint32_t>), grid, dim3(256), 0, s, ne, hh, ww, (int32_t*)table);
+        else
+            hipLaunchKernelGGL((k_table_grid<int64_t, uint32_t>), grid, dim3(256), 0, s, ne, hh, ww, (int64_t*)table);
+    } else {
+        if (index_bits == 32)
+            hipLaunchKernelGGL((k_table_grid<int32_t, int64_t>), grid, dim3(256), 0, s, entries, (int64_t)h,
+                               (int64_t)w, (int32_t*)table);
+        else
+            hipLaunchKernelGGL((k_table_grid<int64_t, int64_t>), grid, dim3(256), 0, s, entries, (int64_t)h,
+                               (int64_t)w, (int64_t*)table);
+    }
     return launch_status();
 }
 
