@@ -48,25 +48,32 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     BwPlan p;
     p.path = bw_mfma_supported(dtype, n, c_in, c_out) ? 1 : 0;
     int tm = 64, tn = 64;
-    if (p.path) bw_mfma_tiles(c_in, c_out, &tm, &tn);
-    const int64_t tiles = 9 * cdiv(c_in, tm) * cdiv(c_out, tn);
+    bool big = false;
+    if (p.path) big = bw_mfma_tiles(c_in, c_out, &tm, &tn);
+    // work units per split: the large-tile kernel splits the center offset's
+    // rows in two halves (its off-center units only visit rows whose neighbor
+    // exists, about half of them at moderate keep rates, so the center units
+    // get half the rows to take about as long)
+    const int units = big ? 10 : 9;
+    const int gran = big ? 256 : 128;  // whole pairs of 64-row stages per unit
+    const int64_t tiles = units * cdiv(c_in, tm) * cdiv(c_out, tn);
     int64_t splits;
     if (p.path) {
-        // Fewest workgroup rounds times the longest split, with a fixed cost
-        // per workgroup worth about 256 rows: splits of whole 128-row pairs of
-        // stages, at most kMaxSplitRows - 128 rows (the LDS row list), at
-        // least 256 rows where n allows. A partial second round costs a full
-        // round, so a count just above the CU count loses to twice as many
-        // half-length splits.
+        // Fewest workgroup rounds times the longest unit, with a fixed cost
+        // per workgroup worth about 256 rows: splits of whole multiples of
+        // gran rows, at most kMaxSplitRows (the LDS row list), at least 256
+        // rows where n allows. A partial second round costs a full round, so
+        // a count just above the CU count loses to twice as many half-length
+        // splits.
         const int64_t cu = cu_count();
-        const int64_t s_min = std::max<int64_t>(1, cdiv(n, kMaxSplitRows - 128));
+        const int64_t s_min = std::max<int64_t>(1, cdiv(n, kMaxSplitRows - gran));
         const int64_t s_cap = std::max<int64_t>(s_min, std::min<int64_t>(cdiv(n, 256), 4 * cu / tiles + 1));
         splits = s_min;
         int64_t best = INT64_MAX;
         for (int64_t sc = s_min; sc <= s_cap; ++sc) {
-            const int64_t r = cdiv(cdiv(std::max<int64_t>(n, 1), sc), 128) * 128;
+            const int64_t r = cdiv(cdiv(std::max<int64_t>(n, 1), sc), gran) * gran;
             const int64_t se = std::max<int64_t>(1, cdiv(n, r));
-            const int64_t cost = cdiv(se * tiles, cu) * (r + 256);
+            const int64_t cost = cdiv(se * tiles, cu) * ((big ? r / 2 : r) + 256);
             if (cost < best) {
                 best = cost;
                 splits = se;
@@ -77,13 +84,13 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     }
     splits = std::max<int64_t>(1, splits);
     int64_t rps = cdiv(std::max<int64_t>(n, 1), splits);
-    // whole pairs of 64-row stages: a split's row list (at most
+    // whole pairs of 64-row stages per unit: a split's row list (at most
     // kMaxSplitRows) is read two 64-row stages per iteration by the MFMA kernel
-    rps = cdiv(rps, 128) * 128;
+    rps = cdiv(rps, gran) * gran;
     splits = std::max<int64_t>(1, cdiv(n, rps));
     p.splits = (int)splits;
     p.rows_per_split = rps;
-    p.ws_bytes = (size_t)splits * ((size_t)9 * c_in * c_out + (size_t)c_out) * acc_bytes(dtype);
+    p.ws_bytes = (size_t)splits * ((size_t)units * c_in * c_out + (size_t)2 * c_out) * acc_bytes(dtype);
     return p;
 }
 

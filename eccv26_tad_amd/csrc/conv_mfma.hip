@@ -875,8 +875,14 @@ __global__ __launch_bounds__(256) void k_bw_mfma(
 
 // ---------------------------------------------------------------------------
 // Backward-weight partials, large tiles (the shapes of the adapter convs).
-// A workgroup owns one offset k, a BM x BN (ci x co) tile of gw and one row
-// split, and has two kinds of waves:
+// A workgroup owns one work unit of a row split and a BM x BN (ci x co) tile
+// of gw. A split has 10 units: each off-center offset k over the split's
+// rows, visiting only the rows whose neighbor k exists (compacted in row
+// order; a missing neighbor's x row is zero and adds nothing), and the center
+// offset over each half of the split (all rows: the center units also sum
+// the bias). At moderate keep rates about half of an off-center offset's
+// neighbors exist, so all units take about as many stages. The workgroup has
+// two kinds of waves:
 //  * WGM x WGN matrix waves, each owning FM x FN 16x16 fragments of the tile;
 //    per 64-row stage they read their fragments from LDS and run the MFMAs.
 //  * WA + WB staging waves: per stage each thread loads an 8-row x 8-channel
@@ -893,8 +899,9 @@ __global__ __launch_bounds__(256) void k_bw_mfma(
 // wave doing both, every wave of a SIMD is in its transpose phase at the same
 // time and the matrix core idles.) Partials are stored in fragment order
 // (each lane's 4 values contiguous); k_bw_reduce sums the splits in a fixed
-// order. In the k == 4, ci-tile 0 workgroups the staging waves also sum the
-// staged go rows per column (bias).
+// order. In the center units of ci-tile 0 the go staging threads also sum
+// their transposed go blocks per column (bias; fp32, v_dot2 against ones),
+// and the row groups' sums are added in order through LDS at the end.
 // ---------------------------------------------------------------------------
 // A transposed stage row (one channel, KR = 64 source rows) is 128 bytes with
 // no padding; its eight 16-byte chunks (8 rows each) are stored at position
@@ -941,21 +948,44 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
     __shared__ f32x4 qsum[4][64];
     const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int bm = wgm * fm * 16, bn = wgn * fn * 16;
-    const int64_t per_split = (int64_t)n_off * c_in * c_out;
-    const int64_t quads = per_split / 4;
+    // a split's partials: one block of c_in * c_out per work unit (with the
+    // 9 offsets: offsets 0-3, the center's two halves, offsets 5-8)
+    const int units = n_off == 9 ? 10 : n_off;
+    const int64_t per_off = (int64_t)c_in * c_out;
+    const int64_t per_split = units * per_off;
+    const int64_t quads = (int64_t)n_off * per_off / 4;
     const int64_t e = blk * 64 + lane;
     const int spt = (splits + 3) / 4;
     const int s0 = g * spt, s1 = min(splits, s0 + spt);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (e < quads) {
-        const float* pe = part + e * 4;
-        for (int q = s0; q < s1; q += 8) {
-            f32x4 v[8];
+        const int ko = (int)(e * 4 / per_off);
+        const int64_t within = e * 4 - ko * per_off;
+        const int unit = n_off == 9 && ko > 4 ? ko + 1 : ko;
+        const float* pe = part + unit * per_off + within;
+        if (n_off == 9 && ko == 4) {
+            // the center's two halves, added in order per split
+            for (int q = s0; q < s1; q += 4) {
+                f32x4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                v[u] = q + u < s1 ? *(const f32x4*)(pe + (int64_t)(q + u) * per_split) : f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int u = 0; u < 4; ++u) {
+                    const bool ok = q + u < s1;
+                    v[2 * u] = ok ? *(const f32x4*)(pe + (int64_t)(q + u) * per_split) : f32x4{0.f, 0.f, 0.f, 0.f};
+                    v[2 * u + 1] = ok ? *(const f32x4*)(pe + per_off + (int64_t)(q + u) * per_split)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc += v[u];
+                for (int u = 0; u < 8; ++u) acc += v[u];
+            }
+        } else {
+            for (int q = s0; q < s1; q += 8) {
+                f32x4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    v[u] = q + u < s1 ? *(const f32x4*)(pe + (int64_t)(q + u) * per_split) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int u = 0; u < 8; ++u) acc += v[u];
+            }
         }
     }
     qsum[g][lane] = acc;
@@ -1003,6 +1033,21 @@ __device__ __forceinline__ void bw_reduce_bias(int64_t c, const float* __restric
     gb[c] = (T)v;
 }
 
+// acc + lo + hi of a pair of 16-bit values (v_dot2 against (1, 1): the
+// products are exact, the sum is fp32)
+template <typename T>
+__device__ __forceinline__ float dot2_ones(uint32_t v, float acc);
+template <>
+__device__ __forceinline__ float dot2_ones<f16>(uint32_t v, float acc) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v), h2{(_Float16)1, (_Float16)1}, acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2_ones<bf16>(uint32_t v, float acc) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b2, v), b2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+}
+
 // staging waves of k_bw_big: one 8-row x 8-channel block of x rows or of go
 // rows per thread and stage.
 // With n_off = 9, nbr is the [n, 9] neighbor table and the partials cover the
@@ -1038,8 +1083,6 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     constexpr int CPT_A = BM / 8, CPT_B = BN / 8;  // channel chunks per row group
     constexpr int WA = (A_ITEMS + 63) / 64, WB = (B_ITEMS + 63) / 64;
     static_assert(NMW + WA + WB == NT / 64, "wave roles");
-    constexpr int NST = 64 * (WA + WB);         // staging threads
-    constexpr int BPT = (BN + NST - 1) / NST;  // bias columns per staging thread
 
     // [buf][channel][row] tiles: the x operand's two buffers, then go's
     __shared__ __align__(16) u16 stage_lds[2 * (BM + BN) * KR];
@@ -1054,26 +1097,68 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int64_t lin = xcd_tile(blockIdx.x, n_blocks);
-    const int tiles = n_off * n_ci_tiles * n_co_tiles;
+    // work units of a split: with the 9 offsets, units 0-3 and 6-9 are the
+    // offsets 0-3 and 5-8 over the split's rows, and units 4 and 5 the center
+    // offset over the split's first and second half
+    const int units = n_off == 9 ? 10 : 1;
+    const int tiles = units * n_ci_tiles * n_co_tiles;
     const int s = (int)(lin / tiles);
     int rem = (int)(lin - (int64_t)s * tiles);
-    const int k = rem / (n_ci_tiles * n_co_tiles);
-    rem -= k * n_ci_tiles * n_co_tiles;
+    const int u = rem / (n_ci_tiles * n_co_tiles);
+    rem -= u * n_ci_tiles * n_co_tiles;
+    const int k = n_off == 9 ? (u < 4 ? u : (u < 6 ? 4 : u - 1)) : 0;
+    const bool center = n_off == 9 && k == 4;
+    const bool compact = n_off == 9 && !center;  // uniform
     const int cit = rem / n_co_tiles, cot = rem % n_co_tiles;
     const int ci0 = cit * BM, co0 = cot * BN;
-    const int64_t r_begin = (int64_t)s * rows_per_split;
-    const int rows = (int)max<int64_t>(0, min(n, r_begin + rows_per_split) - r_begin);
+    const int64_t r_begin = (int64_t)s * rows_per_split + (center ? (u - 4) * (rows_per_split / 2) : 0);
+    const int64_t r_len = center ? rows_per_split / 2 : rows_per_split;
+    const int rows_raw = (int)max<int64_t>(0, min(n, r_begin + r_len) - r_begin);
+    const bool do_bias = ws_bias != nullptr && (n_off == 9 ? center : true) && ci0 == 0;  // uniform
+
+    // An off-center offset's list holds only the rows whose neighbor exists,
+    // in row order (a missing neighbor's x row is zero and adds nothing):
+    // order-preserving compaction, one chunk of NT rows at a time.
+    __shared__ int wcnt[NT / 64];
+    int rows = rows_raw;
+    if (compact) {
+        int total = 0;
+        for (int base = 0; base < rows_raw; base += NT) {
+            const int r = base + tid;
+            const int64_t sr = r < rows_raw ? src_row(nbr, r_begin + r, k, n, tpb) : -1;
+            const bool v = sr >= 0;
+            const uint64_t bal = __ballot(v);
+            const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (lane == 0) wcnt[wave] = __popcll(bal);
+            __syncthreads();
+            int off = 0, all = 0;
+#pragma unroll
+            for (int w = 0; w < NT / 64; ++w) {
+                const int c = wcnt[w];
+                off += w < wave ? c : 0;
+                all += c;
+            }
+            if (v) {
+                srow[0][total + off + before] = (uint32_t)sr * (uint32_t)(c_in * 2);
+                srow[1][total + off + before] = (uint32_t)r * (uint32_t)(c_out * 2);
+            }
+            total += all;
+            __syncthreads();  // wcnt is rewritten by the next chunk
+        }
+        rows = total;
+    }
     const int steps = (rows + KR - 1) / KR;
-    const bool do_bias = ws_bias != nullptr && k == (n_off == 9 ? 4 : 0) && ci0 == 0;  // uniform
 
     // The staging waves read the list two stages at a time up to stage
     // steps_even + 1 (steps rounded up to even), so it is filled that far;
     // with rows_per_split <= kMaxSplitRows (checked on the host) that is at
-    // most TROWS entries.
+    // most TROWS entries. A compacted list is only padded.
     const int steps_even = (steps + 1) & ~1;
-    for (int r = tid; r < (steps_even + 2) * KR; r += NT) {
+    for (int r = (compact ? rows : 0) + tid; r < (steps_even + 2) * KR; r += NT) {
+        const bool live = !compact && r < rows;
         int64_t sr = -1;
-        if (r < rows) {
+        if (live) {
             if (n_off == 9) {
                 sr = src_row(nbr, r_begin + r, k, n, tpb);
             } else {  // row list (NULL: identity)
@@ -1082,7 +1167,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
             }
         }
         srow[0][r] = sr >= 0 ? (uint32_t)sr * (uint32_t)(c_in * 2) : kOOB;
-        srow[1][r] = r < rows ? (uint32_t)r * (uint32_t)(c_out * 2) : kOOB;
+        srow[1][r] = live ? (uint32_t)r * (uint32_t)(c_out * 2) : kOOB;
     }
     __syncthreads();
 
@@ -1114,19 +1199,18 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
             }
         };
         __syncthreads();  // stage 0 staged
-        for (int t = 0; t < steps; t += 2) {
-            compute(0);  // stage t
-            __syncthreads();
-            compute(1);  // stage t+1 (zeros past the end)
+        for (int t = 0; t < steps; ++t) {
+            compute(t & 1);  // stage t
             __syncthreads();
         }
         // partial tile in fragment order: [wave][a][b][lane][4]
-        float* dst = ws + (((int64_t)s * n_off + k) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
+        float* dst = ws + (((int64_t)s * units + u) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
 #pragma unroll
         for (int a = 0; a < FM; ++a)
 #pragma unroll
             for (int b = 0; b < FN; ++b)
                 *(f32x4*)(dst + (((wv * FM + a) * FN + b) * 64 + lane) * 4) = acc[a][b];
+        if (do_bias) __syncthreads();  // the staging waves' bias reduction
     } else {
         // ---------------- staging waves ----------------
         // item e of the wave's operand: rows 8*(e / cpt) .. +7 of the
@@ -1148,7 +1232,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
         const int chan = (role_a ? ci0 : co0) + cl;
         const bool chan_ok = has_item && chan < (role_a ? c_in : c_out);
         const rsrc_t rs = make_rsrc(role_a ? (const void*)x : (const void*)(go + r_begin * c_out),
-                                    role_a ? (uint32_t)(n_src * c_in * 2) : (uint32_t)((int64_t)rows * c_out * 2));
+                                    role_a ? (uint32_t)(n_src * c_in * 2) : (uint32_t)((int64_t)rows_raw * c_out * 2));
         // offsets stay below 2^31 + 2^16 (kOOB plus a channel offset): no wrap
         const uint32_t chan_b = chan_ok ? (uint32_t)chan * 2u : kOOB;
         const uint32_t* const tab = srow[role_a ? 0 : 1] + rgp * BW_IROWS;
@@ -1169,6 +1253,14 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
                 rg[r] = bload16(rs, chan_ok ? so + chan_b : kOOB);
             }
         };
+        // column sums of the staged go rows (the bias gradient; the center
+        // units of column tile 0): each thread adds its 8-row x 8-channel
+        // blocks per channel in fp32, two rows per dot2 instruction on the
+        // transposed registers, and stores one partial per row group
+        const bool bias_thr = do_bias && !role_a;  // wave-uniform
+        float bacc[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) bacc[c] = 0.f;
         auto store = [&](int buf, const u32x4* rg) {
             u32x4 o[8];
             transpose8(rg, o);
@@ -1177,54 +1269,41 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
 #pragma unroll
                 for (int c = 0; c < 8; ++c) *(u32x4*)&d[c * KR + bw_swz(cl + c, rgp)] = o[c];
             }
-        };
-        // column sums of the staged go rows (the bias gradient; one
-        // workgroup per column tile), while the matrix waves use the buffer
-        float bsum[BPT];
+            if (bias_thr) {
 #pragma unroll
-        for (int j = 0; j < BPT; ++j) bsum[j] = 0.f;
-        auto bias_sums = [&](int buf) {
-            if (do_bias) {
+                for (int c = 0; c < 8; ++c)
 #pragma unroll
-                for (int j = 0; j < BPT; ++j) {
-                    const int col = st + j * NST;
-                    if (col < BN) {
-                        // per-lane chunk order chosen so that the 16 lanes
-                        // read together hit distinct bank groups (fixed per
-                        // lane: same sum every run)
-                        const int hi = (col >> 3) & 7, perm = hi ^ (((hi << 1) | (hi >> 2)) & 7);
-#pragma unroll
-                        for (int r = 0; r < KR / 8; ++r) {
-                            const u32x4 v = *(const u32x4*)&Bs[buf][col][bw_swz(col, r ^ perm)];
-#pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                bsum[j] += (float)__builtin_bit_cast(T, (u16)(v[q] & 0xffffu));
-                                bsum[j] += (float)__builtin_bit_cast(T, (u16)(v[q] >> 16));
-                            }
-                        }
-                    }
-                }
+                    for (int q = 0; q < 4; ++q) bacc[c] = dot2_ones<T>(o[c][q], bacc[c]);
             }
         };
         load(0, r0s);
         load(1, r1s);
         store(0, r0s);
         __syncthreads();  // stage 0 staged
-        for (int t = 0; t < steps; t += 2) {
+        int t = 0;
+        for (; t + 1 < steps; t += 2) {
             load(t + 2, r0s);  // registers of set 0 are free again
-            store(1, r1s);     // stage t+1 (zeros past the end)
-            bias_sums(0);
+            store(1, r1s);     // stage t+1
             __syncthreads();
             load(t + 3, r1s);
-            store(0, r0s);     // stage t+2
-            bias_sums(1);
+            store(0, r0s);     // stage t+2 (zeros past the end)
             __syncthreads();
         }
+        if (t < steps) __syncthreads();  // the matrix waves' last single stage
         if (do_bias) {
+            // the row groups' sums added in order through LDS (the stage
+            // buffers are free: every wave is past its last stage)
+            float* const red = (float*)stage_lds;  // [row group][column]
+            if (bias_thr && has_item) {
 #pragma unroll
-            for (int j = 0; j < BPT; ++j) {
-                const int col = st + j * NST;
-                if (col < BN && co0 + col < c_out) ws_bias[(int64_t)s * c_out + co0 + col] = bsum[j];
+                for (int c = 0; c < 8; ++c) red[rgp * BN + cl + c] = bacc[c];
+            }
+            __syncthreads();
+            for (int col = tid - NMW * 64; col < BN; col += NT - NMW * 64) {
+                float v = 0.f;
+#pragma unroll
+                for (int g = 0; g < BW_IROWS; ++g) v += red[g * BN + col];
+                if (co0 + col < c_out) ws_bias[((int64_t)s * 2 + (u - 4)) * c_out + co0 + col] = v;
             }
         }
     }
@@ -1246,7 +1325,8 @@ __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ par
         bw_reduce_quads<T>(blockIdx.x, part, splits, n_off, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles,
                            n_co_tiles, gw);
     else if (gb)
-        bw_reduce_bias<T>(((int64_t)blockIdx.x - quad_blocks) * 256 + threadIdx.x, part_b, splits, c_out, gb);
+        bw_reduce_bias<T>(((int64_t)blockIdx.x - quad_blocks) * 256 + threadIdx.x, part_b,
+                          n_off == 9 ? 2 * splits : splits, c_out, gb);
     if (!oj.gi || (oj.flag && *oj.flag == 0u)) return;
     for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < oj.n * 9; e += (int64_t)gridDim.x * 256)
         orphan_entry<T, false>(e, (const T*)oj.go, oj.nbr, (const T*)oj.w, (T*)oj.gi, oj.n, oj.c_in,
@@ -1517,15 +1597,16 @@ static bool big_cfg(int c_in, int c_out, BigCfg* out) {
     return false;
 }
 
-void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn) {
+bool bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn) {
     BigCfg c;
     if (big_cfg(c_in, c_out, &c)) {
         *tm = 16 * c.wgm * c.fm;
         *tn = 16 * c.wgn * c.fn;
-    } else {
-        *tm = bw_mfma_tile(c_in);
-        *tn = bw_mfma_tile(c_out);
+        return true;
     }
+    *tm = bw_mfma_tile(c_in);
+    *tn = bw_mfma_tile(c_out);
+    return false;
 }
 
 template <typename T, int FM, int FN, int WGM, int WGN>
@@ -1535,12 +1616,14 @@ static int launch_big(const BwPlan& p, const void* go, const void* x, const int3
     constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
     if (c_in % BM != 0 || c_out % BN != 0) return set_error(SVTAD_ERR_INVALID, "bwd_w: widths are not whole tiles");
     const int nci = c_in / BM, nco = c_out / BN;
-    const int64_t blocks = (int64_t)9 * nci * nco * p.splits;
-    // one BM x BN tile per workgroup (splits x 9 x nci x nco of them), then
-    // the bias partials
-    const size_t need = (size_t)blocks * BM * BN * 4 + (part_b ? (size_t)p.splits * c_out * 4 : 0);
-    const int st = check_split_plan("bwd_w", p, n, need, ws_bytes);
+    const int64_t blocks = (int64_t)10 * nci * nco * p.splits;
+    // one BM x BN tile per workgroup (splits x 10 work units x nci x nco of
+    // them), then the bias partials (two per split: the center's halves)
+    const size_t need = (size_t)blocks * BM * BN * 4 + (part_b ? (size_t)2 * p.splits * c_out * 4 : 0);
+    int st = check_split_plan("bwd_w", p, n, need, ws_bytes);
     if (st) return st;
+    if (p.rows_per_split % (4 * KR) != 0)  // the center's halves are whole pairs of stages
+        return set_error(SVTAD_ERR_INVALID, "bwd_w: rows_per_split is not a multiple of 256");
     hipLaunchKernelGGL((k_bw_big<T, FM, FN, WGM, WGN>), dim3((unsigned)blocks),
                        dim3(bw_big_threads(FM, FN, WGM, WGN)),
                        0, s, (const T*)go, (const T*)x, nbr, part, part_b, n, c_in, c_out, tpb,
@@ -1586,7 +1669,10 @@ int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int
             const OrphanJob* oj, bool* oj_taken, hipStream_t s) {
     *oj_taken = false;
     float* part = (float*)ws;
-    float* part_b = gb ? part + (int64_t)p.splits * 9 * c_in * c_out : nullptr;
+    BigCfg bc0;
+    // the large-tile kernel keeps 10 work units per split (the center offset in two halves)
+    const int units = big_cfg(c_in, c_out, &bc0) ? 10 : 9;
+    float* part_b = gb ? part + (int64_t)p.splits * units * c_in * c_out : nullptr;
     const int st = dtype == SVTAD_F16
                        ? bw_dispatch<f16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, ws_bytes, s)
                        : bw_dispatch<bf16>(p, go, x, nbr, part, part_b, n, c_in, c_out, tpb, ws_bytes, s);

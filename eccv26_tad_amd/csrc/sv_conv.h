@@ -81,8 +81,11 @@ constexpr int kMaxSplitRows = 4096;
 // compute units of the current device (256 on MI355X)
 int cu_count();
 int bw_mfma_tile(int c);
-// (ci, co) tile edges of the MFMA backward-weight kernel chosen for a shape.
-void bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn);
+// (ci, co) tile edges of the MFMA backward-weight kernel chosen for a shape;
+// true for the large-tile kernel, whose splits hold 10 work units (the 8
+// off-center offsets over the split's rows, the center offset over each half)
+// and whose rows_per_split is a multiple of 256.
+bool bw_mfma_tiles(int c_in, int c_out, int* tm, int* tn);
 // Orphan pass handed to the backward-weight reduction (one launch less when
 // the backward-input and backward-weight run together): flag as for orphans
 // (NULL: always run).
