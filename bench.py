@@ -281,7 +281,7 @@ def blob_mask(keep: float, seed: int = SEED + 1):
     return m.view(B, T, H, W)
 
 
-def depthwise_measure(dev, reps):
+def depthwise_measure(dev, reps, keeps=None):
     """benchmark config 3: depthwise (groups = C = 192) 3x3 SparseConv2D, fp16,
     B2 x T80 x 14x14, clustered keep masks, fwd + bwd_in + bwd_w with bias (the
     autograd step of SparseDepthwiseConv2d: the forward, then the one-pass
@@ -315,7 +315,7 @@ def depthwise_measure(dev, reps):
         td = time_events(run_dense, reps, warm=5)
         dense = td if dense is None else min(dense, td)
     rows = []
-    for kr in KEEPS:
+    for kr in keeps or KEEPS:
         mask = blob_mask(kr).to(dev)
         table = sv.build_neighbor_table(mask)
         n = int(table.shape[0])
@@ -534,6 +534,8 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE counters) and exit")
+    ap.add_argument("--one-keep", action="store_true",
+                    help="with --only depthwise: time the --keep rate alone (for counter runs)")
     ap.add_argument("--only", choices=("adapter", "prune", "depthwise", "large"), default=None,
                     help="only time the fused adapter or the prune step, print its JSON and exit "
                          "(for kernel traces of those paths)")
@@ -567,7 +569,8 @@ def main():
         print(json.dumps({"prune_step": prune_measure(dev, args.steps, False)}), flush=True)
         return
     if args.only == "depthwise":
-        print(json.dumps({"depthwise": depthwise_measure(dev, args.steps)}), flush=True)
+        keeps = [args.keep] if args.one_keep else KEEPS
+        print(json.dumps({"depthwise": depthwise_measure(dev, args.steps, keeps)}), flush=True)
         return
     if args.only == "large":
         print(json.dumps({"large_channel": large_channel_measure(dev, args.steps)}), flush=True)
@@ -645,7 +648,12 @@ def main():
     phases = {p: time_events(getattr(prob, p), max(args.steps, 20))
               for p in ("pack", "fwd", "bwd_in", "bwd_w", "bwd_w_partials", "bwd")}
     dom = max(("fwd", "bwd_w_partials"), key=phases.get)
-    f_pass = 2 * 9 * n * C * C
+    # algorithmic flops of one GEMM pass: the valid (row, offset) entries E
+    # of the table times 2 * C_in * C_out (the dense-K count 9 * N, which
+    # includes the products with missing neighbors' zero rows, is reported
+    # beside it)
+    f_pass = 2 * prob.valid * C * C
+    f_pass_9n = 2 * 9 * n * C * C
     t_dom = phases[dom] * 1e-3
     by_dom = by["fwd" if dom == "fwd" else "bwd_w"]
     mfma_t = f_pass / (MFMA_PEAK_TFLOPS[dname] * 1e12)
@@ -657,6 +665,10 @@ def main():
         roof = {"bound": "hbm", "achieved": round(by_dom / t_dom / 1e9, 3),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s"}
     roof["frac"] = round(roof["achieved"] / roof["peak"], 5)
+    if roof["unit"] == "TFLOP/s":
+        roof["basis"] = "useful flops 2*E*C^2 per launch, E = valid table entries"
+        roof["achieved_9n"] = round(f_pass_9n / t_dom / 1e12, 3)
+        roof["frac_9n"] = round(roof["achieved_9n"] / roof["peak"], 5)
     key = "k_gg_wideIDF16_Li0" if dom == "fwd" else "k_bw_big"
     roof["traffic"] = pmc_traffic(key) if abs(args.keep - 0.55) < 1e-9 else None
     if roof["traffic"] is not None:

@@ -339,7 +339,9 @@ __global__ __launch_bounds__(256) void k_dw_vec(const T* __restrict__ src, const
     constexpr int VEC = Vec16<T>::N;
     typedef typename Acc<T>::type A;
     const int cpr = c / VEC;
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    // consecutive row blocks on one XCD: the rows a block gathers (within
+    // about one image row of its own) are mostly in the same L2
+    const int64_t e = xcd_tile(blockIdx.x, gridDim.x) * 256 + threadIdx.x;
     if (e >= n * cpr) return;
     const int64_t i = e / cpr;
     const int ch = (int)(e - i * cpr) * VEC;
@@ -436,7 +438,7 @@ __global__ __launch_bounds__(512) void k_dw_bw_vec(const T* __restrict__ go, con
     const int cpr = c / VEC, R = 512 / cpr;
     const int tid = threadIdx.x, rl = tid / cpr, ch = (tid - rl * cpr) * VEC;
     const bool active = rl < R;
-    const int s = blockIdx.x;
+    const int s = (int)xcd_tile(blockIdx.x, gridDim.x);  // neighboring splits on one XCD (shared halo rows)
     const int64_t r_begin = (int64_t)s * rows_per_split;
     const int64_t r_end = min(n, r_begin + rows_per_split);
     const rsrc_t rs = make_rsrc(x, (uint32_t)(n * c * (int64_t)sizeof(T)));
@@ -518,7 +520,7 @@ __global__ __launch_bounds__(512) void k_dw_bwd_vec(const T* __restrict__ go, co
     const int chunk = (kDwChunkRows / R) * R;
     const int tid = threadIdx.x, rl = tid / cpr, ch = (tid - rl * cpr) * VEC;
     const bool active = rl < R;
-    const int s = blockIdx.x;
+    const int s = (int)xcd_tile(blockIdx.x, gridDim.x);  // neighboring splits on one XCD (shared halo rows)
     const int64_t r_begin = (int64_t)s * rows_per_split;
     const int64_t r_end = min(n, r_begin + rows_per_split);
     const rsrc_t rs = make_rsrc(x, (uint32_t)(n * c * (int64_t)sizeof(T)));
