@@ -620,12 +620,15 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
             epilogue(std::integral_constant<int, 0>{});
     }
     __syncthreads();
+    // 16-byte row pieces out, non-temporal: the output is not read by this
+    // launch, and streaming it out saves the L2 write-back at the kernel's end
+    // (c2 at 55 % keep: 1.1-1.3 µs per launch)
     constexpr int CH = BN / 8;
     for (int e = tid; e < BM * CH; e += 256 * WS) {
         const int r = e / CH, c8 = e - (e / CH) * CH;
         const int64_t i = row0 + r;
         const int col = col0 + c8 * 8;
-        if (i < n && col < n_out) *(u32x4*)(out + i * n_out + col) = *(const u32x4*)&ot[r * OP + c8 * 8];
+        if (i < n && col < n_out) __builtin_nontemporal_store(*(const u32x4*)&ot[r * OP + c8 * 8], (u32x4*)(out + i * n_out + col));
     }
 }
 
@@ -940,6 +943,7 @@ __device__ __forceinline__ void transpose8(const u32x4* in, u32x4* out) {
 // (one per wave of the workgroup) share a quadruple: thread g sums its
 // quarter of the splits with all its loads in flight, and the quarters are
 // added in order g = 0..3 through LDS, so the order of the sum is fixed.
+// The partials are read once: non-temporal loads.
 template <typename T>
 __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __restrict__ part,
                                                 int splits, int n_off, int c_in, int c_out, int fm, int fn,
@@ -970,8 +974,8 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const bool ok = q + u < s1;
-                    v[2 * u] = ok ? *(const f32x4*)(pe + (int64_t)(q + u) * per_split) : f32x4{0.f, 0.f, 0.f, 0.f};
-                    v[2 * u + 1] = ok ? *(const f32x4*)(pe + per_off + (int64_t)(q + u) * per_split)
+                    v[2 * u] = ok ? __builtin_nontemporal_load((const f32x4*)(pe + (int64_t)(q + u) * per_split)) : f32x4{0.f, 0.f, 0.f, 0.f};
+                    v[2 * u + 1] = ok ? __builtin_nontemporal_load((const f32x4*)(pe + per_off + (int64_t)(q + u) * per_split))
                                       : f32x4{0.f, 0.f, 0.f, 0.f};
                 }
 #pragma unroll
@@ -982,7 +986,7 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
                 f32x4 v[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u)
-                    v[u] = q + u < s1 ? *(const f32x4*)(pe + (int64_t)(q + u) * per_split) : f32x4{0.f, 0.f, 0.f, 0.f};
+                    v[u] = q + u < s1 ? __builtin_nontemporal_load((const f32x4*)(pe + (int64_t)(q + u) * per_split)) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int u = 0; u < 8; ++u) acc += v[u];
             }
@@ -1203,13 +1207,16 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
             compute(t & 1);  // stage t
             __syncthreads();
         }
-        // partial tile in fragment order: [wave][a][b][lane][4]
+        // partial tile in fragment order: [wave][a][b][lane][4]; non-temporal
+        // stores (read once, by the reduction): they stream out while the
+        // other workgroups finish instead of waiting in the L2 for the write-
+        // back at the kernel's end
         float* dst = ws + (((int64_t)s * units + u) * n_ci_tiles * n_co_tiles + cit * n_co_tiles + cot) * BM * BN;
 #pragma unroll
         for (int a = 0; a < FM; ++a)
 #pragma unroll
             for (int b = 0; b < FN; ++b)
-                *(f32x4*)(dst + (((wv * FM + a) * FN + b) * 64 + lane) * 4) = acc[a][b];
+                __builtin_nontemporal_store(acc[a][b], (f32x4*)(dst + (((wv * FM + a) * FN + b) * 64 + lane) * 4));
         if (do_bias) __syncthreads();  // the staging waves' bias reduction
     } else {
         // ---------------- staging waves ----------------

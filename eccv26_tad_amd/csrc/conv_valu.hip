@@ -374,7 +374,8 @@ __global__ __launch_bounds__(256) void k_dw_vec(const T* __restrict__ src, const
     Vec16<T> o;
 #pragma unroll
     for (int j = 0; j < VEC; ++j) o.e[j] = from_acc<T>(acc[j]);
-    *(u32x4*)(out + i * c + ch) = __builtin_bit_cast(u32x4, o);
+    // non-temporal: not read by this launch (saves the L2 write-back at its end)
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), (u32x4*)(out + i * c + ch));
 }
 
 // The row lanes' sums of a depthwise backward-weight workgroup: thread (row
@@ -581,7 +582,7 @@ __global__ __launch_bounds__(512) void k_dw_bwd_vec(const T* __restrict__ go, co
             Vec16<T> o;
 #pragma unroll
             for (int j = 0; j < VEC; ++j) o.e[j] = from_acc<T>(gs[j]);
-            *(u32x4*)(gi + i * c + ch) = __builtin_bit_cast(u32x4, o);
+            __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), (u32x4*)(gi + i * c + ch));  // as k_dw_vec
         }
     }
     // the weight / bias partials as in k_dw_bw_vec (red aliases nothing the
