@@ -60,11 +60,14 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     int64_t splits;
     if (p.path) {
         // Fewest workgroup rounds times the longest unit, with a fixed cost
-        // per workgroup worth about 256 rows: splits of whole multiples of
-        // gran rows, at most kMaxSplitRows (the LDS row list), at least 256
-        // rows where n allows. A partial second round costs a full round, so
-        // a count just above the CU count loses to twice as many half-length
-        // splits.
+        // per workgroup worth about 256 rows, plus (large-tile kernel) the
+        // partial tiles' write and read-back, worth about 5 rows per
+        // workgroup over the whole grid (measured: at c2 this picks 7 splits
+        // at 10 % keep and 14 at 55 %, 3.4 and 4 µs faster per step than the
+        // 13 and 23 without it): splits of whole multiples of gran rows, at
+        // most kMaxSplitRows (the LDS row list), at least 256 rows where n
+        // allows. A partial second round costs a full round, so a count just
+        // above the CU count loses to twice as many half-length splits.
         const int64_t cu = cu_count();
         const int64_t s_min = std::max<int64_t>(1, cdiv(n, kMaxSplitRows - gran));
         const int64_t s_cap = std::max<int64_t>(s_min, std::min<int64_t>(cdiv(n, 256), 4 * cu / tiles + 1));
@@ -73,7 +76,7 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
         for (int64_t sc = s_min; sc <= s_cap; ++sc) {
             const int64_t r = cdiv(cdiv(std::max<int64_t>(n, 1), sc), gran) * gran;
             const int64_t se = std::max<int64_t>(1, cdiv(n, r));
-            const int64_t cost = cdiv(se * tiles, cu) * ((big ? r / 2 : r) + 256);
+            const int64_t cost = cdiv(se * tiles, cu) * ((big ? r / 2 : r) + 256) + (big ? 5 * se * tiles : 0);
             if (cost < best) {
                 best = cost;
                 splits = se;
