@@ -199,10 +199,12 @@ class SparseConvAdapterFunction(Function):
     ``addmm(go, du, W_d)``, where the two-node chain computes ``du W_d`` and
     then autograd adds ``go`` in a separate pass over the 768-wide tokens.
     The kernels are those of ``AdapterDownFunction``, ``SparseConv2dFunction``
-    and ``AdapterUpFunction``."""
+    and ``AdapterUpFunction``; ``packed`` is the SparseConv2D weight's
+    ``(packed_fwd, packed_bwd)`` as ``SparseConv2dFunction`` takes it."""
 
     @staticmethod
-    def forward(ctx, x, w_d, b_d, w_c, b_c, w_u, b_u, gamma, nbr, n_special, tpb, hm_rows=None, hm_gate=None):
+    def forward(ctx, x, w_d, b_d, w_c, b_c, w_u, b_u, gamma, nbr, n_special, tpb, hm_rows=None, hm_gate=None,
+                packed=None):
         S = int(n_special)
         pre, sp, pa = _ops.adapter_down(x, w_d, b_d, S)
         if hm_rows is not None:
@@ -212,7 +214,10 @@ class SparseConvAdapterFunction(Function):
         if c_in % 4 != 0:
             raise ValueError(f"C_in ({c_in}) must be divisible by 4 for optimized kernel.")
         mode = BIAS_NONE if b_c is None else (BIAS_FP32 if c_in >= IMPLICIT_GEMM_MIN_CIN else BIAS_AFTER)
-        pf, pb = _ops.pack_weight(w_c, True, any(ctx.needs_input_grad))
+        need_bwd = any(ctx.needs_input_grad)
+        if packed is None or (need_bwd and packed[1] is None):
+            packed = _ops.pack_weight(w_c, True, need_bwd)
+        pf, pb = packed
         processed = _ops.fwd_packed(pa, nbr, w_c, pf, b_c, tpb, mode)
         out = _ops.adapter_up(sp, processed, w_u, b_u, gamma, x)
         ctx.save_for_backward(x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma, hm_rows, hm_gate)
@@ -265,7 +270,7 @@ class SparseConvAdapterFunction(Function):
         gw_d = _wgrad(du2, _NO_ROWS(du2), x2) if need[1] else None
         gb_d = _colsum(du2) if has_bd and need[2] else None
         return (gx, gw_d, gb_d, gw_c if need[3] else None, gb_c if need_bc else None, gw_u, gb_u, g_gamma,
-                None, None, None, None, g_gate)
+                None, None, None, None, g_gate, None)
 
 
 def _trunc_normal_init(layer, std):
@@ -389,9 +394,11 @@ class SparseConvAdapter(nn.Module):
                 base = torch.arange(B, device=x.device).view(B, 1) * S + 1
                 hm_rows = (base + cells).reshape(-1).to(torch.int32)
                 hm_gate = self.heatmap_gate
+            cache = conv.packed_weight_cache
+            packed = None if cache is None else cache.get(conv.weight, conv.weight, torch.is_grad_enabled())
             return SparseConvAdapterFunction.apply(x, self.down_proj.weight, self.down_proj.bias, conv.weight,
                                                    conv.bias, self.up_proj.weight, self.up_proj.bias, self.gamma,
-                                                   nbr, S, tokens_per_batch, hm_rows, hm_gate)
+                                                   nbr, S, tokens_per_batch, hm_rows, hm_gate, packed)
         sp, pa = AdapterDownFunction.apply(x, self.down_proj.weight, self.down_proj.bias, S)
         processed = conv(pa, nbr, tokens_per_batch=tokens_per_batch)
         x_comb = torch.cat([sp, processed.view(B, N - S, -1)], dim=1)

@@ -33,13 +33,61 @@ IMPLICIT_GEMM_MIN_CIN = 128
 BIAS_NONE, BIAS_FP32, BIAS_AFTER = 0, 1, 2
 
 
+class PackedWeightCache:
+    """The matrix-core layouts of one module's weight (``pack_weight``), kept
+    across forwards while the weight is unchanged, so that a recomputed
+    forward (activation checkpointing) and inference skip the pack launch.
+
+    An entry is reused when the parameter is the same object at the same
+    address with the same version counter (every in-place update made through
+    the tensor bumps it: optimizer steps, ``load_state_dict``, ``copy_`` under
+    ``no_grad``), the compute dtype (the autocast target) and device match,
+    and the current stream is the one the pack ran on. A training step that
+    updates the weight therefore packs once per step, as without the cache.
+    Writes through ``weight.data`` do not bump the version counter: call
+    ``invalidate()`` after them. Inference tensors have no version counter and
+    are packed on every call.
+
+    The backward-input layout ends with the orphan flag word (set by the
+    backward-input kernel when the table has an entry whose symmetric partner
+    is missing, cleared only by a pack): a reused layout keeps a set flag, which
+    makes later backward passes run the orphan pass even for a symmetric table.
+    That costs one launch and never changes a result."""
+
+    def __init__(self):
+        self.invalidate()
+
+    def invalidate(self):
+        self._param = None
+        self._key = None
+        self._packed = None
+
+    def get(self, param, weight, need_bwd):
+        """``(packed_fwd, packed_bwd)`` for ``weight``, which is ``param`` or its
+        cast to the compute dtype; ``packed_bwd`` is None when not requested.
+        None (the caller packs) off the GPU or for an inference tensor."""
+        if not weight.is_cuda or param.is_inference():
+            return None
+        stream = torch.cuda.current_stream(weight.device).cuda_stream
+        key = (param.data_ptr(), param._version, weight.dtype, weight.device, stream)
+        if param is self._param and key == self._key and (self._packed[1] is not None or not need_bwd):
+            return self._packed
+        pf, pb = _ops.pack_weight(weight.detach(), True, need_bwd)
+        self._param, self._key, self._packed = param, key, (pf, pb if need_bwd else None)
+        return self._packed
+
+
 class SparseConv2dFunction(Function):
     """autograd Function of the sparse 3x3 convolution
-    (reference sparse_conv_layer.py:29-123)."""
+    (reference sparse_conv_layer.py:29-123).
+
+    ``packed`` (not in the reference; optional) is ``(packed_fwd,
+    packed_bwd)`` from ``pack_weight(weight, True, ...)``, ``packed_bwd`` None
+    when it was not requested; without it the weight is packed here."""
 
     @staticmethod
     @custom_fwd
-    def forward(ctx, x, neighbor_indices, weight, bias=None, tokens_per_batch=0, chunk_size=0):
+    def forward(ctx, x, neighbor_indices, weight, bias=None, tokens_per_batch=0, chunk_size=0, packed=None):
         _, C_in, C_out = weight.shape
         if C_in % 4 != 0:
             raise ValueError(f"C_in ({C_in}) must be divisible by 4 for optimized kernel.")
@@ -53,8 +101,11 @@ class SparseConv2dFunction(Function):
             mode = BIAS_AFTER
         # Both matrix-core weight layouts in one launch; the backward-input one
         # is kept for backward (empty tensors where the shape has none).
-        packed_fwd, packed_bwd = _ops.pack_weight(weight, True, bool(ctx.needs_input_grad[0]))
-        ctx.save_for_backward(x, neighbor_indices, weight, bias, packed_bwd)
+        need_bwd = bool(ctx.needs_input_grad[0])
+        if packed is None or (need_bwd and packed[1] is None):
+            packed = _ops.pack_weight(weight, True, need_bwd)
+        packed_fwd, packed_bwd = packed
+        ctx.save_for_backward(x, neighbor_indices, weight, bias, packed_bwd if need_bwd else None)
         return _ops.fwd_packed(x, neighbor_indices, weight, packed_fwd, bias, tokens_per_batch, mode)
 
     @staticmethod
@@ -73,7 +124,7 @@ class SparseConv2dFunction(Function):
             grad_input = gi.view(x.shape) if x.dim() == 3 else gi
             grad_weight = gw
             grad_bias = gb if need_b else None
-            return grad_input, None, grad_weight, grad_bias, None, None
+            return grad_input, None, grad_weight, grad_bias, None, None, None
         if ctx.needs_input_grad[0]:
             grad_input = _ops.bwd_in_packed(go, neighbor_indices, weight, packed_bwd,
                                             x.numel() // x.shape[-1], C_in, tpb)
@@ -85,7 +136,7 @@ class SparseConv2dFunction(Function):
                 grad_weight = gw
             if need_b:
                 grad_bias = gb
-        return grad_input, None, grad_weight, grad_bias, None, None
+        return grad_input, None, grad_weight, grad_bias, None, None, None
 
 
 def _table_and_tpb(x, neighbor_indices, tokens_per_batch):
@@ -129,6 +180,10 @@ class SparseConv2d(nn.Module):
     neighbor_indices ``[N, 9]`` / ``[B, N, 9]`` (int32 or int64, -1 = missing).
     ``tokens_per_batch`` may be passed to skip the reference's ``max()``
     heuristic; ``None`` keeps it, evaluated on the device (no host sync).
+
+    ``packed_weight_cache`` (a ``PackedWeightCache``; not in the reference)
+    keeps the weight's matrix-core layouts between forwards while the weight
+    is unchanged; set it to None to pack on every forward.
     """
 
     def __init__(self, in_channels, out_channels, bias=True, chunk_size=4096):
@@ -141,6 +196,7 @@ class SparseConv2d(nn.Module):
             self.bias = nn.Parameter(torch.Tensor(out_channels))
         else:
             self.register_parameter("bias", None)
+        self.packed_weight_cache = PackedWeightCache()
         self.reset_parameters()
 
     def reset_parameters(self):
@@ -162,7 +218,11 @@ class SparseConv2d(nn.Module):
             B, N, C = x.shape
             x = x.reshape(-1, C)
         x, weight, bias = _autocast_cast(x, self.weight, self.bias)
-        out = SparseConv2dFunction.apply(x, nbr, weight, bias, tpb, self.chunk_size)
+        cache = self.packed_weight_cache
+        packed = None
+        if cache is not None:
+            packed = cache.get(self.weight, weight, torch.is_grad_enabled() and x.requires_grad)
+        out = SparseConv2dFunction.apply(x, nbr, weight, bias, tpb, self.chunk_size, packed)
         if is_batched:
             out = out.view(B, N, -1)
         return out

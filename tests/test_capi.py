@@ -316,6 +316,22 @@ def test_cin_not_divisible_by_4_raises():
                                    torch.zeros(9, 6, 4), None, 0, 0)
 
 
+def test_packed_weight_cache_off_gpu():
+    """The packed-weight cache holds nothing for a CPU weight (the Function
+    then packs, which fails loudly without a GPU), and is not module state."""
+    import torch
+
+    from eccv26_tad_amd import SparseConv2d
+
+    m = SparseConv2d(16, 16)
+    assert m.packed_weight_cache.get(m.weight, m.weight, True) is None
+    assert m.packed_weight_cache._packed is None
+    assert set(m.state_dict()) == {"weight", "bias"}
+    with torch.inference_mode():
+        inf = torch.nn.Parameter(torch.zeros(9, 16, 16))
+    assert m.packed_weight_cache.get(inf, inf, False) is None
+
+
 def test_legacy_weight_remap():
     import torch
 

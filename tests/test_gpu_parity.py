@@ -479,6 +479,105 @@ def test_module_local_table_heuristic(dev, oracle):
     assert torch.allclose(y_local, y_global, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+def test_module_packed_weight_cache(dev, oracle, dname, monkeypatch):
+    """The module's packed-weight cache: a forward on an unchanged weight
+    (inference, a checkpointed recompute) packs nothing and gives the same bits
+    as a module that packs on every call; an in-place weight update, a new
+    dtype under autocast or invalidate() repack, and the results follow the
+    oracle."""
+    import torch
+    import torch.utils.checkpoint as ckpt
+
+    import eccv26_tad_amd.sparse_conv_layer as scl
+    from eccv26_tad_amd import SparseConv2d, build_neighbor_table
+
+    calls = []
+    real_pack = scl._ops.pack_weight
+
+    def counting_pack(*a):
+        calls.append(a[1:])
+        return real_pack(*a)
+
+    monkeypatch.setattr(scl._ops, "pack_weight", counting_pack)
+    torch.manual_seed(3)
+    rng = np.random.default_rng(17)
+    dt = _dt(dname)
+    mask = topk_mask(rng, 2, 4, 14, 14, 0.55)
+    table = build_neighbor_table(torch.from_numpy(mask).to(dev), batched=True)
+    nb, c = table.shape[1], 192
+    m = SparseConv2d(c, c).to(dev).to(dt)
+    ref = SparseConv2d(c, c).to(dev).to(dt)
+    ref.packed_weight_cache = None
+    ref.load_state_dict(m.state_dict())
+    x = torch.randn(2, nb, c, device=dev, dtype=dt)
+    go = torch.randn(2, nb, c, device=dev, dtype=dt)
+    t = table.reshape(-1, 9).cpu().numpy()
+
+    def oracle_ok(y, w, what):
+        xr, wr, br = (_np32(a) for a in (x.reshape(-1, c), w, m.bias))
+        return _err_ok(oracle, _np32(y).reshape(-1, c), oracle.fwd(xr, t, wr, br), TOL[dname], what)
+
+    # inference: one pack (forward layout only) for three forwards
+    with torch.no_grad():
+        calls.clear()
+        ys = [m(x, table) for _ in range(3)]
+        assert calls == [(True, False)]
+        y_ref = ref(x, table)
+    for y in ys:
+        assert torch.equal(y, y_ref)
+    assert oracle_ok(ys[0], m.weight, "inference")
+
+    # an in-place update bumps the version counter: repack, new result
+    with torch.no_grad():
+        m.weight.mul_(0.5)
+        ref.weight.mul_(0.5)
+        calls.clear()
+        y2 = m(x, table)
+        assert len(calls) == 1
+        assert torch.equal(y2, ref(x, table))
+        assert not torch.equal(y2, ys[0])
+    assert oracle_ok(y2, m.weight, "after weight update")
+
+    # training step with activation checkpointing: the recompute reuses the
+    # layouts the first forward packed (both, as x needs a gradient)
+    xg = x.clone().requires_grad_(True)
+    xr_ = x.clone().requires_grad_(True)
+    calls.clear()
+    y = ckpt.checkpoint(m, xg, table, use_reentrant=False)
+    y.backward(go)
+    assert calls == [(True, True)]
+    yr = ref(xr_, table)
+    yr.backward(go)
+    assert torch.equal(y, yr)
+    assert torch.equal(xg.grad, xr_.grad)
+    assert torch.equal(m.weight.grad, ref.weight.grad)
+    assert torch.equal(m.bias.grad, ref.bias.grad)
+
+    # a write through .data is not seen by the version counter; invalidate() repacks
+    with torch.no_grad():
+        m.weight.data.mul_(2.0)
+        m.packed_weight_cache.invalidate()
+        calls.clear()
+        y3 = m(x, table)
+        assert len(calls) == 1
+    assert oracle_ok(y3, m.weight, "after invalidate")
+
+    # autocast to the other half type packs that dtype's layout
+    other = torch.bfloat16 if dt == torch.float16 else torch.float16
+    m32 = SparseConv2d(c, c).to(dev)
+    x32 = x.float()
+    with torch.no_grad(), torch.autocast("cuda", dtype=dt):
+        calls.clear()
+        a = m32(x32, table)
+        b = m32(x32, table)
+        assert len(calls) == 1 and torch.equal(a, b)
+    with torch.no_grad(), torch.autocast("cuda", dtype=other):
+        calls.clear()
+        o = m32(x32, table)
+        assert len(calls) == 1 and o.dtype == other
+
+
 # ---------------------------------------------------------------------------
 # depthwise
 # ---------------------------------------------------------------------------
