@@ -719,6 +719,62 @@ def test_depthwise_one_pass_backward_row_chunks(dev, dname, c):
 # determinism
 # ---------------------------------------------------------------------------
 
+BW_TR_CASES = [
+    # (shape B,T,H,W), keep, C_in, C_out, dtype: the tile configurations of
+    # the transposed-read backward-weight kernel (192 x 192, 128 x 256,
+    # 128 x 128 tiles), several tiles per split, empty and short splits
+    ((2, 8, 14, 14), 0.55, 192, 192, "float16"),
+    ((2, 8, 14, 14), 0.1, 192, 192, "bfloat16"),
+    ((1, 4, 16, 16), 0.5, 256, 256, "bfloat16"),
+    ((1, 4, 16, 16), 0.4, 128, 128, "float16"),
+    ((1, 3, 14, 14), 0.7, 384, 384, "float16"),
+    ((1, 1, 5, 7), 0.3, 192, 192, "float16"),
+]
+
+
+@pytest.mark.skip(reason="the transposed-read backward-weight kernel (loads straight into LDS, "
+                         "ds_read_b64_tr_b16 fragments) made a GPU memory fault on its first case; "
+                         "no cause was found on the CPU, so the kernel was taken out and this "
+                         "comparison does not run")
+@pytest.mark.parametrize("case", BW_TR_CASES, ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}x{c[3]}-{c[4]}")
+def test_bw_transposed_read_kernel_matches_staging_kernel(dev, oracle, case, monkeypatch):
+    """The backward-weight partials from LDS transposing reads (default) and
+    from the staging-wave kernel (SVTAD_BW_TR=0) take the same MFMA inputs in
+    the same order: bit-identical weight gradients. The bias is summed
+    differently (an MFMA against ones vs dot2 row groups): both against the
+    oracle."""
+    import torch
+
+    import opentad_sparse_ops as ops
+
+    shape, keep, ci, co, dname = case
+    dt = _dt(dname)
+    mask, x, w, b, go = _conv_case(41, shape, keep, ci, co, dt)
+    t = oracle.build_table(mask)
+    x, go = _rounded(x, dt), _rounded(go, dt)
+    X, G, T = _t(x, dev, dt), _t(go, dev, dt), torch.from_numpy(t).to(dev)
+    _say(f"bw kernels {case} n={x.shape[0]}")
+    monkeypatch.delenv("SVTAD_BW_TR", raising=False)
+    gw_tr, gb_tr = ops.bwd_w_bias(G, X, T, ci, 0, True)
+    torch.cuda.synchronize()
+    monkeypatch.setenv("SVTAD_BW_TR", "0")
+    gw_st, gb_st = ops.bwd_w_bias(G, X, T, ci, 0, True)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("SVTAD_BW_TR")
+    assert torch.equal(gw_tr, gw_st)
+    tol = TOL[dname]
+    assert _err_ok(oracle, _np32(gw_tr), oracle.bwd_w(go, x, t), tol, "gw")
+    assert _err_ok(oracle, _np32(gb_tr), oracle.bias_grad(go), tol, "gb (transposed reads)")
+    assert _err_ok(oracle, _np32(gb_st), oracle.bias_grad(go), tol, "gb (staging waves)")
+    # the linear layers' weight gradient runs the same kernel with one offset
+    rows = torch.from_numpy(np.random.default_rng(5).integers(0, x.shape[0], x.shape[0]).astype(np.int32)).to(dev)
+    wg_tr = ops.linear_wgrad(G, rows, X)
+    monkeypatch.setenv("SVTAD_BW_TR", "0")
+    wg_st = ops.linear_wgrad(G, rows, X)
+    monkeypatch.delenv("SVTAD_BW_TR")
+    assert torch.equal(wg_tr, wg_st)
+
+
 def test_backward_is_deterministic(dev, oracle):
     import opentad_sparse_ops as ops
     import torch
