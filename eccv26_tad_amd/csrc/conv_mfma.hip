@@ -1122,33 +1122,49 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
 
     // An off-center offset's list holds only the rows whose neighbor exists,
     // in row order (a missing neighbor's x row is zero and adds nothing):
-    // order-preserving compaction, one chunk of NT rows at a time.
-    __shared__ int wcnt[NT / 64];
+    // order-preserving compaction over chunks of NT rows. The table entries of
+    // every chunk are loaded first (one memory round trip for the split), the
+    // per-wave counts of all chunks meet in LDS behind one barrier, and each
+    // thread then places its rows after the rows of earlier chunks and waves.
+    constexpr int MAXCH = (kMaxSplitRows + NT - 1) / NT;
+    __shared__ int wcnt[MAXCH][NT / 64];
     int rows = rows_raw;
     if (compact) {
-        int total = 0;
-        for (int base = 0; base < rows_raw; base += NT) {
-            const int r = base + tid;
-            const int64_t sr = r < rows_raw ? src_row(nbr, r_begin + r, k, n, tpb) : -1;
-            const bool v = sr >= 0;
-            const uint64_t bal = __ballot(v);
-            const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-            if (lane == 0) wcnt[wave] = __popcll(bal);
-            __syncthreads();
-            int off = 0, all = 0;
+        int sv[MAXCH];
 #pragma unroll
-            for (int w = 0; w < NT / 64; ++w) {
-                const int c = wcnt[w];
-                off += w < wave ? c : 0;
-                all += c;
+        for (int c = 0; c < MAXCH; ++c) {
+            const int r = c * NT + tid;
+            sv[c] = r < rows_raw ? (int)src_row(nbr, r_begin + r, k, n, tpb) : -1;
+        }
+#pragma unroll
+        for (int c = 0; c < MAXCH; ++c) {
+            if (c * NT < rows_raw) {  // uniform
+                const uint64_t bal = __ballot(sv[c] >= 0);
+                if (lane == 0) wcnt[c][wave] = __popcll(bal);
             }
-            if (v) {
-                srow[0][total + off + before] = (uint32_t)sr * (uint32_t)(c_in * 2);
-                srow[1][total + off + before] = (uint32_t)r * (uint32_t)(c_out * 2);
+        }
+        __syncthreads();
+        int total = 0;
+#pragma unroll
+        for (int c = 0; c < MAXCH; ++c) {
+            if (c * NT < rows_raw) {  // uniform
+                const bool v = sv[c] >= 0;
+                const uint64_t bal = __ballot(v);
+                const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                int off = 0, all = 0;
+#pragma unroll
+                for (int w = 0; w < NT / 64; ++w) {
+                    const int cnt = wcnt[c][w];
+                    off += w < wave ? cnt : 0;
+                    all += cnt;
+                }
+                if (v) {
+                    srow[0][total + off + before] = (uint32_t)sv[c] * (uint32_t)(c_in * 2);
+                    srow[1][total + off + before] = (uint32_t)(c * NT + tid) * (uint32_t)(c_out * 2);
+                }
+                total += all;
             }
-            total += all;
-            __syncthreads();  // wcnt is rewritten by the next chunk
         }
         rows = total;
     }
