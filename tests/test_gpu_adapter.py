@@ -126,6 +126,33 @@ def test_fused_adapter_matches_fp32_reference(dev, dname, case):
     assert y.dtype == dt
 
 
+def test_fused_adapter_packed_weight_cache(dev):
+    """The fused adapter reuses its sparse conv's packed weight while the
+    weight is unchanged and repacks after an in-place update: the same bits
+    as a copy that packs on every call, and the training step still matches
+    the float32 reference after the update."""
+    import copy
+
+    mod, idx, table, x, go = _setup(dev, torch.float16, B=3, T=4, H=6, W=7, keep=0.3, embed=128,
+                                    mlp_ratio=0.5, S=0, seed=33)
+    H, W, T = 6, 7, 4
+    cache = mod.sparse_conv.packed_weight_cache
+    with torch.no_grad():
+        y1 = mod(x, H, W, idx, T * H * W, table)
+        first = cache._packed
+        y2 = mod(x, H, W, idx, T * H * W, table)
+        assert cache._packed is first and first is not None
+        assert torch.equal(y1, y2)
+        mod.sparse_conv.weight.mul_(0.5)
+        y3 = mod(x, H, W, idx, T * H * W, table)
+        assert cache._packed is not first
+        fresh = copy.deepcopy(mod)
+        fresh.sparse_conv.packed_weight_cache = None
+        assert torch.equal(y3, fresh(x, H, W, idx, T * H * W, table))
+        assert not torch.equal(y3, y1)
+    _check_against_fp32(mod, idx, table, x, go, H, W, T)
+
+
 # the production configurations set adapter_use_attn to 1, 2 or 3
 # (configs/vitsparse/*/...sparse_adapter.py); 4 is the temporal variant
 @pytest.mark.parametrize("dname", ["float16", "bfloat16"])
