@@ -100,14 +100,27 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
 static BwPlan plan_dw_bw(int64_t n, int c, int dtype) {
     BwPlan p;
     p.path = 0;
-    // about 64 rows per split, at most one split per CU: one workgroup of
-    // the vectorized kernel per split (it holds a CU alone), one per
-    // 64-channel block in the scalar one
-    (void)c;
-    int64_t splits = std::min<int64_t>(cu_count(), std::max<int64_t>(1, cdiv(n, 64)));
-    int64_t rps = cdiv(std::max<int64_t>(n, 1), splits);
-    rps = cdiv(rps, 4) * 4;
-    splits = std::max<int64_t>(1, cdiv(n, rps));
+    const int64_t cu = cu_count();
+    const int vec = dtype == SVTAD_F64 ? 2 : dtype == SVTAD_F32 ? 4 : 8;  // elements per 16 bytes
+    int64_t rps;
+    if (c % vec == 0 && c / vec <= 256) {
+        // The vectorized kernels: one 512-thread workgroup per split (it
+        // holds a CU alone) walks its rows R = 512 / (c / vec) at a time, one
+        // dependent gather round per pass. Every CU gets a split while each
+        // has at least R rows: the fewest passes, and the last one partly
+        // filled rather than fewer splits of full passes (at c = 192 fp16,
+        // 3136 rows: 150 splits of one pass instead of 49 of four; 17248
+        // rows: 254 splits of 68 rows, 0.6 us faster than 206 of 84).
+        const int64_t r = 512 / (c / vec);
+        const int64_t splits = std::min<int64_t>(cu, std::max<int64_t>(1, cdiv(n, r)));
+        rps = cdiv(std::max<int64_t>(n, 1), splits);
+    } else {
+        // the scalar kernel (one workgroup per 64-channel block and split):
+        // about 64 rows per split, at most one split per CU
+        const int64_t splits = std::min<int64_t>(cu, std::max<int64_t>(1, cdiv(n, 64)));
+        rps = cdiv(cdiv(std::max<int64_t>(n, 1), splits), 4) * 4;
+    }
+    const int64_t splits = std::max<int64_t>(1, cdiv(n, rps));
     p.splits = (int)splits;
     p.rows_per_split = rps;
     p.ws_bytes = (size_t)splits * ((size_t)9 * c + (size_t)c) * acc_bytes(dtype);
