@@ -5,6 +5,7 @@
 
 #include "sv_common.h"
 #include "sv_internal.h"
+#include "sv_mfma.h"
 
 namespace svtad {
 
@@ -276,14 +277,36 @@ __global__ __launch_bounds__(256) void k_table_build(const uint8_t* __restrict__
     const int64_t f0 = (int64_t)blockIdx.x * fpw;
     const int64_t f1 = min<int64_t>(n_frames, f0 + fpw);
 
-    // kept cells before the range
-    const int64_t pre_bytes = f0 * cells;
-    int cnt = 0;  // < 2^31: the host limits the mask to 4 MiB
-    for (int64_t c = tid; c < pre_bytes / 16; c += 256) {
-        const uint4 v = *(const uint4*)(mask + c * 16);
-        cnt += nonzero_bytes(v.x) + nonzero_bytes(v.y) + nonzero_bytes(v.z) + nonzero_bytes(v.w);
-    }
-    for (int64_t b = (pre_bytes / 16) * 16 + tid; b < pre_bytes; b += 256) cnt += mask[b] != 0;
+    // kept cells before the range, eight 16-byte reads per thread in flight
+    // at a time (buffer loads: a read past the prefix returns zeros, so the
+    // batch has no branch; one read and its wait per iteration made the last
+    // workgroup of a 160-frame mask wait for eight dependent rounds), plus
+    // the prefix's last pre_bytes % 16 bytes
+    const int pre_bytes = (int)(f0 * cells);  // < 4 MiB (host limit)
+    const int nvec = pre_bytes / 16;
+    const rsrc_t rm = make_rsrc(mask, (uint32_t)nvec * 16u);
+    const int tail = nvec * 16 + tid;
+    // the first 256 cells of the first frame, read with the prefix
+    const rsrc_t rf = make_rsrc(mask, (uint32_t)(n_frames * cells));
+    const bool first_kept = __builtin_amdgcn_raw_buffer_load_b8(
+                                rf, f0 < f1 && tid < cells ? (uint32_t)(pre_bytes + tid) : kOOB, 0, 0) != 0;
+    int cnt = 0;
+    auto batch = [&](int c0, bool with_tail) {
+        u32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int c = c0 + u * 256 + tid;
+            v[u] = bload16(rm, c < nvec ? (uint32_t)c * 16u : kOOB);
+        }
+        if (with_tail)
+            cnt += __builtin_amdgcn_raw_buffer_load_b8(make_rsrc(mask, (uint32_t)pre_bytes),
+                                                       tail < pre_bytes ? (uint32_t)tail : kOOB, 0, 0) != 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            cnt += nonzero_bytes(v[u][0]) + nonzero_bytes(v[u][1]) + nonzero_bytes(v[u][2]) + nonzero_bytes(v[u][3]);
+    };
+    batch(0, true);  // the whole prefix of masks up to 2048 x 16 bytes
+    for (int c0 = 256 * 8; c0 < nvec; c0 += 256 * 8) batch(c0, false);
     for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
     if (tid == 0) base_s = 0;
     __syncthreads();
@@ -296,7 +319,7 @@ __global__ __launch_bounds__(256) void k_table_build(const uint8_t* __restrict__
         int kept_total = 0;
         for (int b0 = 0; b0 < cells; b0 += 256) {
             const int p = b0 + tid;
-            const bool kept = p < cells && m[p] != 0;
+            const bool kept = f == f0 && b0 == 0 ? first_kept : p < cells && m[p] != 0;
             const uint64_t bal = __ballot(kept);
             const int before = __popcll(bal & ((1ull << lane) - 1ull));
             if (lane == 0) wsum[wid] = __popcll(bal);
