@@ -208,6 +208,8 @@ extern "C" int svtad_pack_weight(const void* weight, void* packed_fwd, void* pac
     if ((packed_fwd && !gg_mfma_workspace(dtype, c_in, c_out)) ||
         (packed_bwd && !gg_mfma_workspace(dtype, c_out, c_in)))
         return set_error(SVTAD_ERR_UNSUPPORTED, "pack_weight: shape/dtype has no packed layout");
+    if (9LL * c_in * c_out * 2 >= (int64_t)INT32_MAX)  // the pack kernel reads w with 32-bit offsets
+        return set_error(SVTAD_ERR_UNSUPPORTED, "pack_weight: weight of 2 GiB or more");
     if (!al16(packed_fwd) || !al16(packed_bwd))
         return set_error(SVTAD_ERR_INVALID, "pack_weight: packed buffers must be 16-byte aligned");
     pack_weight(weight, packed_fwd, packed_bwd, c_in, c_out, (hipStream_t)stream);

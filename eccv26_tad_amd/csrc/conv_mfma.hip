@@ -639,6 +639,28 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
 // with B(k,c,n) = w[k][c][n] for the forward (c over c_in, n over c_out) and
 // w[k][n][c] for backward-input (c over c_out, n over c_in). One thread per
 // 16-byte fragment slot; grid cdiv(9*NCS*NB*64, 256).
+//
+// The 8 values of a slot come from buffer loads (zeros past n_out), issued
+// together: forward B(k, c + e, n) = w[k][c + e][n] are 8 strided 2-byte
+// loads, backward-input B(k, c + e, n) = w[k][n][c + e] one 16-byte load when
+// w is 16-byte aligned. (Plain loads under an n < n_out test compiled to a
+// branch and a wait per pair of values, four dependent rounds per slot.) kb
+// is offset k's first element; every offset fits 32 bits (host check).
+template <bool FWD>
+__device__ __forceinline__ u32x4 pack_slot(rsrc_t rw, uint32_t kb, int c, int n, int c_red, int n_out, bool al16) {
+    if (!FWD && al16) return bload16(rw, n < n_out ? (kb + (uint32_t)n * c_red + c) * 2u : kOOB);
+    uint32_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t idx = FWD ? kb + (uint32_t)(c + e) * n_out + n : kb + (uint32_t)n * c_red + c + e;
+        v[e] = __builtin_amdgcn_raw_buffer_load_b16(rw, n < n_out ? idx * 2u : kOOB, 0, 0);
+    }
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = v[2 * j] | (v[2 * j + 1] << 16);
+    return o;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void k_pack_frag(const u16* __restrict__ w, u16* __restrict__ wf,
                                                    int c_red, int n_out, uint32_t* __restrict__ flag) {
@@ -646,26 +668,18 @@ __global__ __launch_bounds__(256) void k_pack_frag(const u16* __restrict__ w, u1
     const int64_t slot = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (flag && slot == 0) *flag = 0u;  // orphan flag after a backward-input layout
     if (slot >= (int64_t)9 * ncs * nb * 64) return;
+    // slot counts stay below 2^31 (the weight is under 2 GiB): 32-bit index math
     const int lane = (int)(slot & 63);
-    int64_t q = slot >> 6;
-    const int b = (int)(q % nb);
-    q /= nb;
-    const int cs = (int)(q % ncs);
-    const int k = (int)(q / ncs);
+    uint32_t q = (uint32_t)(slot >> 6);
+    const int b = (int)(q % (uint32_t)nb);
+    q /= (uint32_t)nb;
+    const int cs = (int)(q % (uint32_t)ncs);
+    const int k = (int)(q / (uint32_t)ncs);
     const int n = b * 16 + (lane & 15);
     const int c = cs * KS + (lane >> 4) * 8;
-    const u16* wk = w + (int64_t)k * c_red * n_out;
-    u16 v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        u16 x = 0;
-        if (n < n_out) x = MODE == MODE_FWD ? wk[(int64_t)(c + e) * n_out + n] : wk[(int64_t)n * c_red + c + e];
-        v[e] = x;
-    }
-    u32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = (unsigned)v[2 * j] | ((unsigned)v[2 * j + 1] << 16);
-    *(u32x4*)(wf + slot * 8) = o;
+    const rsrc_t rw = make_rsrc(w, 9u * (uint32_t)c_red * (uint32_t)n_out * 2u);
+    *(u32x4*)(wf + slot * 8) = pack_slot<MODE == MODE_FWD>(rw, (uint32_t)k * c_red * n_out, c, n, c_red, n_out,
+                                                          ((uintptr_t)w & 15) == 0);
 }
 
 // Both fragment-ordered layouts in one launch: slots [0, sf) write the
@@ -682,24 +696,19 @@ __global__ __launch_bounds__(256) void k_pack_both(const u16* __restrict__ w, u1
     const int c_red = fwd ? c_in : c_out, n_out = fwd ? c_out : c_in;
     const int ncs = c_red / KS, nb = (n_out + 15) / 16;
     const int lane = (int)(slot & 63);
-    int64_t q = slot >> 6;
-    const int b = (int)(q % nb);
-    q /= nb;
-    const int cs = (int)(q % ncs);
-    const int k = (int)(q / ncs);
+    uint32_t q = (uint32_t)(slot >> 6);  // below 2^31 (host check on the weight size)
+    const int b = (int)(q % (uint32_t)nb);
+    q /= (uint32_t)nb;
+    const int cs = (int)(q % (uint32_t)ncs);
+    const int k = (int)(q / (uint32_t)ncs);
     const int n = b * 16 + (lane & 15);
     const int c = cs * KS + (lane >> 4) * 8;
-    const u16* wk = w + (int64_t)k * c_in * c_out;
-    u16 v[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        u16 x = 0;
-        if (n < n_out) x = fwd ? wk[(int64_t)(c + e) * c_out + n] : wk[(int64_t)n * c_out + c + e];
-        v[e] = x;
-    }
-    u32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = (unsigned)v[2 * j] | ((unsigned)v[2 * j + 1] << 16);
+    const rsrc_t rw = make_rsrc(w, 9u * (uint32_t)c_in * (uint32_t)c_out * 2u);
+    const uint32_t kb = (uint32_t)k * c_in * c_out;
+    const bool al16 = ((uintptr_t)w & 15) == 0;
+    // sf is a multiple of 64: fwd is uniform in a wave
+    const u32x4 o = fwd ? pack_slot<true>(rw, kb, c, n, c_red, n_out, al16)
+                        : pack_slot<false>(rw, kb, c, n, c_red, n_out, al16);
     *(u32x4*)((fwd ? wf_fwd : wf_bwd) + slot * 8) = o;
 }
 
