@@ -304,6 +304,14 @@ extern "C" int svtad_bwd_packed(const void* grad_out, const void* x, const int32
     if (workspace_bytes < p.ws_bytes)
         return set_error(SVTAD_ERR_WORKSPACE, "bwd_packed: workspace smaller than svtad_bwd_w_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;
+    // grad_in and the partials in one launch where neither fills the chip
+    if (p.path == 1 && n > 0) {
+        uint32_t* f = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
+        st = bwd_fused_mfma(dtype, p, grad_out, x, nbr, weight, packed_bwd, f, grad_in, grad_w, grad_bias,
+                            workspace, workspace_bytes, n, c_in, c_out, tokens_per_batch, s);
+        if (st < 0) return st;
+        if (st == 1) return launch_status();
+    }
     // 1. grad_in (keeps the orphan flag after the packed layout)
     const uint32_t* flag = nullptr;
     if (n > 0) {

@@ -21,6 +21,8 @@
 #include <type_traits>
 
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "sv_common.h"
 #include "sv_conv.h"
@@ -247,11 +249,23 @@ constexpr int gg_lds_rows(int CR, int FM, int FN, int WS) {
                      (FM * 16 * (4 * FN * 16 + 8) * 2 + CR * 2 - 1) / (CR * 2)));
 }
 
+template <int CR, int FM, int FN, int WS>
+struct GgWideLds {
+    __align__(16) u16 Ab[gg_lds_rows(CR, FM, FN, WS)][CR];
+    int srow[9][FM * 16];  // gathered source row, -1 if missing
+    int kvalid[9];
+    int klist[10];
+    int nk_s, lo_s, hi_s;
+};
+
+// One tile of the wide gathered GEMM, run by threads [0, 256 * WS) of a
+// workgroup (k_gg_wide, or the backward-input role of k_bwd_fused) in the
+// LDS block L.
 template <typename T, int MODE, int CR, int FM, int FN, int D, int WS>
-__global__ __launch_bounds__(256 * WS) void k_gg_wide(
-    const T* __restrict__ src, const int32_t* __restrict__ nbr, const T* __restrict__ wb,
-    const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n, int n_out,
-    int64_t tpb, int n_col_tiles, int64_t n_tiles, uint32_t* __restrict__ orphan_flag) {
+__device__ __forceinline__ void gg_wide_tile(
+    GgWideLds<CR, FM, FN, WS>& L, int64_t tile, const T* __restrict__ src, const int32_t* __restrict__ nbr,
+    const T* __restrict__ wb, const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n,
+    int n_out, int64_t tpb, int n_col_tiles, uint32_t* __restrict__ orphan_flag) {
     constexpr int BM = FM * 16;
     constexpr int BN = 4 * FN * 16;
     constexpr int NC = CR / KS;
@@ -266,16 +280,18 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     constexpr int LROWS = gg_lds_rows(CR, FM, FN, WS);
     static_assert(NC % D == 0, "ring depth must divide the steps of a slice");
 
-    __shared__ __align__(16) u16 Ab[LROWS][RP];
-    __shared__ int srow[9][BM];  // gathered source row, -1 if missing
-    __shared__ int kvalid[9];
-    __shared__ int klist[10];
-    __shared__ int nk_s, lo_s, hi_s;
+    static_assert(sizeof(L.Ab) == (size_t)LROWS * RP * 2, "LDS rows");
+    auto& Ab = L.Ab;
+    auto& srow = L.srow;
+    auto& kvalid = L.kvalid;
+    auto& klist = L.klist;
+    int& nk_s = L.nk_s;
+    int& lo_s = L.lo_s;
+    int& hi_s = L.hi_s;
 
     const int tid = threadIdx.x;
     const int set = tid >> 8, ltid = tid & 255;
     const int lane = tid & 63, wave = ltid >> 6;
-    const int64_t tile = xcd_tile(blockIdx.x, n_tiles);
     const int64_t row0 = (tile / n_col_tiles) * BM;
     const int col0 = (int)(tile % n_col_tiles) * BN;
     const rsrc_t rs_src = make_rsrc(src, (uint32_t)(n * CR * 2));
@@ -559,7 +575,7 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
         // order); 16-byte rows of 4 columns, the pitch padded by 4 floats so
         // the 16 rows of an instruction fall on different banks
         constexpr int RED = BN + 4;
-        static_assert((size_t)BM * RED * 4 <= sizeof(Ab), "the partial accumulators must fit in LDS");
+        static_assert((size_t)BM * RED * 4 <= sizeof(L.Ab), "the partial accumulators must fit in LDS");
         float* red = (float*)&Ab[0][0];
         for (int h = 1; h < WS; ++h) {
             if (set == h) {
@@ -585,7 +601,7 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     // columns per 8-byte store, then write whole 16-byte chunks so each
     // output row goes out as one run
     constexpr int OP = BN + 8;
-    static_assert((size_t)BM * OP * 2 <= sizeof(Ab), "output tile must fit in LDS");
+    static_assert((size_t)BM * OP * 2 <= sizeof(L.Ab), "output tile must fit in LDS");
     u16* ot = &Ab[0][0];
     // one straight-line copy per bias mode (a mode test per element compiles
     // to a branch per element, which cost more than the rest of the epilogue)
@@ -630,6 +646,16 @@ __global__ __launch_bounds__(256 * WS) void k_gg_wide(
         const int col = col0 + c8 * 8;
         if (i < n && col < n_out) __builtin_nontemporal_store(*(const u32x4*)&ot[r * OP + c8 * 8], (u32x4*)(out + i * n_out + col));
     }
+}
+
+template <typename T, int MODE, int CR, int FM, int FN, int D, int WS>
+__global__ __launch_bounds__(256 * WS) void k_gg_wide(
+    const T* __restrict__ src, const int32_t* __restrict__ nbr, const T* __restrict__ wb,
+    const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n, int n_out,
+    int64_t tpb, int n_col_tiles, int64_t n_tiles, uint32_t* __restrict__ orphan_flag) {
+    __shared__ GgWideLds<CR, FM, FN, WS> lds;
+    gg_wide_tile<T, MODE, CR, FM, FN, D, WS>(lds, xcd_tile(blockIdx.x, n_tiles), src, nbr, wb, bias, bias_mode,
+                                             out, n, n_out, tpb, n_col_tiles, orphan_flag);
 }
 
 // Weight in MFMA fragment order for the gathered GEMMs. For reduction step cs
@@ -1076,11 +1102,26 @@ constexpr int bw_big_threads(int fm, int fn, int wgm, int wgn) {
     return 64 * (wgm * wgn + bw_stage_waves(fm, fn, wgm, wgn));
 }
 
+template <int FM, int FN, int WGM, int WGN>
+struct BwBigLds {
+    static constexpr int NT = bw_big_threads(FM, FN, WGM, WGN);
+    // [buf][channel][row] tiles: the x operand's two buffers, then go's
+    __align__(16) u16 stage[2 * (WGM * FM * 16 + WGN * FN * 16) * KR];
+    // byte offsets of the split's rows in x (gathered) and in go (linear),
+    // kOOB for missing neighbors and for rows past the split; two stages
+    // past the last one so that the prefetch needs no bounds test
+    __align__(16) uint32_t srow[2][kMaxSplitRows + 2 * KR];
+    int wcnt[(kMaxSplitRows + NT - 1) / NT][NT / 64];  // per-wave counts of the row-list compaction
+};
+
+// One work unit (split s, unit u, ci tile, co tile = lin) of the
+// backward-weight partials, run by all bw_big_threads threads of a workgroup
+// (k_bw_big, or the backward-weight role of k_bwd_fused) in the LDS block L.
 template <typename T, int FM, int FN, int WGM, int WGN>
-__global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
-    const T* __restrict__ go, const T* __restrict__ x, const int32_t* __restrict__ nbr,
-    float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int c_in, int c_out,
-    int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks, int n_off,
+__device__ __forceinline__ void bw_big_unit(
+    BwBigLds<FM, FN, WGM, WGN>& L, int64_t lin, const T* __restrict__ go, const T* __restrict__ x,
+    const int32_t* __restrict__ nbr, float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n,
+    int c_in, int c_out, int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int n_off,
     int64_t n_src) {
     constexpr int NT = bw_big_threads(FM, FN, WGM, WGN);
     constexpr int NMW = WGM * WGN;     // matrix waves
@@ -1097,19 +1138,14 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     constexpr int WA = (A_ITEMS + 63) / 64, WB = (B_ITEMS + 63) / 64;
     static_assert(NMW + WA + WB == NT / 64, "wave roles");
 
-    // [buf][channel][row] tiles: the x operand's two buffers, then go's
-    __shared__ __align__(16) u16 stage_lds[2 * (BM + BN) * KR];
+    static_assert(sizeof(L.stage) == (size_t)2 * (BM + BN) * KR * 2, "stage tiles");
+    u16* const stage_lds = L.stage;
     u16(*const As)[BM][KR] = (u16(*)[BM][KR])stage_lds;
     u16(*const Bs)[BN][KR] = (u16(*)[BN][KR])(stage_lds + 2 * BM * KR);
-    // byte offsets of the split's rows in x (gathered) and in go (linear),
-    // kOOB for missing neighbors and for rows past the split; two stages
-    // past the last one so that the prefetch needs no bounds test
-    constexpr int TROWS = kMaxSplitRows + 2 * KR;
-    __shared__ __align__(16) uint32_t srow[2][TROWS];
+    auto& srow = L.srow;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int64_t lin = xcd_tile(blockIdx.x, n_blocks);
     // work units of a split: with the 9 offsets, units 0-3 and 6-9 are the
     // offsets 0-3 and 5-8 over the split's rows, and units 4 and 5 the center
     // offset over the split's first and second half
@@ -1136,7 +1172,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     // per-wave counts of all chunks meet in LDS behind one barrier, and each
     // thread then places its rows after the rows of earlier chunks and waves.
     constexpr int MAXCH = (kMaxSplitRows + NT - 1) / NT;
-    __shared__ int wcnt[MAXCH][NT / 64];
+    auto& wcnt = L.wcnt;
     int rows = rows_raw;
     if (compact) {
         int sv[MAXCH];
@@ -1182,7 +1218,8 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     // The staging waves read the list two stages at a time up to stage
     // steps_even + 1 (steps rounded up to even), so it is filled that far;
     // with rows_per_split <= kMaxSplitRows (checked on the host) that is at
-    // most TROWS entries. A compacted list is only padded.
+    // most kMaxSplitRows + 2 * KR entries (L.srow). A compacted list is only
+    // padded.
     const int steps_even = (steps + 1) & ~1;
     for (int r = (compact ? rows : 0) + tid; r < (steps_even + 2) * KR; r += NT) {
         const bool live = !compact && r < rows;
@@ -1338,6 +1375,46 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
                 if (co0 + col < c_out) ws_bias[((int64_t)s * 2 + (u - 4)) * c_out + co0 + col] = v;
             }
         }
+    }
+}
+
+template <typename T, int FM, int FN, int WGM, int WGN>
+__global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
+    const T* __restrict__ go, const T* __restrict__ x, const int32_t* __restrict__ nbr,
+    float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int c_in, int c_out,
+    int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks, int n_off,
+    int64_t n_src) {
+    __shared__ BwBigLds<FM, FN, WGM, WGN> lds;
+    bw_big_unit<T, FM, FN, WGM, WGN>(lds, xcd_tile(blockIdx.x, n_blocks), go, x, nbr, ws, ws_bias, n, c_in,
+                                     c_out, tpb, rows_per_split, n_ci_tiles, n_co_tiles, n_off, n_src);
+}
+
+// Backward-input and the backward-weight partials in one launch, for shapes
+// where neither grid fills the chip (low keep rates): workgroups [0, n_bw)
+// of the XCD-major order run the backward-weight units (all
+// bw_big_threads threads), the rest the gathered-GEMM tiles of
+// backward-input (threads [0, 256 * GWS); the other waves end at once, and
+// a workgroup barrier waits only for waves that have not ended). The two
+// roles share one LDS block. The host launches it only when the grid fits
+// one workgroup per CU and the tile kernel's registers fit this launch's.
+template <typename T, int CR, int GFM, int GFN, int GD, int GWS, int FM, int FN, int WGM, int WGN>
+__global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bwd_fused(
+    const T* __restrict__ go, const int32_t* __restrict__ nbr, const T* __restrict__ wb, T* __restrict__ gi,
+    int n_in, int n_col_tiles, uint32_t* __restrict__ orphan_flag, const T* __restrict__ x,
+    float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int64_t tpb, int64_t rows_per_split,
+    int n_ci_tiles, int n_co_tiles, int64_t n_bw, int64_t n_blocks) {
+    typedef GgWideLds<CR, GFM, GFN, GWS> GL;
+    typedef BwBigLds<FM, FN, WGM, WGN> BL;
+    static_assert(256 * GWS <= bw_big_threads(FM, FN, WGM, WGN), "tile role threads");
+    __shared__ __align__(16) char lds[sizeof(GL) > sizeof(BL) ? sizeof(GL) : sizeof(BL)];
+    const int64_t lin = xcd_tile(blockIdx.x, n_blocks);
+    if (lin < n_bw) {
+        bw_big_unit<T, FM, FN, WGM, WGN>(*(BL*)lds, lin, go, x, nbr, ws, ws_bias, n, n_in, CR, tpb,
+                                         rows_per_split, n_ci_tiles, n_co_tiles, 9, n);
+    } else {
+        if (threadIdx.x >= 256 * GWS) return;
+        gg_wide_tile<T, MODE_BWDIN, CR, GFM, GFN, GD, GWS>(*(GL*)lds, lin - n_bw, go, nbr, wb, nullptr, 0, gi, n,
+                                                         n_in, tpb, n_col_tiles, orphan_flag);
     }
 }
 
@@ -1696,6 +1773,22 @@ static int bw_dispatch(const BwPlan& p, const void* go, const void* x, const int
     return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_w: no tile configuration for these widths");
 }
 
+// Ordered reduction of the large-tile partials into gw / gb (k_bw_reduce),
+// which also runs the orphan job oj (may be NULL).
+static void bw_big_reduce(int dtype, const BigCfg& bc, int splits, const float* part, const float* part_b,
+                          void* gw, void* gb, int c_in, int c_out, const OrphanJob* oj, hipStream_t s) {
+    const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
+    const int64_t blocks = cdiv((int64_t)9 * c_in * c_out / 4, 64) + (gb ? cdiv(c_out, 256) : 0);
+    const dim3 grid((unsigned)blocks);
+    const OrphanJob job = oj ? *oj : OrphanJob{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
+    if (dtype == SVTAD_F16)
+        hipLaunchKernelGGL((k_bw_reduce<f16>), grid, dim3(256), 0, s, part, gb ? part_b : nullptr, splits, 9,
+                           c_in, c_out, bc.fm, bc.fn, bc.wgm, bc.wgn, nci, nco, (f16*)gw, (f16*)gb, job);
+    else
+        hipLaunchKernelGGL((k_bw_reduce<bf16>), grid, dim3(256), 0, s, part, gb ? part_b : nullptr, splits, 9,
+                           c_in, c_out, bc.fm, bc.fn, bc.wgm, bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb, job);
+}
+
 int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
             void* gw, void* gb, void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb,
             const OrphanJob* oj, bool* oj_taken, hipStream_t s) {
@@ -1712,24 +1805,103 @@ int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int
     if (!gw) return SVTAD_OK;  // partials only
     BigCfg bc;
     if (big_cfg(c_in, c_out, &bc)) {
-        const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
-        const int64_t blocks = cdiv((int64_t)9 * c_in * c_out / 4, 64) + (gb ? cdiv(c_out, 256) : 0);
-        const dim3 grid((unsigned)blocks);
-        const OrphanJob job = oj ? *oj : OrphanJob{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
-        if (dtype == SVTAD_F16)
-            hipLaunchKernelGGL((k_bw_reduce<f16>), grid, dim3(256), 0, s, (const float*)part,
-                               (const float*)part_b, p.splits, 9, c_in, c_out, bc.fm, bc.fn, bc.wgm,
-                               bc.wgn, nci, nco, (f16*)gw, (f16*)gb, job);
-        else
-            hipLaunchKernelGGL((k_bw_reduce<bf16>), grid, dim3(256), 0, s, (const float*)part,
-                               (const float*)part_b, p.splits, 9, c_in, c_out, bc.fm, bc.fn, bc.wgm,
-                               bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb, job);
+        bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, oj, s);
         *oj_taken = oj != nullptr;
         return SVTAD_OK;
     }
     split_reduce(dtype, part, 9LL * c_in * c_out, p.splits, gw, s);
     if (gb) split_reduce(dtype, part_b, (int64_t)c_out, p.splits, gb, s);
     return SVTAD_OK;
+}
+
+// The fused backward's choice: the backward-input tile shape (row fragments
+// gfm, column fragments per wave gfn) and the backward-weight split count.
+// SVTAD_BWD_FUSED in the environment overrides it: "off" never fuses,
+// "<gfm>x<gfn>" or "<gfm>x<gfn>:<splits>" forces a shape (one of 3x1, 3x3,
+// 4x3) for measurements; the launch checks still apply.
+struct FusedChoice { int gfm, gfn, splits; };
+static int fused_env(FusedChoice* c) {  // -1 off, 0 automatic, 1 forced (read on every call)
+    const char* e = getenv("SVTAD_BWD_FUSED");
+    if (!e || !*e) return 0;
+    if (!strcmp(e, "off")) return -1;
+    FusedChoice f{0, 0, 0};
+    if (sscanf(e, "%dx%d:%d", &f.gfm, &f.gfn, &f.splits) < 2) return 0;
+    *c = f;
+    return 1;
+}
+
+template <typename T, int GFM, int GFN>
+static void launch_fused(const void* go, const int32_t* nbr, const void* wb, void* gi, uint32_t* flag,
+                         const void* x, float* part, float* part_b, int64_t n, int64_t tpb, int64_t rps,
+                         int64_t n_gg, int64_t n_bw, hipStream_t s) {
+    constexpr int C = 192;
+    hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, 6, 3, 2, 4>), dim3((unsigned)(n_gg + n_bw)),
+                       dim3(bw_big_threads(6, 3, 2, 4)), 0, s, (const T*)go, nbr, (const T*)wb, (T*)gi, C,
+                       C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, 1, 1, n_bw, n_gg + n_bw);
+}
+
+int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, const int32_t* nbr,
+                   const void* w, const void* packed_bwd, uint32_t* flag, void* gi, void* gw, void* gb,
+                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
+    constexpr int C = 192;
+    if ((dtype != SVTAD_F16 && dtype != SVTAD_BF16) || c_in != C || c_out != C || n <= 0 || p0.path != 1 ||
+        !gg_mfma_packed_ok(dtype, n, c_out, c_in) || !bw_mfma_supported(dtype, n, c_in, c_out) ||
+        !aligned16(go) || !aligned16(x) || !aligned16(packed_bwd) || !aligned16(gi))
+        return 0;
+    FusedChoice ch{0, 0, p0.splits};
+    const int env = fused_env(&ch);
+    if (env < 0) return 0;
+    const int64_t cu = cu_count();
+    auto n_gg = [&](int gfm, int gfn) { return cdiv(n, 16 * gfm) * (C / (64 * gfn)); };
+    if (env == 0) {
+        // the tile shape the backward-input launch would take (pick_fm), or
+        // a full-width tile of three row fragments in place of the 64-column
+        // one; only shapes whose registers fit 128 per wave (FM <= 4)
+        static const int have[] = {1, 2, 3, 4, 5, 6, 8};
+        const int fm = pick_fm(n, 1, have, 7);
+        static const FusedChoice narrow[] = {{3, 1, 0}, {3, 3, 0}};
+        const FusedChoice* cands = fm <= 2 ? narrow : nullptr;
+        FusedChoice wide{fm, 3, 0};
+        const int nc = fm <= 2 ? 2 : (fm <= 4 ? 1 : 0);
+        if (fm > 2) cands = &wide;
+        bool found = false;
+        for (int q = 0; q < nc && !found; ++q)
+            if (n_gg(cands[q].gfm, cands[q].gfn) + 10LL * p0.splits <= cu) {
+                ch = FusedChoice{cands[q].gfm, cands[q].gfn, p0.splits};
+                found = true;
+            }
+        if (!found) return 0;
+    } else {
+        if (ch.splits <= 0) ch.splits = p0.splits;
+        if (!((ch.gfm == 3 && ch.gfn == 1) || (ch.gfm == 3 && ch.gfn == 3) || (ch.gfm == 4 && ch.gfn == 3)))
+            return set_error(SVTAD_ERR_INVALID, "bwd_packed: SVTAD_BWD_FUSED shape is not 3x1, 3x3 or 4x3");
+    }
+    // the split plan for ch.splits: whole 256-row units
+    BwPlan p = p0;
+    p.rows_per_split = cdiv(cdiv(n, (int64_t)ch.splits), 256) * 256;
+    p.splits = (int)cdiv(n, p.rows_per_split);
+    const size_t need = (size_t)p.splits * 10 * c_in * c_out * 4 + (gb ? (size_t)2 * p.splits * c_out * 4 : 0);
+    const int st = check_split_plan("bwd_packed", p, n, need, ws_bytes);
+    if (st) return st;
+    float* part = (float*)ws;
+    float* part_b = gb ? part + (int64_t)p.splits * 10 * c_in * c_out : nullptr;
+    const int64_t gg = n_gg(ch.gfm, ch.gfn), bw = 10LL * p.splits;
+#define SVTAD_FUSED_CASE(FM, FN)                                                                          \
+    if (ch.gfm == FM && ch.gfn == FN) {                                                                   \
+        if (dtype == SVTAD_F16)                                                                           \
+            launch_fused<f16, FM, FN>(go, nbr, packed_bwd, gi, flag, x, part, part_b, n, tpb,            \
+                                      p.rows_per_split, gg, bw, s);                                       \
+        else                                                                                              \
+            launch_fused<bf16, FM, FN>(go, nbr, packed_bwd, gi, flag, x, part, part_b, n, tpb,           \
+                                       p.rows_per_split, gg, bw, s);                                      \
+    }
+    SVTAD_FUSED_CASE(3, 1)
+    SVTAD_FUSED_CASE(3, 3)
+    SVTAD_FUSED_CASE(4, 3)
+#undef SVTAD_FUSED_CASE
+    const OrphanJob job{go, nbr, w, gi, n, c_in, c_out, tpb, flag};
+    bw_big_reduce(dtype, BigCfg{6, 3, 2, 4}, p.splits, part, part_b, gw, gb, c_in, c_out, &job, s);
+    return 1;
 }
 
 // Row-split plan of a linear layer's weight gradient (one offset): splits

@@ -108,6 +108,17 @@ int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int
             void* gw, void* gb, void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb,
             const OrphanJob* oj, bool* oj_taken, hipStream_t s);
 
+// Backward-input and the backward-weight partials in one launch, then the
+// ordered reduction (with the flag-gated orphan pass of flag, the word after
+// packed_bwd), at C_in = C_out = 192 in f16 / bf16 when both grids together
+// fit one workgroup per CU (low keep rates). p0 is plan_bw's plan (its
+// split count, or fewer). Returns 1 when launched, 0 when the shape does not
+// qualify (nothing launched), or an SVTAD_ERR_* (message set, nothing
+// launched).
+int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, const int32_t* nbr,
+                   const void* w, const void* packed_bwd, uint32_t* flag, void* gi, void* gw, void* gb,
+                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s);
+
 // A linear layer's weight gradient out[ci][co] = sum_i g[rows[i]][ci] x[i][co]
 // (rows NULL: row i of g), i < n, on the backward-weight partial kernel with
 // one offset and its ordered reduction. path 0 in the plan: no large-tile

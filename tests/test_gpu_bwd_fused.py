@@ -1,0 +1,139 @@
+"""The one-launch backward (backward-input tiles and backward-weight partials
+in one grid, then the ordered reduction) at the full c2 shape, C = 192.
+
+svtad_bwd_packed takes it where both grids together fit one workgroup per
+CU (10 % and 25 % keep at c2); SVTAD_BWD_FUSED=off turns it off and
+"<gfm>x<gfn>[:<splits>]" forces a tile shape and split count. Checked:
+
+* automatic choice and a forced 64-column tile against the two-launch path:
+  bit-identical (same row tiles, same offsets per wave set, same splits);
+* a forced four-row-fragment tile and a forced smaller split count: within
+  one rounding of the two-launch path, and every result against the fp64
+  oracle at the north-star bar;
+* an asymmetric table (orphan entries: the flag set inside the launch, the
+  orphan pass in the reduction) against the oracle;
+* a forced shape outside the instantiated ones is rejected before any launch.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from tests.helpers import kaiming_weight, topk_mask
+from tests.test_gpu_fullsize import _gw_fp64, _sub_bwd_in
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2  # max-scaled error bar of the north star (f16 / bf16)
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _problem(dev, oracle, keep, dname, seed, drop=0.0):
+    import torch
+
+    import eccv26_tad_amd as sv
+
+    dt = {"float16": torch.float16, "bfloat16": torch.bfloat16}[dname]
+    rng = np.random.default_rng(seed)
+    mask = topk_mask(rng, 2, 80, 14, 14, keep)
+    t = oracle.build_table(mask)
+    if drop > 0:  # one side of some symmetric pairs removed: orphan entries
+        off = (t >= 0) & (rng.random(t.shape) < drop)
+        off[:, 4] = False
+        t = np.where(off, -1, t).astype(np.int32)
+    n, c = t.shape[0], 192
+
+    def rounded(a):
+        return torch.from_numpy(a).to(dt).float().numpy()
+
+    x = rounded(rng.standard_normal((n, c)).astype(np.float32))
+    w = rounded(kaiming_weight(rng, c, c))
+    go = rounded(rng.standard_normal((n, c)).astype(np.float32))
+    X, W, G = (torch.from_numpy(a).to(dev, dt) for a in (x, w, go))
+    T = torch.from_numpy(t).to(dev)
+    return sv.ops, dict(x=x, w=w, go=go, t=t, X=X, W=W, G=G, T=T, n=n, c=c, rng=rng)
+
+
+def _bwd(ops, P, monkeypatch, mode):
+    import torch
+
+    if mode is None:
+        monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
+    else:
+        monkeypatch.setenv("SVTAD_BWD_FUSED", mode)
+    _, pb = ops.pack_weight(P["W"], False, True)
+    gi, gw, gb = ops.bwd_packed(P["G"], P["X"], P["T"], P["W"], pb, P["c"], 0, True)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
+    return [a.float().cpu().numpy() for a in (gi, gw, gb)]
+
+
+def _oracle_errs(oracle, P, res):
+    gi, gw, gb = res
+    rows = np.sort(P["rng"].choice(P["n"], size=min(2048, P["n"]), replace=False))
+    return {
+        "grad_x": oracle.rel_err(gi[rows], _sub_bwd_in(oracle, P["go"], P["t"], P["w"], rows)),
+        "grad_w": oracle.rel_err(gw, _gw_fp64(P["go"], P["x"], P["t"])),
+        "grad_b": oracle.rel_err(gb, P["go"].astype(np.float64).sum(0)),
+    }
+
+
+def _scaled(a, b):
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("keep,dname", [(0.10, "float16"), (0.25, "float16"), (0.10, "bfloat16")])
+def test_fused_matches_two_launch(dev, oracle, monkeypatch, keep, dname):
+    ops, P = _problem(dev, oracle, keep, dname, 3100 + int(keep * 100))
+    _say(f"fused backward, keep {keep} {dname}, n = {P['n']}")
+    ref = _bwd(ops, P, monkeypatch, "off")
+    for mode in (None, "3x1", "3x3"):
+        got = _bwd(ops, P, monkeypatch, mode)
+        for name, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref):
+            assert np.array_equal(a, b), (mode, name, _scaled(a, b))
+    _say("  automatic, 3x1, 3x3: bit-identical to the two-launch path")
+    for mode in ("4x3", "3x3:4"):
+        got = _bwd(ops, P, monkeypatch, mode)
+        d = {k: _scaled(a, b) for k, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref)}
+        e = _oracle_errs(oracle, P, got)
+        _say(f"  {mode}: vs two-launch", {k: f"{v:.2e}" for k, v in d.items()},
+             "vs oracle", {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
+        for k, v in d.items():
+            assert v <= 4e-3, (mode, k, v)
+        for k, v in e.items():
+            assert v <= TOL, (mode, k, v)
+    e = _oracle_errs(oracle, P, ref)
+    _say("  two-launch vs oracle", {k: f"{v:.2e}" for k, v in e.items()})
+    for k, v in e.items():
+        assert v <= TOL, (k, v)
+
+
+def test_fused_orphans(dev, oracle, monkeypatch):
+    """An asymmetric table at 10 % keep: the orphan entries reach grad_x
+    through the flag set in the one-launch backward."""
+    ops, P = _problem(dev, oracle, 0.10, "float16", 3300, drop=0.2)
+    _say(f"fused backward, asymmetric table, n = {P['n']}")
+    ref = _bwd(ops, P, monkeypatch, "off")
+    for mode in (None, "3x1"):
+        got = _bwd(ops, P, monkeypatch, mode)
+        e = _oracle_errs(oracle, P, got)
+        d = _scaled(got[0], ref[0])
+        _say(f"  {mode}: grad_x vs two-launch {d:.2e}, vs oracle",
+             {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
+        assert d <= 4e-3, (mode, d)
+        assert np.array_equal(got[1], ref[1]) and np.array_equal(got[2], ref[2]), mode
+        for k, v in e.items():
+            assert v <= TOL, (mode, k, v)
+
+
+def test_fused_bad_forced_shape(dev, oracle, monkeypatch):
+    ops, P = _problem(dev, oracle, 0.10, "float16", 3400)
+    with pytest.raises(RuntimeError, match="SVTAD_BWD_FUSED"):
+        _bwd(ops, P, monkeypatch, "5x3")
