@@ -1864,12 +1864,22 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
         FusedChoice wide{fm, 3, 0};
         const int nc = fm <= 2 ? 2 : (fm <= 4 ? 1 : 0);
         if (fm > 2) cands = &wide;
+        // The split count drops below the plan's (at most to half of it) so
+        // that the grid fits: the tile role takes as long as the longer
+        // splits, and fewer partials shorten the reduction. Measured at c2
+        // (step medians): 10 % keep 41.0 us two-launch, 36.8 fused with
+        // full-width tiles and 7 splits, 32.5 with 64-column tiles and 5;
+        // 40 % keep 62.3 two-launch, 53.4 fused with 6 splits (55.1 with 5,
+        // 61.1 with 4). A grid over one round (c2 at 55 %) was slower.
         bool found = false;
-        for (int q = 0; q < nc && !found; ++q)
-            if (n_gg(cands[q].gfm, cands[q].gfn) + 10LL * p0.splits <= cu) {
-                ch = FusedChoice{cands[q].gfm, cands[q].gfn, p0.splits};
+        for (int q = 0; q < nc && !found; ++q) {
+            const int64_t room = (cu - n_gg(cands[q].gfm, cands[q].gfn)) / 10;
+            const int64_t sp = std::min<int64_t>(p0.splits, room);
+            if (sp >= 1 && 2 * sp >= p0.splits) {
+                ch = FusedChoice{cands[q].gfm, cands[q].gfn, (int)sp};
                 found = true;
             }
+        }
         if (!found) return 0;
     } else {
         if (ch.splits <= 0) ch.splits = p0.splits;
