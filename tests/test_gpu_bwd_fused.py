@@ -37,7 +37,7 @@ def _say(*a):
     sys.stdout.flush()
 
 
-def _problem(dev, oracle, keep, dname, seed, drop=0.0):
+def _problem(dev, oracle, keep, dname, seed, drop=0.0, per_sample=False):
     import torch
 
     import eccv26_tad_amd as sv
@@ -51,6 +51,11 @@ def _problem(dev, oracle, keep, dname, seed, drop=0.0):
         off[:, 4] = False
         t = np.where(off, -1, t).astype(np.int32)
     n, c = t.shape[0], 192
+    tab, tpb = t, 0
+    if per_sample:  # per-sample indices (tokens_per_batch): equal kept counts per sample
+        tpb = n // 2
+        tab = t.copy()
+        tab[tab >= 0] %= tpb
 
     def rounded(a):
         return torch.from_numpy(a).to(dt).float().numpy()
@@ -59,8 +64,8 @@ def _problem(dev, oracle, keep, dname, seed, drop=0.0):
     w = rounded(kaiming_weight(rng, c, c))
     go = rounded(rng.standard_normal((n, c)).astype(np.float32))
     X, W, G = (torch.from_numpy(a).to(dev, dt) for a in (x, w, go))
-    T = torch.from_numpy(t).to(dev)
-    return sv.ops, dict(x=x, w=w, go=go, t=t, X=X, W=W, G=G, T=T, n=n, c=c, rng=rng)
+    T = torch.from_numpy(tab).to(dev)
+    return sv.ops, dict(x=x, w=w, go=go, t=t, X=X, W=W, G=G, T=T, n=n, c=c, rng=rng, tpb=tpb)
 
 
 def _bwd(ops, P, monkeypatch, mode):
@@ -71,7 +76,7 @@ def _bwd(ops, P, monkeypatch, mode):
     else:
         monkeypatch.setenv("SVTAD_BWD_FUSED", mode)
     _, pb = ops.pack_weight(P["W"], False, True)
-    gi, gw, gb = ops.bwd_packed(P["G"], P["X"], P["T"], P["W"], pb, P["c"], 0, True)
+    gi, gw, gb = ops.bwd_packed(P["G"], P["X"], P["T"], P["W"], pb, P["c"], P["tpb"], True)
     torch.cuda.synchronize()
     monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
     return [a.float().cpu().numpy() for a in (gi, gw, gb)]
@@ -122,6 +127,24 @@ def test_fused_matches_two_launch(dev, oracle, monkeypatch, keep, dname, same, o
             assert v <= TOL, (mode, k, v)
     e = _oracle_errs(oracle, P, ref)
     _say("  two-launch vs oracle", {k: f"{v:.2e}" for k, v in e.items()})
+    for k, v in e.items():
+        assert v <= TOL, (k, v)
+
+
+@pytest.mark.parametrize("keep", [0.10, 0.25])
+def test_fused_per_sample_table(dev, oracle, monkeypatch, keep):
+    """Per-sample neighbor indices (tokens_per_batch = n / B): the one-launch
+    backward equals the two-launch path bit for bit with the same tile and
+    splits, and the oracle (on the global form of the same table)."""
+    ops, P = _problem(dev, oracle, keep, "float16", 3500 + int(keep * 100), per_sample=True)
+    _say(f"fused backward, per-sample table, keep {keep}, n = {P['n']}, tpb = {P['tpb']}")
+    ref = _bwd(ops, P, monkeypatch, "off")
+    got = _bwd(ops, P, monkeypatch, "3x1")
+    for name, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref):
+        assert np.array_equal(a, b), (name, _scaled(a, b))
+    got = _bwd(ops, P, monkeypatch, None)
+    e = _oracle_errs(oracle, P, got)
+    _say("  automatic vs oracle", {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
     for k, v in e.items():
         assert v <= TOL, (k, v)
 
