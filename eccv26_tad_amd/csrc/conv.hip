@@ -261,6 +261,20 @@ extern "C" size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, in
     return plan_bw(n, c_in, c_out, dtype).ws_bytes;
 }
 
+extern "C" int svtad_bwd_fused_plan(int64_t n, int c_in, int c_out, int dtype, int* tile_row_frags,
+                                    int* tile_col_frags, int* splits) {
+    if (!tile_row_frags || !tile_col_frags || !splits)
+        return set_error(SVTAD_ERR_INVALID, "bwd_fused_plan: null pointer");
+    *tile_row_frags = *tile_col_frags = *splits = 0;
+    const int st = check_common("bwd_fused_plan", n, c_in, c_out, 0, dtype);
+    if (st) return st;
+    BwPlan p;
+    const int r = bwd_fused_plan(dtype, plan_bw(n, c_in, c_out, dtype), n, c_in, c_out, tile_row_frags,
+                                 tile_col_frags, &p);
+    if (r == 1) *splits = p.splits;
+    return r;
+}
+
 extern "C" int svtad_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,
                            void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n,
                            int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream) {

@@ -1840,19 +1840,17 @@ static void launch_fused(const void* go, const int32_t* nbr, const void* wb, voi
                        C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, 1, 1, n_bw, n_gg + n_bw);
 }
 
-int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, const int32_t* nbr,
-                   const void* w, const void* packed_bwd, uint32_t* flag, void* gi, void* gw, void* gb,
-                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
+int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, int* gfm, int* gfn,
+                   BwPlan* p_out) {
     constexpr int C = 192;
     if ((dtype != SVTAD_F16 && dtype != SVTAD_BF16) || c_in != C || c_out != C || n <= 0 || p0.path != 1 ||
-        !gg_mfma_packed_ok(dtype, n, c_out, c_in) || !bw_mfma_supported(dtype, n, c_in, c_out) ||
-        !aligned16(go) || !aligned16(x) || !aligned16(packed_bwd) || !aligned16(gi))
+        !gg_mfma_packed_ok(dtype, n, c_out, c_in) || !bw_mfma_supported(dtype, n, c_in, c_out))
         return 0;
     FusedChoice ch{0, 0, p0.splits};
     const int env = fused_env(&ch);
     if (env < 0) return 0;
     const int64_t cu = cu_count();
-    auto n_gg = [&](int gfm, int gfn) { return cdiv(n, 16 * gfm) * (C / (64 * gfn)); };
+    auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (C / (64 * fn)); };
     if (env == 0) {
         // the tile shape the backward-input launch would take (pick_fm), or
         // a full-width tile of three row fragments in place of the 64-column
@@ -1890,9 +1888,24 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     BwPlan p = p0;
     p.rows_per_split = cdiv(cdiv(n, (int64_t)ch.splits), 256) * 256;
     p.splits = (int)cdiv(n, p.rows_per_split);
+    *gfm = ch.gfm;
+    *gfn = ch.gfn;
+    *p_out = p;
+    return 1;
+}
+
+int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, const int32_t* nbr,
+                   const void* w, const void* packed_bwd, uint32_t* flag, void* gi, void* gw, void* gb,
+                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
+    if (!aligned16(go) || !aligned16(x) || !aligned16(packed_bwd) || !aligned16(gi)) return 0;
+    FusedChoice ch{0, 0, 0};
+    BwPlan p;
+    const int fp = bwd_fused_plan(dtype, p0, n, c_in, c_out, &ch.gfm, &ch.gfn, &p);
+    if (fp != 1) return fp;
     const size_t need = (size_t)p.splits * 10 * c_in * c_out * 4 + (gb ? (size_t)2 * p.splits * c_out * 4 : 0);
     const int st = check_split_plan("bwd_packed", p, n, need, ws_bytes);
     if (st) return st;
+    auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (192 / (64 * fn)); };
     float* part = (float*)ws;
     float* part_b = gb ? part + (int64_t)p.splits * 10 * c_in * c_out : nullptr;
     const int64_t gg = n_gg(ch.gfm, ch.gfn), bw = 10LL * p.splits;

@@ -115,6 +115,12 @@ int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int
 // split count, or fewer). Returns 1 when launched, 0 when the shape does not
 // qualify (nothing launched), or an SVTAD_ERR_* (message set, nothing
 // launched).
+// The one-launch backward's plan for a shape (host only): 1 with the
+// backward-input tile shape (gfm row fragments, gfn column fragments per
+// wave) and the split plan, 0 when the shape keeps two launches, or an
+// SVTAD_ERR_* for a bad SVTAD_BWD_FUSED override (message set).
+int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, int* gfm, int* gfn,
+                   BwPlan* p_out);
 int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, const int32_t* nbr,
                    const void* w, const void* packed_bwd, uint32_t* flag, void* gi, void* gw, void* gb,
                    void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s);

@@ -343,3 +343,46 @@ def test_legacy_weight_remap():
     out = remap_legacy_sparse_conv_weights(sd, model)
     assert out["blk.sparse_conv.weight"].shape == (9, 8, 4)
     assert torch.equal(out["blk.sparse_conv.weight"][2, 5], legacy[5, 2])
+
+
+def _fused_plan(lib, n, ci, co, dt):
+    a, b, s = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    st = lib.svtad_bwd_fused_plan(I64(n), ci, co, dt, ctypes.byref(a), ctypes.byref(b), ctypes.byref(s))
+    return st, (a.value, b.value, s.value)
+
+
+def test_bwd_fused_plan_at_config_2(lib, monkeypatch):
+    """The one-launch backward's choice at config 2 (C = 192 fp16, 256 CUs
+    assumed on a host without a GPU): the backward-input tiles and the
+    backward-weight units fit one workgroup per CU at 10-40 % keep, with at
+    least half the plan's row splits; 55 % keep and above keep two launches.
+    Shapes outside C = 192 f16 / bf16 never fuse."""
+    monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
+    want = {3136: (1, (3, 1, 5)), 7840: (1, (3, 3, 8)), 12544: (1, (4, 3, 6)),
+            17248: (0, (0, 0, 0)), 21952: (0, (0, 0, 0)), 31360: (0, (0, 0, 0))}
+    for n, w in want.items():
+        st, got = _fused_plan(lib, n, 192, 192, 1)
+        assert (st, got) == w, (n, st, got)
+        for tr, tc, sp in [got] if st == 1 else []:
+            tiles = -(-n // (16 * tr)) * (192 // (64 * tc))
+            assert tiles + 10 * sp <= 256  # one workgroup per CU
+    assert _fused_plan(lib, 3136, 192, 192, 2)[0] == 1  # bf16
+    assert _fused_plan(lib, 3136, 192, 192, 0)[0] == 0  # f32: VALU kernels
+    assert _fused_plan(lib, 4916, 256, 256, 2)[0] == 0  # config 4
+    assert _fused_plan(lib, 3136, 192, 128, 1)[0] == 0
+
+
+def test_bwd_fused_plan_override(lib, monkeypatch):
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "off")
+    assert _fused_plan(lib, 3136, 192, 192, 1) == (0, (0, 0, 0))
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "3x3:4")
+    st, (tr, tc, sp) = _fused_plan(lib, 3136, 192, 192, 1)
+    assert (st, tr, tc, sp) == (1, 3, 3, 4)
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "4x3")  # the plan's split count (7 at 3136 rows)
+    assert _fused_plan(lib, 3136, 192, 192, 1) == (1, (4, 3, 7))
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "5x3")
+    st, _ = _fused_plan(lib, 3136, 192, 192, 1)
+    assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
+    monkeypatch.delenv("SVTAD_BWD_FUSED")
+    st, _ = _fused_plan(lib, -1, 192, 192, 1)
+    assert st == -1
