@@ -1830,20 +1830,29 @@ static int fused_env(FusedChoice* c) {  // -1 off, 0 automatic, 1 forced (read o
     return 1;
 }
 
-template <typename T, int GFM, int GFN>
+// C_in = C_out = C: backward-input tiles of GFM row fragments and GFN column
+// fragments per wave, backward-weight units on the large-tile configuration
+// (BFM, BFN, BWM, BWN) of that width.
+template <typename T, int C, int GFM, int GFN, int BFM, int BFN, int BWM, int BWN>
 static void launch_fused(const void* go, const int32_t* nbr, const void* wb, void* gi, uint32_t* flag,
                          const void* x, float* part, float* part_b, int64_t n, int64_t tpb, int64_t rps,
                          int64_t n_gg, int64_t n_bw, hipStream_t s) {
-    constexpr int C = 192;
-    hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, 6, 3, 2, 4>), dim3((unsigned)(n_gg + n_bw)),
-                       dim3(bw_big_threads(6, 3, 2, 4)), 0, s, (const T*)go, nbr, (const T*)wb, (T*)gi, C,
-                       C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, 1, 1, n_bw, n_gg + n_bw);
+    constexpr int NCI = C / (16 * BWM * BFM), NCO = C / (16 * BWN * BFN);
+    static_assert(NCI * 16 * BWM * BFM == C && NCO * 16 * BWN * BFN == C, "whole tiles");
+    hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, BFM, BFN, BWM, BWN>), dim3((unsigned)(n_gg + n_bw)),
+                       dim3(bw_big_threads(BFM, BFN, BWM, BWN)), 0, s, (const T*)go, nbr, (const T*)wb, (T*)gi, C,
+                       C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, NCI, NCO, n_bw, n_gg + n_bw);
 }
+
+// Units per split of the one-launch backward's large-tile configuration at
+// width c (10 work units per ci x co tile): c = 192 takes one 192 x 192 tile,
+// c = 256 two 128 x 256 tiles.
+static int fused_units(int c) { return c == 192 ? 10 : (c == 256 ? 20 : 0); }
 
 int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, int* gfm, int* gfn,
                    BwPlan* p_out) {
-    constexpr int C = 192;
-    if ((dtype != SVTAD_F16 && dtype != SVTAD_BF16) || c_in != C || c_out != C || n <= 0 || p0.path != 1 ||
+    const int C = c_in, U = fused_units(C);
+    if ((dtype != SVTAD_F16 && dtype != SVTAD_BF16) || c_in != c_out || U == 0 || n <= 0 || p0.path != 1 ||
         !gg_mfma_packed_ok(dtype, n, c_out, c_in) || !bw_mfma_supported(dtype, n, c_in, c_out))
         return 0;
     FusedChoice ch{0, 0, p0.splits};
@@ -1852,28 +1861,34 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
     const int64_t cu = cu_count();
     auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (C / (64 * fn)); };
     if (env == 0) {
-        // the tile shape the backward-input launch would take (pick_fm), or
-        // a full-width tile of three row fragments in place of the 64-column
-        // one; only shapes whose registers fit 128 per wave (FM <= 4)
+        // C = 192: the tile shape the backward-input launch would take
+        // (pick_fm), or a full-width tile of three row fragments in place of
+        // the 64-column one; only shapes whose registers fit 128 per wave
+        // (FM <= 4). C = 256: the 128-column tiles of three row fragments
+        // that the backward-input launch takes for few rows (its full-width
+        // tiles need more registers).
         static const int have[] = {1, 2, 3, 4, 5, 6, 8};
-        const int fm = pick_fm(n, 1, have, 7);
+        const int fm = pick_fm(n, 1, have, C == 256 ? 6 : 7);
         static const FusedChoice narrow[] = {{3, 1, 0}, {3, 3, 0}};
-        const FusedChoice* cands = fm <= 2 ? narrow : nullptr;
+        static const FusedChoice narrow256[] = {{3, 2, 0}};
         FusedChoice wide{fm, 3, 0};
-        const int nc = fm <= 2 ? 2 : (fm <= 4 ? 1 : 0);
-        if (fm > 2) cands = &wide;
-        // The split count drops below the plan's (at most to half of it) so
-        // that the grid fits: the tile role takes as long as the longer
-        // splits, and fewer partials shorten the reduction. Measured at c2
-        // (step medians): 10 % keep 41.0 us two-launch, 36.8 fused with
-        // full-width tiles and 7 splits, 32.5 with 64-column tiles and 5;
-        // 40 % keep 62.3 two-launch, 53.4 fused with 6 splits (55.1 with 5,
-        // 61.1 with 4). A grid over one round (c2 at 55 %) was slower.
+        const FusedChoice* cands = C == 256 ? narrow256 : (fm <= 2 ? narrow : &wide);
+        const int nc = C == 256 ? (fm <= 2 ? 1 : 0) : (fm <= 2 ? 2 : (fm <= 4 ? 1 : 0));
+        // The split count drops below the plan's (at most to half of it,
+        // rounded down) so that the grid fits: the tile role takes as long
+        // as the longer splits, and fewer partials shorten the reduction.
+        // Measured (step medians): c2 10 % keep 41.0 us two-launch, 36.8
+        // fused with full-width tiles and 7 splits, 32.5 with 64-column tiles
+        // and 5; c2 40 % keep 62.3 two-launch, 53.4 fused with 6 splits (55.1
+        // with 5, 61.1 with 4); c4 10 % keep (C = 256) 55.4 two-launch, 49.9
+        // fused with 2 splits (50.2 with 3, 50.4 with 4, 52.4 with the plan's
+        // 5 over more than one round). A grid over one round at c2 55 % was
+        // slower.
         bool found = false;
         for (int q = 0; q < nc && !found; ++q) {
-            const int64_t room = (cu - n_gg(cands[q].gfm, cands[q].gfn)) / 10;
+            const int64_t room = (cu - n_gg(cands[q].gfm, cands[q].gfn)) / U;
             const int64_t sp = std::min<int64_t>(p0.splits, room);
-            if (sp >= 1 && 2 * sp >= p0.splits) {
+            if (sp >= 1 && 2 * sp + 1 >= p0.splits) {
                 ch = FusedChoice{cands[q].gfm, cands[q].gfn, (int)sp};
                 found = true;
             }
@@ -1881,8 +1896,12 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         if (!found) return 0;
     } else {
         if (ch.splits <= 0) ch.splits = p0.splits;
-        if (!((ch.gfm == 3 && ch.gfn == 1) || (ch.gfm == 3 && ch.gfn == 3) || (ch.gfm == 4 && ch.gfn == 3)))
-            return set_error(SVTAD_ERR_INVALID, "bwd_packed: SVTAD_BWD_FUSED shape is not 3x1, 3x3 or 4x3");
+        const bool ok192 = C == 192 && ((ch.gfm == 3 && ch.gfn == 1) || (ch.gfm == 3 && ch.gfn == 3) ||
+                                        (ch.gfm == 4 && ch.gfn == 3));
+        const bool ok256 = C == 256 && ch.gfm == 3 && ch.gfn == 2;
+        if (!ok192 && !ok256)
+            return set_error(SVTAD_ERR_INVALID,
+                             "bwd_packed: SVTAD_BWD_FUSED shape is not 3x1, 3x3 or 4x3 (C = 192) or 3x2 (C = 256)");
     }
     // the split plan for ch.splits: whole 256-row units
     BwPlan p = p0;
@@ -1905,25 +1924,28 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     const size_t need = (size_t)p.splits * 10 * c_in * c_out * 4 + (gb ? (size_t)2 * p.splits * c_out * 4 : 0);
     const int st = check_split_plan("bwd_packed", p, n, need, ws_bytes);
     if (st) return st;
-    auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (192 / (64 * fn)); };
+    auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (c_in / (64 * fn)); };
     float* part = (float*)ws;
     float* part_b = gb ? part + (int64_t)p.splits * 10 * c_in * c_out : nullptr;
-    const int64_t gg = n_gg(ch.gfm, ch.gfn), bw = 10LL * p.splits;
-#define SVTAD_FUSED_CASE(FM, FN)                                                                          \
-    if (ch.gfm == FM && ch.gfn == FN) {                                                                   \
+    const int64_t gg = n_gg(ch.gfm, ch.gfn), bw = (int64_t)fused_units(c_in) * p.splits;
+#define SVTAD_FUSED_CASE(C, FM, FN, BFM, BFN, BWM, BWN)                                                   \
+    if (c_in == C && ch.gfm == FM && ch.gfn == FN) {                                                      \
         if (dtype == SVTAD_F16)                                                                           \
-            launch_fused<f16, FM, FN>(go, nbr, packed_bwd, gi, flag, x, part, part_b, n, tpb,            \
-                                      p.rows_per_split, gg, bw, s);                                       \
+            launch_fused<f16, C, FM, FN, BFM, BFN, BWM, BWN>(go, nbr, packed_bwd, gi, flag, x, part,     \
+                                                             part_b, n, tpb, p.rows_per_split, gg, bw, s); \
         else                                                                                              \
-            launch_fused<bf16, FM, FN>(go, nbr, packed_bwd, gi, flag, x, part, part_b, n, tpb,           \
-                                       p.rows_per_split, gg, bw, s);                                      \
+            launch_fused<bf16, C, FM, FN, BFM, BFN, BWM, BWN>(go, nbr, packed_bwd, gi, flag, x, part,    \
+                                                              part_b, n, tpb, p.rows_per_split, gg, bw, s); \
     }
-    SVTAD_FUSED_CASE(3, 1)
-    SVTAD_FUSED_CASE(3, 3)
-    SVTAD_FUSED_CASE(4, 3)
+    SVTAD_FUSED_CASE(192, 3, 1, 6, 3, 2, 4)
+    SVTAD_FUSED_CASE(192, 3, 3, 6, 3, 2, 4)
+    SVTAD_FUSED_CASE(192, 4, 3, 6, 3, 2, 4)
+    SVTAD_FUSED_CASE(256, 3, 2, 4, 4, 2, 4)
 #undef SVTAD_FUSED_CASE
     const OrphanJob job{go, nbr, w, gi, n, c_in, c_out, tpb, flag};
-    bw_big_reduce(dtype, BigCfg{6, 3, 2, 4}, p.splits, part, part_b, gw, gb, c_in, c_out, &job, s);
+    BigCfg bc;
+    big_cfg(c_in, c_out, &bc);  // the configuration launch_fused used (6,3,2,4 / 4,4,2,4)
+    bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, &job, s);
     return 1;
 }
 

@@ -110,8 +110,8 @@ int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int
 
 // Backward-input and the backward-weight partials in one launch, then the
 // ordered reduction (with the flag-gated orphan pass of flag, the word after
-// packed_bwd), at C_in = C_out = 192 in f16 / bf16 when both grids together
-// fit one workgroup per CU (low keep rates). p0 is plan_bw's plan (its
+// packed_bwd), at C_in = C_out = 192 or 256 in f16 / bf16 when both grids
+// together fit one workgroup per CU (low keep rates). p0 is plan_bw's plan (its
 // split count, or fewer). Returns 1 when launched, 0 when the shape does not
 // qualify (nothing launched), or an SVTAD_ERR_* (message set, nothing
 // launched).

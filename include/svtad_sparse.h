@@ -165,14 +165,15 @@ int svtad_bwd_packed(const void* grad_out, const void* x, const int32_t* nbr, co
                      int64_t tokens_per_batch, int dtype, void* stream);
 
 /*
- * Where neither backward grid fills the GPU (C_in = C_out = 192, f16 / bf16,
- * low keep rates), svtad_bwd_packed runs backward-input and the
+ * Where neither backward grid fills the GPU (C_in = C_out = 192 or 256, f16 /
+ * bf16, low keep rates), svtad_bwd_packed runs backward-input and the
  * backward-weight partials in one launch. This host-only query (no GPU work)
  * returns 1 when it would, with the backward-input tile shape (row fragments
  * of 16 rows, column fragments of 16 per wave) and the row-split count; 0
  * when the shape keeps two launches; SVTAD_ERR_INVALID for bad sizes or a bad
  * SVTAD_BWD_FUSED override ("off", "<rows>x<cols>[:<splits>]" with the shape
- * one of 3x1, 3x3, 4x3; read from the environment on every call). It
+ * one of 3x1, 3x3, 4x3 at C = 192 or 3x2 at C = 256; read from the
+ * environment on every call). It
  * describes how svtad_bwd_packed replaces the reference's two backward calls
  * (sparse_conv_layer.py:101-117); the reference has no such query.
  */

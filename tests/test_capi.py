@@ -356,7 +356,7 @@ def test_bwd_fused_plan_at_config_2(lib, monkeypatch):
     assumed on a host without a GPU): the backward-input tiles and the
     backward-weight units fit one workgroup per CU at 10-40 % keep, with at
     least half the plan's row splits; 55 % keep and above keep two launches.
-    Shapes outside C = 192 f16 / bf16 never fuse."""
+    Other widths than 192 and 256, and f32, never fuse."""
     monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
     want = {3136: (1, (3, 1, 5)), 7840: (1, (3, 3, 8)), 12544: (1, (4, 3, 6)),
             17248: (0, (0, 0, 0)), 21952: (0, (0, 0, 0)), 31360: (0, (0, 0, 0))}
@@ -368,7 +368,12 @@ def test_bwd_fused_plan_at_config_2(lib, monkeypatch):
             assert tiles + 10 * sp <= 256  # one workgroup per CU
     assert _fused_plan(lib, 3136, 192, 192, 2)[0] == 1  # bf16
     assert _fused_plan(lib, 3136, 192, 192, 0)[0] == 0  # f32: VALU kernels
-    assert _fused_plan(lib, 4916, 256, 256, 2)[0] == 0  # config 4
+    # config 4 (C = 256 bf16): 128-column tiles of three row fragments and 2
+    # splits at 10 % keep; two launches at 25 % and 55 %
+    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 2))
+    assert _fused_plan(lib, 12288, 256, 256, 2)[0] == 0
+    assert _fused_plan(lib, 27034, 256, 256, 2)[0] == 0
+    assert _fused_plan(lib, 4916, 512, 512, 2)[0] == 0  # no one-launch configuration at C = 512
     assert _fused_plan(lib, 3136, 192, 128, 1)[0] == 0
 
 
@@ -383,6 +388,9 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     monkeypatch.setenv("SVTAD_BWD_FUSED", "5x3")
     st, _ = _fused_plan(lib, 3136, 192, 192, 1)
     assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "3x2")  # the C = 256 shape
+    assert _fused_plan(lib, 3136, 192, 192, 1)[0] == -1
+    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 5))  # the plan's 5 splits
     monkeypatch.delenv("SVTAD_BWD_FUSED")
     st, _ = _fused_plan(lib, -1, 192, 192, 1)
     assert st == -1

@@ -1,8 +1,10 @@
 """The one-launch backward (backward-input tiles and backward-weight partials
-in one grid, then the ordered reduction) at the full c2 shape, C = 192.
+in one grid, then the ordered reduction) at the full c2 shape, C = 192, and
+at config 4's, C = 256.
 
 svtad_bwd_packed takes it where both grids together fit one workgroup per
-CU (10 %, 25 % and 40 % keep at c2, with fewer row splits where needed);
+CU (10 %, 25 % and 40 % keep at c2, 10 % at c4, with fewer row splits where
+needed);
 SVTAD_BWD_FUSED=off turns it off and "<gfm>x<gfn>[:<splits>]" forces a tile
 shape and split count. Checked:
 
@@ -37,20 +39,22 @@ def _say(*a):
     sys.stdout.flush()
 
 
-def _problem(dev, oracle, keep, dname, seed, drop=0.0, per_sample=False):
+def _problem(dev, oracle, keep, dname, seed, drop=0.0, per_sample=False, c=192, grid=(2, 80, 14, 14)):
+    """Config 2's grid and width by default; config 4 is c=256, grid
+    (2, 96, 16, 16)."""
     import torch
 
     import eccv26_tad_amd as sv
 
     dt = {"float16": torch.float16, "bfloat16": torch.bfloat16}[dname]
     rng = np.random.default_rng(seed)
-    mask = topk_mask(rng, 2, 80, 14, 14, keep)
+    mask = topk_mask(rng, *grid, keep)
     t = oracle.build_table(mask)
     if drop > 0:  # one side of some symmetric pairs removed: orphan entries
         off = (t >= 0) & (rng.random(t.shape) < drop)
         off[:, 4] = False
         t = np.where(off, -1, t).astype(np.int32)
-    n, c = t.shape[0], 192
+    n = t.shape[0]
     tab, tpb = t, 0
     if per_sample:  # per-sample indices (tokens_per_batch): equal kept counts per sample
         tpb = n // 2
@@ -147,6 +151,29 @@ def test_fused_per_sample_table(dev, oracle, monkeypatch, keep):
     _say("  automatic vs oracle", {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
     for k, v in e.items():
         assert v <= TOL, (k, v)
+
+
+def test_fused_config4(dev, oracle, monkeypatch):
+    """Config 4 at 10 % keep (C = 256 bf16, N = 4916): 128-column tiles of
+    three row fragments beside 128 x 256 backward-weight units. With the
+    plan's 5 splits the results equal the two launches bit for bit; the
+    automatic choice takes 2 splits."""
+    ops, P = _problem(dev, oracle, 0.10, "bfloat16", 3600, c=256, grid=(2, 96, 16, 16))
+    _say(f"fused backward, config 4, n = {P['n']}")
+    ref = _bwd(ops, P, monkeypatch, "off")
+    got = _bwd(ops, P, monkeypatch, "3x2")
+    for name, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref):
+        assert np.array_equal(a, b), (name, _scaled(a, b))
+    for mode in (None, "3x2:3"):
+        got = _bwd(ops, P, monkeypatch, mode)
+        d = {k: _scaled(a, b) for k, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref)}
+        e = _oracle_errs(oracle, P, got)
+        _say(f"  {mode or 'automatic'}: vs two-launch", {k: f"{v:.2e}" for k, v in d.items()},
+             "vs oracle", {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
+        for k, v in d.items():
+            assert v <= 4e-3, (mode, k, v)
+        for k, v in e.items():
+            assert v <= TOL, (mode, k, v)
 
 
 def test_fused_orphans(dev, oracle, monkeypatch):
