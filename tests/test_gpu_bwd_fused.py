@@ -197,6 +197,21 @@ def test_fused_orphans(dev, oracle, monkeypatch):
             assert v <= TOL, (mode, k, v)
 
 
+def test_fused_without_bias(dev, oracle, monkeypatch):
+    """with_bias=False (no bias partials, no bias reduction): the same input
+    and weight gradients as with the bias, bit for bit, and no bias output."""
+    import torch
+
+    ops, P = _problem(dev, oracle, 0.10, "float16", 3700)
+    monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
+    _, pb = ops.pack_weight(P["W"], False, True)
+    gi, gw, gb = ops.bwd_packed(P["G"], P["X"], P["T"], P["W"], pb, P["c"], 0, True)
+    gi2, gw2, gb2 = ops.bwd_packed(P["G"], P["X"], P["T"], P["W"], pb, P["c"], 0, False)
+    torch.cuda.synchronize()
+    assert gb2.numel() == 0 and gb.numel() == P["c"]
+    assert torch.equal(gi, gi2) and torch.equal(gw, gw2)
+
+
 def test_fused_bad_forced_shape(dev, oracle, monkeypatch):
     ops, P = _problem(dev, oracle, 0.10, "float16", 3400)
     with pytest.raises(RuntimeError, match="SVTAD_BWD_FUSED"):
