@@ -1820,12 +1820,13 @@ int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int
 // "<gfm>x<gfn>" or "<gfm>x<gfn>:<splits>" forces a shape (one of 3x1, 3x3,
 // 4x3) for measurements; the launch checks still apply.
 struct FusedChoice { int gfm, gfn, splits; };
-static int fused_env(FusedChoice* c) {  // -1 off, 0 automatic, 1 forced (read on every call)
+// -1 off, 0 automatic, 1 forced, -2 unreadable (read on every call)
+static int fused_env(FusedChoice* c) {
     const char* e = getenv("SVTAD_BWD_FUSED");
     if (!e || !*e) return 0;
     if (!strcmp(e, "off")) return -1;
     FusedChoice f{0, 0, 0};
-    if (sscanf(e, "%dx%d:%d", &f.gfm, &f.gfn, &f.splits) < 2) return 0;
+    if (sscanf(e, "%dx%d:%d", &f.gfm, &f.gfn, &f.splits) < 2) return -2;
     *c = f;
     return 1;
 }
@@ -1857,6 +1858,8 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         return 0;
     FusedChoice ch{0, 0, p0.splits};
     const int env = fused_env(&ch);
+    if (env == -2)
+        return set_error(SVTAD_ERR_INVALID, "bwd_packed: SVTAD_BWD_FUSED is neither off nor <rows>x<cols>[:<splits>]");
     if (env < 0) return 0;
     const int64_t cu = cu_count();
     auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (C / (64 * fn)); };

@@ -388,6 +388,9 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     monkeypatch.setenv("SVTAD_BWD_FUSED", "5x3")
     st, _ = _fused_plan(lib, 3136, 192, 192, 1)
     assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "fused")  # unreadable
+    st, _ = _fused_plan(lib, 3136, 192, 192, 1)
+    assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x2")  # the C = 256 shape
     assert _fused_plan(lib, 3136, 192, 192, 1)[0] == -1
     assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 5))  # the plan's 5 splits
