@@ -40,6 +40,7 @@ def _setup(dev, dt, B, T, H, W, keep, embed, mlp_ratio, S, seed, **variant):
     idx = torch.from_numpy(np.stack([np.flatnonzero(flat[b]) for b in range(B)])).to(dev)
     table = sv.build_neighbor_table(torch.from_numpy(mask).to(dev)).view(B, -1, 9)
     g = torch.Generator().manual_seed(seed)
+    torch.manual_seed(seed)  # the module's own initialisation draws from the global generator
     mod = sv.SparseConvAdapter(embed, mlp_ratio, **variant)
     with torch.no_grad():
         # non-trivial values where the init leaves zeros or ones (up_proj,
