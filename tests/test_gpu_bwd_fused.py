@@ -212,6 +212,43 @@ def test_fused_without_bias(dev, oracle, monkeypatch):
     assert torch.equal(gi, gi2) and torch.equal(gw, gw2)
 
 
+def test_fused_step_in_hip_graph(dev, oracle, monkeypatch):
+    """The training step at 10 % keep (pack, forward, one-launch backward,
+    reduction) captured in a HIP graph: every replay, with eager work and
+    synchronisations between them, equals the eager step bit for bit."""
+    import torch
+
+    ops, P = _problem(dev, oracle, 0.10, "float16", 3800)
+    monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
+    c = P["c"]
+    b = torch.linspace(-0.1, 0.1, c, device=dev).half()
+
+    def step():
+        pf, pb = ops.pack_weight(P["W"], True, True)
+        y = ops.fwd_packed(P["X"], P["T"], P["W"], pf, b, 0, 1)
+        gi, gw, gb = ops.bwd_packed(P["G"], P["X"], P["T"], P["W"], pb, c, 0, True)
+        return y, gi, gw, gb
+
+    ref = [a.clone() for a in step()]
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = step()
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for a, e in zip(out, ref):
+            assert torch.equal(a, e), r
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+    _say("  three graph replays equal the eager step")
+
+
 def test_fused_bad_forced_shape(dev, oracle, monkeypatch):
     ops, P = _problem(dev, oracle, 0.10, "float16", 3400)
     with pytest.raises(RuntimeError, match="SVTAD_BWD_FUSED"):
