@@ -168,7 +168,9 @@ int svtad_bwd_packed(const void* grad_out, const void* x, const int32_t* nbr, co
  * Where neither backward grid fills the GPU (C_in = C_out = 192 or 256, f16 /
  * bf16, low keep rates), svtad_bwd_packed runs backward-input and the
  * backward-weight partials in one launch. This host-only query (no GPU work)
- * returns 1 when it would, with the backward-input tile shape (row fragments
+ * returns 1 when it would (given 16-byte aligned grad_out, x, packed_bwd and
+ * grad_in, which svtad_bwd_packed also needs for it), with the
+ * backward-input tile shape (row fragments
  * of 16 rows, column fragments of 16 per wave) and the row-split count; 0
  * when the shape keeps two launches; SVTAD_ERR_INVALID for bad sizes or a bad
  * SVTAD_BWD_FUSED override ("off", "<rows>x<cols>[:<splits>]" with the shape
