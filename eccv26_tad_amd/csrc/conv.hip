@@ -61,10 +61,12 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
     if (p.path) {
         // Fewest workgroup rounds times the longest unit, with a fixed cost
         // per workgroup worth about 256 rows, plus (large-tile kernel) the
-        // partial tiles' write and read-back, worth about 5 rows per
-        // workgroup over the whole grid (measured: at c2 this picks 7 splits
-        // at 10 % keep and 14 at 55 %, 3.4 and 4 µs faster per step than the
-        // 13 and 23 without it): splits of whole multiples of gran rows, at
+        // partial tiles' write and read-back, worth about 3 rows per
+        // workgroup over the whole grid. At c2 this picks 7 splits at 10 %
+        // keep and 17 at 55 %; without the partial term it picked 13 and 23,
+        // 3.4 and 4 µs slower per step. A weight of 5 rows picked 14 at
+        // 55 %, 15 at 70 % and 18 at 100 %: the backward ran 0.2-1.5 µs
+        // slower than with 17, 22 and 25. Splits are whole multiples of gran rows, at
         // most kMaxSplitRows (the LDS row list), at least 256 rows where n
         // allows. A partial second round costs a full round, so a count just
         // above the CU count loses to twice as many half-length splits.
@@ -76,7 +78,7 @@ static BwPlan plan_bw(int64_t n, int c_in, int c_out, int dtype) {
         for (int64_t sc = s_min; sc <= s_cap; ++sc) {
             const int64_t r = cdiv(cdiv(std::max<int64_t>(n, 1), sc), gran) * gran;
             const int64_t se = std::max<int64_t>(1, cdiv(n, r));
-            const int64_t cost = cdiv(se * tiles, cu) * ((big ? r / 2 : r) + 256) + (big ? 5 * se * tiles : 0);
+            const int64_t cost = cdiv(se * tiles, cu) * ((big ? r / 2 : r) + 256) + (big ? 3 * se * tiles : 0);
             if (cost < best) {
                 best = cost;
                 splits = se;

@@ -1877,9 +1877,9 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         FusedChoice wide{fm, 3, 0};
         const FusedChoice* cands = C == 256 ? narrow256 : (fm <= 2 ? narrow : &wide);
         const int nc = C == 256 ? (fm <= 2 ? 1 : 0) : (fm <= 2 ? 2 : (fm <= 4 ? 1 : 0));
-        // The split count drops below the plan's (at most to half of it,
-        // rounded down) so that the grid fits: the tile role takes as long
-        // as the longer splits, and fewer partials shorten the reduction.
+        // The split count drops below the plan's so that the grid fits, while
+        // splits stay within 2560 rows: the tile role takes as long as the
+        // longer splits, and fewer partials shorten the reduction.
         // Measured (step medians): c2 10 % keep 41.0 us two-launch, 36.8
         // fused with full-width tiles and 7 splits, 32.5 with 64-column tiles
         // and 5; c2 40 % keep 62.3 two-launch, 53.4 fused with 6 splits (55.1
@@ -1891,7 +1891,7 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         for (int q = 0; q < nc && !found; ++q) {
             const int64_t room = (cu - n_gg(cands[q].gfm, cands[q].gfn)) / U;
             const int64_t sp = std::min<int64_t>(p0.splits, room);
-            if (sp >= 1 && 2 * sp + 1 >= p0.splits) {
+            if (sp >= 1 && sp * 2560 >= n) {
                 ch = FusedChoice{cands[q].gfm, cands[q].gfn, (int)sp};
                 found = true;
             }

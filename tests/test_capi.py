@@ -354,8 +354,8 @@ def _fused_plan(lib, n, ci, co, dt):
 def test_bwd_fused_plan_at_config_2(lib, monkeypatch):
     """The one-launch backward's choice at config 2 (C = 192 fp16, 256 CUs
     assumed on a host without a GPU): the backward-input tiles and the
-    backward-weight units fit one workgroup per CU at 10-40 % keep, with at
-    least half the plan's row splits; 55 % keep and above keep two launches.
+    backward-weight units fit one workgroup per CU at 10-40 % keep, with
+    splits of at most 2560 rows; 55 % keep and above keep two launches.
     Other widths than 192 and 256, and f32, never fuse."""
     monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
     want = {3136: (1, (3, 1, 5)), 7840: (1, (3, 3, 8)), 12544: (1, (4, 3, 6)),
@@ -393,7 +393,7 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x2")  # the C = 256 shape
     assert _fused_plan(lib, 3136, 192, 192, 1)[0] == -1
-    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 5))  # the plan's 5 splits
+    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 7))  # the plan's 7 splits
     monkeypatch.delenv("SVTAD_BWD_FUSED")
     st, _ = _fused_plan(lib, -1, 192, 192, 1)
     assert st == -1

@@ -156,7 +156,7 @@ def test_fused_per_sample_table(dev, oracle, monkeypatch, keep):
 def test_fused_config4(dev, oracle, monkeypatch):
     """Config 4 at 10 % keep (C = 256 bf16, N = 4916): 128-column tiles of
     three row fragments beside 128 x 256 backward-weight units. With the
-    plan's 5 splits the results equal the two launches bit for bit; the
+    plan's split count the results equal the two launches bit for bit; the
     automatic choice takes 2 splits."""
     ops, P = _problem(dev, oracle, 0.10, "bfloat16", 3600, c=256, grid=(2, 96, 16, 16))
     _say(f"fused backward, config 4, n = {P['n']}")
