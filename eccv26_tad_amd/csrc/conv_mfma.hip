@@ -1898,7 +1898,14 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         }
         if (!found) return 0;
     } else {
+        // a forced split count is clamped to what the launch accepts: at most
+        // the plan's count (the workspace is sized for it), and enough splits
+        // that none exceeds the LDS row list (kMaxSplitRows)
+        const int64_t lo = cdiv(n, (int64_t)kMaxSplitRows);
+        if (lo > p0.splits)
+            return set_error(SVTAD_ERR_INVALID, "bwd_packed: SVTAD_BWD_FUSED has no split count the workspace holds");
         if (ch.splits <= 0) ch.splits = p0.splits;
+        ch.splits = (int)std::min<int64_t>(std::max<int64_t>(ch.splits, lo), p0.splits);
         const bool ok192 = C == 192 && ((ch.gfm == 3 && ch.gfn == 1) || (ch.gfm == 3 && ch.gfn == 3) ||
                                         (ch.gfm == 4 && ch.gfn == 3));
         const bool ok256 = C == 256 && ch.gfm == 3 && ch.gfn == 2;
@@ -1931,8 +1938,10 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     float* part = (float*)ws;
     float* part_b = gb ? part + (int64_t)p.splits * 10 * c_in * c_out : nullptr;
     const int64_t gg = n_gg(ch.gfm, ch.gfn), bw = (int64_t)fused_units(c_in) * p.splits;
+    bool launched = false;
 #define SVTAD_FUSED_CASE(C, FM, FN, BFM, BFN, BWM, BWN)                                                   \
     if (c_in == C && ch.gfm == FM && ch.gfn == FN) {                                                      \
+        launched = true;                                                                                  \
         if (dtype == SVTAD_F16)                                                                           \
             launch_fused<f16, C, FM, FN, BFM, BFN, BWM, BWN>(go, nbr, packed_bwd, gi, flag, x, part,     \
                                                              part_b, n, tpb, p.rows_per_split, gg, bw, s); \
@@ -1945,6 +1954,9 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     SVTAD_FUSED_CASE(192, 4, 3, 6, 3, 2, 4)
     SVTAD_FUSED_CASE(256, 3, 2, 4, 4, 2, 4)
 #undef SVTAD_FUSED_CASE
+    // a plan without an instantiation leaves the partials unwritten: no
+    // reduction of them, the caller runs the two launches instead
+    if (!launched) return 0;
     const OrphanJob job{go, nbr, w, gi, n, c_in, c_out, tpb, flag};
     BigCfg bc;
     big_cfg(c_in, c_out, &bc);  // the configuration launch_fused used (6,3,2,4 / 4,4,2,4)
@@ -1974,7 +1986,7 @@ BwPlan plan_wgrad(int64_t n, int c_in, int c_out) {
 template <typename T, int FM, int FN, int WGM, int WGN>
 static int launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
                         float* part, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out,
-                        hipStream_t s) {
+                        bool out_f32, hipStream_t s) {
     constexpr int BM = WGM * FM * 16, BN = WGN * FN * 16;
     if (c_in % BM != 0 || c_out % BN != 0)
         return set_error(SVTAD_ERR_INVALID, "linear_wgrad: widths are not whole tiles");
@@ -1989,21 +2001,26 @@ static int launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, con
                        blocks, 1, n_src);
     const dim3 grid((unsigned)cdiv((int64_t)c_in * c_out / 4, 64));
     const OrphanJob none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
-    hipLaunchKernelGGL((k_bw_reduce<T>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
-                       p.splits, 1, c_in, c_out, FM, FN, WGM, WGN, nci, nco, (T*)out, (T*)nullptr, none);
+    if (out_f32)
+        hipLaunchKernelGGL((k_bw_reduce<float>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
+                           p.splits, 1, c_in, c_out, FM, FN, WGM, WGN, nci, nco, (float*)out, (float*)nullptr, none);
+    else
+        hipLaunchKernelGGL((k_bw_reduce<T>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
+                           p.splits, 1, c_in, c_out, FM, FN, WGM, WGN, nci, nco, (T*)out, (T*)nullptr, none);
     return SVTAD_OK;
 }
 
 int wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
-               void* ws, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s) {
+               void* ws, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out, bool out_f32,
+               hipStream_t s) {
     BigCfg bc;
     if (!p.path || !big_cfg(c_in, c_out, &bc))
         return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: no tile configuration for these widths");
 #define SVTAD_WG_CASE(M, N, WM, WN)                                                                           \
     if (bc.fm == M && bc.fn == N && bc.wgm == WM && bc.wgn == WN)                                             \
         return dtype == SVTAD_F16                                                                             \
-                   ? launch_wgrad<f16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, ws_bytes, n, n_src, c_in, c_out, s) \
-                   : launch_wgrad<bf16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, ws_bytes, n, n_src, c_in, c_out, s);
+                   ? launch_wgrad<f16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, ws_bytes, n, n_src, c_in, c_out, out_f32, s) \
+                   : launch_wgrad<bf16, M, N, WM, WN>(p, g, rows, x, out, (float*)ws, ws_bytes, n, n_src, c_in, c_out, out_f32, s);
     SVTAD_WG_CASE(6, 3, 2, 4)
     SVTAD_WG_CASE(4, 4, 2, 4)
     SVTAD_WG_CASE(4, 2, 2, 4)

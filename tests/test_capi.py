@@ -394,6 +394,13 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x2")  # the C = 256 shape
     assert _fused_plan(lib, 3136, 192, 192, 1)[0] == -1
     assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 7))  # the plan's 7 splits
+    # forced split counts are clamped to what the launch accepts: no more than
+    # the plan's (the workspace holds that many), no split above 4096 rows
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "3x3:1000")
+    assert _fused_plan(lib, 3136, 192, 192, 1) == (1, (3, 3, 7))
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "3x1:1")
+    st, (tr, tc, sp) = _fused_plan(lib, 12544, 192, 192, 1)
+    assert st == 1 and (tr, tc) == (3, 1) and sp == 4  # 3328 rows each
     monkeypatch.delenv("SVTAD_BWD_FUSED")
     st, _ = _fused_plan(lib, -1, 192, 192, 1)
     assert st == -1

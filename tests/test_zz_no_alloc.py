@@ -92,3 +92,37 @@ def test_fwd_noalloc_rejects_weights_beyond_the_array(dev):
     buf = ctypes.create_string_buffer(64)
     st = lib.svtad_fwd_noalloc(buf, buf, buf, None, 0, buf, I64(16), 512, 1024, I64(0), F16, None)
     assert st == -3 and b"static workspace" in lib.svtad_last_error()
+
+
+def test_fwd_noalloc_replays_in_a_hip_graph(dev):
+    """The allocation-free forward captured in a HIP graph (torch.cuda.graph),
+    after one eager call on the device (the first call per device looks up the
+    array's device address, which stays outside the capture): three replays,
+    with other GPU work and synchronisations between them, each equal to the
+    eager svtad_fwd bit for bit."""
+    import torch
+
+    lib = _lib()
+    print("fwd_noalloc under graph capture: c2 at 25 % keep, C=192 fp16", flush=True)
+    table, x, w, b = _case(dev, 7003, 0.25, 2, 80, 14, 14, 192, torch.float16)
+    a, ref = _run_both(lib, dev, table, x, w, b, F16)  # the eager call (and the reference)
+    assert torch.equal(a, ref)
+    n, c = x.shape
+    out = torch.full((n, c), float("nan"), device=dev, dtype=x.dtype)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    graph = torch.cuda.CUDAGraph()
+    status = []
+    with torch.cuda.graph(graph):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        status.append(lib.svtad_fwd_noalloc(ptr(x), ptr(table), ptr(w), ptr(b), BIAS_FP32, ptr(out), I64(n), c, c,
+                                            I64(0), F16, stream))
+    assert status == [0], lib.svtad_last_error()
+    for r in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {r}"
+        # other work on the array's device between replays
+        junk = torch.randn(512, 512, device=dev) @ torch.randn(512, 512, device=dev)
+        torch.cuda.synchronize()
+        del junk
