@@ -203,25 +203,32 @@ def dense_adapter_ms(prob, dev, dtype, reps):
     return time_events(run, reps, warm=5)
 
 
-def adapter_measure(dev, reps):
+def adapter_measure(dev, reps, amp=False, use_attn=0):
     """SparseConvAdapter (fused GEMM epilogues, no host sync) against the
     unfused chain of the reference adapter (vit_sparse_adapter_poguise.py:
-    305-362,652-653, with the .max() heuristic) at the ViT-B adapter shape:
+    305-362,511-653, with the .max() heuristic) at the ViT-B adapter shape:
     B2 x (1 CLS + kept tokens of T80 x 14x14 at 55 % keep) x 768, hidden 256
-    (the reference rounds 768 / 4 up to a power of two), float16. Forward
-    alone and forward + backward (input and all parameter gradients)."""
+    (the reference rounds 768 / 4 up to a power of two). Forward alone and
+    forward + backward (input and all parameter gradients). Precision: a
+    float16 module and input, or with ``amp`` the reference's training mode,
+    float32 parameters and input under torch.autocast(bfloat16)
+    (opentad/cores/train_engine.py:672), where both paths cast to bfloat16
+    and return float32. ``use_attn`` 2 is the vitsparse configs' variant
+    (visual tokens attend to the key tokens; one key token here)."""
+    import contextlib
+
     import torch
 
     import eccv26_tad_amd as sv
 
-    dtype = torch.float16
+    dtype = torch.float32 if amp else torch.float16
     mask = make_mask(0.55).to(dev)
     table = sv.build_neighbor_table(mask)
     n_kept = table.shape[0] // B
     table = table.view(B, n_kept, 9)
     idx = torch.nonzero(mask.view(B, -1))[:, 1].view(B, n_kept)
     g = torch.Generator().manual_seed(SEED + 5)
-    mod = sv.SparseConvAdapter(768, 0.25)
+    mod = sv.SparseConvAdapter(768, 0.25, use_attn=use_attn, n_key_tokens=1)
     with torch.no_grad():
         mod.up_proj.weight.copy_(torch.randn(mod.up_proj.weight.shape, generator=g) * 0.02)
     mod = mod.to(dev, dtype)
@@ -229,29 +236,49 @@ def adapter_measure(dev, reps):
     go = torch.randn(B, 1 + n_kept, 768, generator=g).to(dev, dtype)
     params = [x] + list(mod.parameters())
     args = (H, W, idx, T * H * W, table)
+    ctx = (lambda: torch.autocast("cuda", dtype=torch.bfloat16)) if amp else contextlib.nullcontext
+    with ctx():
+        if mod._fused_dtype(x) is None:
+            raise RuntimeError("adapter bench: the fused path would not run")
 
     def fwd_fused():
-        with torch.no_grad():
+        with torch.no_grad(), ctx():
             return mod(x, *args)
 
     def fwd_unfused():
-        with torch.no_grad():
+        with torch.no_grad(), ctx():
             return mod.reference_forward(x, *args)
 
     def step_fused():
-        return torch.autograd.grad(mod(x, *args), params, go)
+        with ctx():
+            y = mod(x, *args)
+        return torch.autograd.grad(y, params, go)
 
     def step_unfused():
-        return torch.autograd.grad(mod.reference_forward(x, *args), params, go)
+        with ctx():
+            y = mod.reference_forward(x, *args)
+        return torch.autograd.grad(y, params, go)
 
     t = {name: time_events(fn, reps, warm=5) for name, fn in
          (("fwd", fwd_fused), ("fwd_unfused", fwd_unfused), ("step", step_fused), ("step_unfused", step_unfused))}
-    out = {"workload": f"x [{B}, 1+{n_kept}, 768] fp16, hidden {mod.hidden_dims}, keep 0.55"}
+    prec = "fp32 params and input under autocast(bf16)" if amp else "fp16"
+    out = {"workload": f"x [{B}, 1+{n_kept}, 768] {prec}, hidden {mod.hidden_dims}, use_attn {use_attn}, "
+                       f"keep 0.55"}
     for k, v in t.items():
         out[k + "_us"] = round(v * 1e3, 2)
     out["fwd_speedup"] = round(t["fwd_unfused"] / t["fwd"], 3)
     out["step_speedup"] = round(t["step_unfused"] / t["step"], 3)
     return out
+
+
+def adapter_rows(dev, reps):
+    """The adapter rows of the bench: a float16 module, and the reference's
+    training mode (float32 parameters under autocast(bfloat16)), both
+    without attention. (With use_attn 2 and one key token both paths spend
+    about 2 x 11 ms of host time per step before two of PyTorch's bfloat16
+    batched products of the attention branch, which hides the adapter.)"""
+    return {"fp16": adapter_measure(dev, reps),
+            "autocast_bf16": adapter_measure(dev, reps, amp=True)}
 
 
 def blob_mask(keep: float, seed: int = SEED + 1):
@@ -563,7 +590,7 @@ def main():
         print(json.dumps({"copy_calibration_bytes": nbytes, "launches": 5}), flush=True)
         return
     if args.only == "adapter":
-        print(json.dumps({"adapter": adapter_measure(dev, args.steps)}), flush=True)
+        print(json.dumps({"adapter": adapter_rows(dev, args.steps)}), flush=True)
         return
     if args.only == "prune":
         print(json.dumps({"prune_step": prune_measure(dev, args.steps, False)}), flush=True)
@@ -704,7 +731,7 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     prune = None if args.no_sweep else prune_measure(dev, 20, not args.no_cpu)
-    adapter = None if args.no_sweep else adapter_measure(dev, 20)
+    adapter = None if args.no_sweep else adapter_rows(dev, 20)
     depthwise = None if args.no_sweep else depthwise_measure(dev, 20)
     large = None if args.no_sweep else large_channel_measure(dev, 10)
     if adapter is not None:

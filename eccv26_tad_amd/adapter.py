@@ -62,13 +62,28 @@ The input gradient is one GEMM with the residual's term as its addend
 ``AdapterDownFunction`` and ``AdapterUpFunction`` are the same kernels as two
 separate nodes around a ``SparseConv2d``.
 
-The fused path takes float16 / bfloat16 GPU tensors with parameters of the
-same dtype, outside autocast. Any other call (float32 input, autocast with
-float32 parameters as in the reference's training loop, CPU tensors, no
-kept tokens) runs ``reference_forward``: the unfused chain in the
-reference's op order, whose SparseConv2d applies the reference's autocast
-casts, so the output dtype is the reference's (float32 under autocast with
-a float32 ``gamma``).
+The fused path runs in a compute dtype ``cd`` of float16 / bfloat16:
+
+* outside autocast, the dtype of x when x and every parameter share it;
+* under ``torch.autocast("cuda")`` with a float16 / bfloat16 target, the
+  autocast dtype, with x and the parameters in it or in float32. This is how
+  the reference runs the adapter: its training and test loops wrap the model
+  in ``torch.cuda.amp.autocast(dtype=torch.bfloat16)`` with float32
+  parameters (``opentad/cores/train_engine.py:672``,
+  ``opentad/cores/test_engine.py:63``, ``amp=True`` in the vitsparse
+  configs). The nodes cast x and the weights to ``cd`` as autocast casts
+  them for ``nn.Linear`` and SparseConv2d (``sparse_conv_layer.py:191-202``).
+  ``gamma`` stays float32, so ``up_proj(c) * gamma`` promotes to float32 as
+  in the reference: the up GEMM's epilogue multiplies the rounded ``z`` by the
+  float32 gamma and adds the residual in float32, and the output is float32.
+  The heatmap injection adds ``sampled * gate`` in float32 with one rounding
+  to ``cd`` (SparseConv2d's cast of its float32 input there). Gradients reach
+  the parameters in their own dtype; the gradient of a float32 gain is summed
+  in fp32 and stored as float32.
+
+Any other call (float32 input and parameters without autocast, a CPU tensor,
+mixed dtypes outside autocast, no kept tokens) runs ``reference_forward``:
+the unfused chain in the reference's op order.
 """
 from __future__ import annotations
 
@@ -85,6 +100,11 @@ from .sparse_conv_layer import (BIAS_AFTER, BIAS_FP32, BIAS_NONE, IMPLICIT_GEMM_
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
 
 
+def _cast(t, dtype):
+    """``t`` in ``dtype`` (None stays None): autocast's cast of an operand."""
+    return t if t is None or t.dtype == dtype else t.to(dtype)
+
+
 def _colsum(a):
     """Column sums of a [rows, n] matrix (the Linear bias gradients): fp32
     accumulation over row splits added in a fixed order, result in a's
@@ -98,14 +118,32 @@ def _NO_ROWS(like):
     return torch.empty(0, dtype=torch.int32, device=like.device)
 
 
-def _wgrad(g, rows, x):
+def _wgrad(g, rows, x, f32=False):
     """A Linear layer's weight gradient ``g[rows]^T x`` (``rows`` empty: the
     first ``len(x)`` rows of g) on the split-row kernel; widths that are not
-    multiples of 64 (no tile configuration there) take a library GEMM."""
+    multiples of 64 (no tile configuration there) take a library GEMM. With
+    ``f32`` the fp32 sums come back unrounded."""
     if g.shape[1] % 64 == 0 and x.shape[1] % 64 == 0:
-        return _ops.linear_wgrad(g, rows, x)
+        return _ops.linear_wgrad(g, rows, x, f32)
     gr = g.index_select(0, rows) if rows.numel() else g[: x.shape[0]]
+    if f32:
+        return torch.matmul(gr.t().float(), x.float())
     return torch.matmul(gr.t(), x)
+
+
+def _up_wgrad(go, B, N, S, a_sp, a_pa):
+    """``G = go^T cat(a_special, a_patch)`` of the up projection in fp32,
+    unrounded (rounded once later, after the gamma scale, as the reference
+    rounds the gradient of ``(c W^T + b) * gamma`` once): the patch rows on
+    the split-row kernel (rows of go picked by a row list), the few special
+    rows as a small fp32 product."""
+    n = go.shape[-1]
+    go2 = go.reshape(-1, n)
+    if S == 0:
+        return _wgrad(go2, _NO_ROWS(go2), a_pa, True)
+    k = a_pa.shape[-1]
+    G = _wgrad(go2, _patch_rows(B, N, S, go.device), a_pa, True)
+    return G.add_(torch.matmul(go[:, :S].reshape(-1, n).t().float(), a_sp.reshape(-1, k).float()))
 
 
 _PATCH_ROWS = {}
@@ -128,68 +166,81 @@ def _patch_rows(B, N, S, device):
 
 
 class AdapterDownFunction(Function):
-    """``(act_special, act_patch) = split(GELU(x W^T + b))``; x ``[B, N, k]``."""
+    """``(act_special, act_patch) = split(GELU(x W^T + b))``; x ``[B, N, k]``.
+    ``cd`` (default: x's dtype) is the compute dtype that x, the weight and
+    the bias are cast to (autocast's casts)."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, n_special):
-        pre, sp, pa = _ops.adapter_down(x, weight, bias, int(n_special))
-        ctx.save_for_backward(x, weight, pre)
-        ctx.has_bias = bias is not None
+    def forward(ctx, x, weight, bias, n_special, cd=None):
+        cd = x.dtype if cd is None else cd
+        xc, wc, bc = _cast(x, cd), _cast(weight, cd), _cast(bias, cd)
+        pre, sp, pa = _ops.adapter_down(xc, wc, bc, int(n_special))
+        ctx.save_for_backward(xc, wc, pre)
+        ctx.dtypes = (x.dtype, weight.dtype, None if bias is None else bias.dtype)
         ctx.n_special = int(n_special)
         return sp, pa
 
     @staticmethod
     def backward(ctx, g_sp, g_pa):
-        x, weight, pre = ctx.saved_tensors
+        xc, wc, pre = ctx.saved_tensors
+        x_dt, w_dt, b_dt = ctx.dtypes
         n = pre.shape[-1]
+        cd = pre.dtype
         # GELU backward straight from the two gradient buffers (no assembled dg)
-        du = _ops.gelu_backward_split(g_sp, g_pa, pre, ctx.n_special)
+        du = _ops.gelu_backward_split(_cast(g_sp, cd), _cast(g_pa, cd), pre, ctx.n_special)
         du2 = du.reshape(-1, n)
-        gx = torch.matmul(du, weight) if ctx.needs_input_grad[0] else None
-        gw = _wgrad(du2, _NO_ROWS(du2), x.reshape(-1, x.shape[-1])) if ctx.needs_input_grad[1] else None
-        gb = _colsum(du2) if ctx.has_bias and ctx.needs_input_grad[2] else None
-        return gx, gw, gb, None
+        gx = torch.matmul(du, wc).to(x_dt) if ctx.needs_input_grad[0] else None
+        gw = _wgrad(du2, _NO_ROWS(du2), xc.reshape(-1, xc.shape[-1])).to(w_dt) if ctx.needs_input_grad[1] else None
+        gb = _colsum(du2).to(b_dt) if b_dt is not None and ctx.needs_input_grad[2] else None
+        return gx, gw, gb, None, None
 
 
 class AdapterUpFunction(Function):
-    """``out = T(z * gamma) + residual``, ``z = cat(a_special, a_patch) W^T + b``."""
+    """``out = z * gamma + residual``, ``z = T(cat(a_special, a_patch) W^T + b)``.
+
+    ``cd`` (default: a_patch's dtype) is the compute dtype the A rows, the
+    weight and the bias are cast to. With a gamma of ``cd`` the product is
+    rounded to ``cd`` and so is the sum (residual of ``cd``). With a float32
+    gamma (autocast, float32 parameters) the product and the residual add are
+    float32; the output is float32 with ``out_float32`` (the reference's
+    promotion of ``z * gamma + x``) and otherwise rounded once to ``cd``."""
 
     @staticmethod
-    def forward(ctx, a_special, a_patch, weight, bias, gamma, residual):
-        out = _ops.adapter_up(a_special, a_patch, weight, bias, gamma, residual)
-        ctx.save_for_backward(a_special, a_patch, weight, bias, gamma)
+    def forward(ctx, a_special, a_patch, weight, bias, gamma, residual, out_float32=False, cd=None):
+        cd = a_patch.dtype if cd is None else cd
+        sp, pa, wc, bc = _cast(a_special, cd), _cast(a_patch, cd), _cast(weight, cd), _cast(bias, cd)
+        out = _ops.adapter_up(sp, pa, wc, bc, gamma, residual, bool(out_float32))
+        ctx.save_for_backward(sp, pa, wc, bc, gamma)
+        ctx.dtypes = (a_special.dtype, a_patch.dtype, weight.dtype, None if bias is None else bias.dtype,
+                      residual.dtype)
         return out
 
     @staticmethod
     def backward(ctx, go):
-        a_sp, a_pa, weight, bias, gamma = ctx.saved_tensors
+        a_sp, a_pa, wc, bc, gamma = ctx.saved_tensors
+        sp_dt, pa_dt, w_dt, b_dt, res_dt = ctx.dtypes
         B, N, n = go.shape
         S = a_sp.shape[1]
-        k = weight.shape[1]
+        k = wc.shape[1]
         go = go.contiguous()
-        go2 = go.reshape(-1, n)
-        # go^T c without building c = cat(a_special, a_patch): the patch rows
-        # on the split-row kernel (rows of go picked by a row list), the few
-        # special rows as a small GEMM
-        if S > 0:
-            G = _wgrad(go2, _patch_rows(B, N, S, go.device), a_pa)
-            G = G + torch.matmul(go[:, :S].reshape(-1, n).t(), a_sp.reshape(-1, k))
-        else:
-            G = _wgrad(go2, _NO_ROWS(go2), a_pa)
+        goc = _cast(go, wc.dtype)  # a float32 output gradient rounded to the compute dtype
+        go2 = goc.reshape(-1, n)
+        # go^T c without building c = cat(a_special, a_patch), in fp32
+        G = _up_wgrad(goc, B, N, S, a_sp, a_pa)
         gsum = _colsum(go2)
-        g_gamma = None
-        if ctx.needs_input_grad[4]:
-            g_gamma = _ops.gamma_grad(weight, G, bias, gsum if bias is not None else None)
-            g_gamma = g_gamma.view(gamma.shape).to(gamma.dtype)
+        # gamma's gradient (in gamma's dtype) and the gamma-scaled W, G and
+        # sum(go) in one pass
+        g_gamma, w_g, gw, gb = _ops.up_proj_grads(wc, G, bc, gsum if bc is not None else None, gamma)
+        g_gamma = g_gamma.view(gamma.shape) if ctx.needs_input_grad[4] else None
         g_sp = g_pa = None
         if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
             # (go * gamma) W = go (gamma W): gamma folded into the small weight
-            dc = torch.matmul(go, weight * gamma)  # [B, N, k]
-            g_sp = dc[:, :S] if ctx.needs_input_grad[0] else None
-            g_pa = dc[:, S:].reshape(-1, k) if ctx.needs_input_grad[1] else None
-        gw = G * gamma if ctx.needs_input_grad[2] else None
-        gb = gsum * gamma if bias is not None and ctx.needs_input_grad[3] else None
-        return g_sp, g_pa, gw, gb, g_gamma, go
+            dc = torch.matmul(goc, w_g)  # [B, N, k]
+            g_sp = dc[:, :S].to(sp_dt) if ctx.needs_input_grad[0] else None
+            g_pa = dc[:, S:].reshape(-1, k).to(pa_dt) if ctx.needs_input_grad[1] else None
+        gw = gw.to(w_dt) if ctx.needs_input_grad[2] else None
+        gb = gb.to(b_dt) if b_dt is not None and ctx.needs_input_grad[3] else None
+        return g_sp, g_pa, gw, gb, g_gamma, go.to(res_dt), None, None
 
 
 class SparseConvAdapterFunction(Function):
@@ -204,9 +255,16 @@ class SparseConvAdapterFunction(Function):
 
     @staticmethod
     def forward(ctx, x, w_d, b_d, w_c, b_c, w_u, b_u, gamma, nbr, n_special, tpb, hm_rows=None, hm_gate=None,
-                packed=None):
+                packed=None, cd=None):
         S = int(n_special)
-        pre, sp, pa = _ops.adapter_down(x, w_d, b_d, S)
+        cd = x.dtype if cd is None else cd
+        # autocast's casts (none when everything is already in cd); gamma and
+        # the heatmap gate keep their dtype, as in the reference chain
+        params = (w_d, b_d, w_c, b_c, w_u, b_u, gamma, hm_gate)
+        ctx.dtypes = tuple(None if t is None else t.dtype for t in (x,) + params)
+        xc = _cast(x, cd)
+        w_d, b_d, w_c, b_c, w_u, b_u = (_cast(t, cd) for t in (w_d, b_d, w_c, b_c, w_u, b_u))
+        pre, sp, pa = _ops.adapter_down(xc, w_d, b_d, S)
         if hm_rows is not None:
             # heatmap injection on the SparseConv2D input (in place)
             _ops.heatmap_add_(pa, sp, hm_rows, hm_gate)
@@ -219,8 +277,10 @@ class SparseConvAdapterFunction(Function):
             packed = _ops.pack_weight(w_c, True, need_bwd)
         pf, pb = packed
         processed = _ops.fwd_packed(pa, nbr, w_c, pf, b_c, tpb, mode)
-        out = _ops.adapter_up(sp, processed, w_u, b_u, gamma, x)
-        ctx.save_for_backward(x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma, hm_rows, hm_gate)
+        # z * gamma + x: float32 when gamma is a float32 parameter (the
+        # reference's dtype promotion under autocast), else in cd
+        out = _ops.adapter_up(sp, processed, w_u, b_u, gamma, x, gamma.dtype == torch.float32 and cd != gamma.dtype)
+        ctx.save_for_backward(xc, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma, hm_rows, hm_gate)
         ctx.flags = (S, int(tpb), b_d is not None)
         return out
 
@@ -228,17 +288,17 @@ class SparseConvAdapterFunction(Function):
     def backward(ctx, go):
         x, w_d, pre, sp, pa, nbr, w_c, b_c, pb, processed, w_u, b_u, gamma, hm_rows, hm_gate = ctx.saved_tensors
         S, tpb, has_bd = ctx.flags
+        x_dt, wd_dt, bd_dt, wc_dt, bc_dt, wu_dt, bu_dt, _, _ = ctx.dtypes
         need = ctx.needs_input_grad
         B, N, n = go.shape
         k = w_u.shape[1]
+        cd = x.dtype
         go = go.contiguous()
+        go_res = go  # the residual's gradient (float32 under autocast)
+        go = _cast(go, cd)
         go2 = go.reshape(-1, n)
-        # up projection: G = go^T cat(sp, processed) without the cat
-        if S > 0:
-            G = _wgrad(go2, _patch_rows(B, N, S, go.device), processed)
-            G = G + torch.matmul(go[:, :S].reshape(-1, n).t(), sp.reshape(-1, k))
-        else:
-            G = _wgrad(go2, _NO_ROWS(go2), processed)
+        # up projection: G = go^T cat(sp, processed) without the cat, in fp32
+        G = _up_wgrad(go, B, N, S, sp, processed)
         gsum = _colsum(go2)
         # gamma's gradient and the gamma-scaled W_u, G and sum(go) in one pass
         g_gamma, w_u_g, gw_u, gb_u = _ops.up_proj_grads(w_u, G, b_u, gsum if b_u is not None else None, gamma)
@@ -260,17 +320,28 @@ class SparseConvAdapterFunction(Function):
             if need[12]:
                 g_gate = (gi_pa.float() * sp_rows.index_select(0, hm_rows).float()).sum().view(hm_gate.shape)
                 g_gate = g_gate.to(hm_gate.dtype)
-            g_sp = g_sp.reshape(-1, hidden).index_add(0, hm_rows, gi_pa * hm_gate).view(sp.shape)
+            # g * gate as one fp32 product rounded to cd (PyTorch's multiply
+            # in cd, or the cast of its float32 product under autocast)
+            g_sp = g_sp.reshape(-1, hidden).index_add(0, hm_rows, (gi_pa.float() * hm_gate.float()).to(cd))
+            g_sp = g_sp.view(sp.shape)
         # down projection: GELU backward from the two gradient buffers, then
         # the input gradient with the residual's go in the same GEMM
         du = _ops.gelu_backward_split(g_sp, gi_pa, pre, S)
         du2 = du.reshape(-1, du.shape[-1])
         x2 = x.reshape(-1, x.shape[-1])
-        gx = torch.addmm(go2, du2, w_d).view(x.shape) if need[0] else None
-        gw_d = _wgrad(du2, _NO_ROWS(du2), x2) if need[1] else None
-        gb_d = _colsum(du2) if has_bd and need[2] else None
-        return (gx, gw_d, gb_d, gw_c if need[3] else None, gb_c if need_bc else None, gw_u, gb_u, g_gamma,
-                None, None, None, None, g_gate, None)
+        gx = None
+        if need[0]:
+            if x_dt == cd:
+                gx = torch.addmm(go2, du2, w_d).view(x.shape)
+            else:
+                # float32 x under autocast: the down projection's gradient
+                # (in cd) upcast and added to the residual's float32 gradient
+                gx = torch.matmul(du2, w_d).to(x_dt).add_(go_res.reshape(-1, n)).view(x.shape)
+        gw_d = _wgrad(du2, _NO_ROWS(du2), x2).to(wd_dt) if need[1] else None
+        gb_d = _colsum(du2).to(bd_dt) if has_bd and need[2] else None
+        return (gx, gw_d, gb_d, gw_c.to(wc_dt) if need[3] else None,
+                gb_c.to(bc_dt) if need_bc else None, _cast(gw_u, wu_dt), _cast(gb_u, bu_dt), g_gamma,
+                None, None, None, None, g_gate, None, None)
 
 
 def _trunc_normal_init(layer, std):
@@ -364,15 +435,33 @@ class SparseConvAdapter(nn.Module):
             return ((y * H_hm) // h) * W_hm + (xc * W_hm) // w
         return spatial
 
-    def _fusable(self, x):
-        return (x.is_cuda and x.dtype in _FUSED_DTYPES and not torch.is_autocast_enabled("cuda")
-                and self.down_proj.weight.dtype == x.dtype)
+    def _fused_dtype(self, x):
+        """The compute dtype of the fused path for input ``x``, or None when the
+        call runs the unfused chain: outside autocast, x's float16 / bfloat16
+        dtype when every parameter has it; under ``torch.autocast("cuda")``
+        with a float16 / bfloat16 target, that target when x and every
+        parameter are in it or in float32 (a float32 x needs a float32 gamma,
+        which makes the output float32 as in the reference)."""
+        if not x.is_cuda:
+            return None
+        dts = {p.dtype for p in self.parameters()}
+        if torch.is_autocast_enabled("cuda"):
+            cd = torch.get_autocast_dtype("cuda")
+            if cd not in _FUSED_DTYPES or x.dtype not in (cd, torch.float32) or not dts <= {cd, torch.float32}:
+                return None
+            if x.dtype == torch.float32 and self.gamma.dtype != torch.float32:
+                return None
+            return cd
+        if x.dtype in _FUSED_DTYPES and dts == {x.dtype}:
+            return x.dtype
+        return None
 
     def forward(self, x, h, w, indices, total_num_patches, neighbor_indices=None, tokens_per_batch=0):
         """``x [B, N, embed]``; ``indices [B, N_kept]`` (flattened ``t*h*w + y*w
         + x`` positions of the kept tokens); ``neighbor_indices`` ``[B, N_kept,
         9]`` or ``[B * N_kept, 9]``. ``total_num_patches`` is ``T*h*w``."""
-        if not self._fusable(x) or indices.shape[1] == 0:
+        cd = self._fused_dtype(x)
+        if cd is None or indices.shape[1] == 0:
             return self.reference_forward(x, h, w, indices, total_num_patches, neighbor_indices)
         B, N, _ = x.shape
         S = self._n_special(x, indices)
@@ -395,22 +484,28 @@ class SparseConvAdapter(nn.Module):
                 hm_rows = (base + cells).reshape(-1).to(torch.int32)
                 hm_gate = self.heatmap_gate
             cache = conv.packed_weight_cache
-            packed = None if cache is None else cache.get(conv.weight, conv.weight, torch.is_grad_enabled())
+            packed = None
+            if cache is not None:
+                packed = cache.get(conv.weight, _cast(conv.weight, cd), torch.is_grad_enabled())
             return SparseConvAdapterFunction.apply(x, self.down_proj.weight, self.down_proj.bias, conv.weight,
                                                    conv.bias, self.up_proj.weight, self.up_proj.bias, self.gamma,
-                                                   nbr, S, tokens_per_batch, hm_rows, hm_gate, packed)
-        sp, pa = AdapterDownFunction.apply(x, self.down_proj.weight, self.down_proj.bias, S)
+                                                   nbr, S, tokens_per_batch, hm_rows, hm_gate, packed, cd)
+        sp, pa = AdapterDownFunction.apply(x, self.down_proj.weight, self.down_proj.bias, S, cd)
         processed = conv(pa, nbr, tokens_per_batch=tokens_per_batch)
         x_comb = torch.cat([sp, processed.view(B, N - S, -1)], dim=1)
-        x_comb = self._attention_branch(x_comb, S, indices, h, w, total_num_patches, fused=True)
+        x_comb = self._attention_branch(x_comb, S, indices, h, w, total_num_patches, fused=True, cd=cd)
         empty = x_comb.new_empty(B, 0, x_comb.shape[-1])
         return AdapterUpFunction.apply(empty, x_comb.reshape(B * N, -1), self.up_proj.weight, self.up_proj.bias,
-                                       self.gamma, x)
+                                       self.gamma, x, self.gamma.dtype == torch.float32 and cd != torch.float32, cd)
 
-    def _attention_branch(self, x_comb, S, indices, h, w, total_num_patches, fused):
+    def _attention_branch(self, x_comb, S, indices, h, w, total_num_patches, fused, cd=None):
         """The ``use_attn`` branch on ``x_combined`` (vit_sparse_adapter_poguise.py:
         511-650). With ``fused`` the ``shortcut + attn_proj(.) * attn_gamma`` of
-        variants 1-3 runs on the up GEMM's epilogue."""
+        variants 1-3 runs on the up GEMM's epilogue, in the compute dtype
+        ``cd``. Under autocast with a float32 ``attn_gamma`` the reference's
+        sum is float32 and its only consumer, ``up_proj``, casts it to the
+        autocast dtype; the epilogue rounds the float32 sum to ``cd`` once,
+        which gives that cast's values directly."""
         shortcut = x_comb
         B, N, C = x_comb.shape
         if self.use_attn >= 4:
@@ -454,7 +549,7 @@ class SparseConvAdapter(nn.Module):
         if fused:
             empty = xa.new_empty(B, 0, A)
             return AdapterUpFunction.apply(empty, xa.reshape(B * N, A), self.attn_proj.weight, self.attn_proj.bias,
-                                           self.attn_gamma, shortcut)
+                                           self.attn_gamma, shortcut, False, cd)
         return shortcut + self.attn_proj(xa) * self.attn_gamma
 
     def reference_forward(self, x, h, w, indices, total_num_patches, neighbor_indices=None):

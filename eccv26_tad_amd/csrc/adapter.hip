@@ -54,19 +54,28 @@ __device__ __forceinline__ float gelu_erf(float u) { return 0.5f * u * (1.0f + e
 // LDS rows are BK + 8 elements: for BK = 64 (144 bytes) and BK = 32 (80
 // bytes) the 16 rows one fragment read touches fall on distinct bank groups.
 // Global rows of the output and residual are moved as 16-byte pieces.
-template <typename T, int EPI, int FM, int FN, int BK>
+//
+// MIX (up epilogue only) takes gamma, the residual and the output each in T
+// or in fp32, as `mix` says (MIX_GAMMA_F32, MIX_RES_F32, MIX_OUT_F32): the
+// dtypes of the reference chain under autocast, where gamma is an fp32
+// parameter, so z * gamma is an fp32 product of the rounded z (no rounding
+// to T), and the residual add is in fp32; the sum is stored as fp32 or
+// rounded once to T.
+enum { MIX_GAMMA_F32 = 1, MIX_RES_F32 = 2, MIX_OUT_F32 = 4 };
+template <typename T, int EPI, int FM, int FN, int BK, bool MIX = false>
 __global__ __launch_bounds__(256) void k_adapter_gemm(
     const T* __restrict__ a0, const T* __restrict__ a1, const T* __restrict__ w,
-    const T* __restrict__ bias, const T* __restrict__ gamma, const T* __restrict__ res,
+    const T* __restrict__ bias, const void* __restrict__ gamma, const void* __restrict__ res,
     T* __restrict__ out0, T* __restrict__ out1, T* __restrict__ out2, int64_t m_rows, int k_red,
-    int n_out, RowMap rm, int n_col_tiles, int64_t n_tiles) {
+    int n_out, RowMap rm, int n_col_tiles, int64_t n_tiles, int mix) {
     constexpr int BM = 2 * FM * 16, BN = 2 * FN * 16;
     constexpr int CPR = BK / 8;                                  // 16-byte chunks per row and stage
     constexpr int LP = BK + 8;                                   // LDS pitch in elements
     constexpr int A_PER = BM * CPR / 256, B_PER = BN * CPR / 256;  // chunks per thread
     static_assert(A_PER * 256 == BM * CPR && B_PER * 256 == BN * CPR, "tile / thread count");
     constexpr int OP = BN + 8;  // pitch (elements) of the output tiles of the epilogue
-    constexpr int SMEM = cmax_i(2 * (BM + BN) * LP, 2 * BM * OP);
+    constexpr int OPF = BN + 4;  // pitch (floats) of the fp32 tile of the mixed epilogue
+    constexpr int SMEM = cmax_i(cmax_i(2 * (BM + BN) * LP, 2 * BM * OP), MIX ? 2 * BM * OPF : 0);
     // one array: the stage buffers, reused by the epilogue's two output tiles
     __shared__ __align__(16) u16 smem[SMEM];
     u16(*const As)[BM][LP] = (u16(*)[BM][LP])smem;
@@ -175,7 +184,10 @@ __global__ __launch_bounds__(256) void k_adapter_gemm(
     // rather than 8-byte pieces of 16 rows.
     u16* const tile0 = smem;             // z (down: the Linear output) or T(z * gamma)
     u16* const tile1 = smem + BM * OP;   // down: GELU(z)
-    const float gm = EPI == EPI_UP_SCALE_RES ? (float)gamma[0] : 0.f;
+    float* const tilef = (float*)smem;   // mixed up epilogue: z * gamma in fp32
+    const bool g32 = MIX && (mix & MIX_GAMMA_F32);
+    const float gm = EPI != EPI_UP_SCALE_RES ? 0.f
+                     : g32 ? *(const float*)gamma : (float)*(const T*)gamma;
 #pragma unroll
     for (int b = 0; b < FN; ++b) {
         const int nl = wn * FN * 16 + b * 16 + (lane >> 4) * 4;
@@ -188,15 +200,24 @@ __global__ __launch_bounds__(256) void k_adapter_gemm(
         for (int a = 0; a < FM; ++a) {
             const int ml = wm * FM * 16 + a * 16 + (lane & 15);
             u16 z[4], gz[4];
+            float zf[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const T zt = (T)(acc[a][b][j] + bv[j]);
                 if constexpr (EPI == EPI_DOWN_GELU) {
                     z[j] = __builtin_bit_cast(u16, zt);
                     gz[j] = __builtin_bit_cast(u16, (T)gelu_erf((float)zt));
+                } else if constexpr (MIX) {
+                    // fp32 product of the rounded z; rounded to T only when gamma is T
+                    const float p = f32_rounded((float)zt * gm);
+                    zf[j] = g32 ? p : (float)(T)p;
                 } else {
                     z[j] = __builtin_bit_cast(u16, (T)((float)zt * gm));
                 }
+            }
+            if constexpr (MIX) {
+                *(f32x4*)&tilef[ml * OPF + nl] = f32x4{zf[0], zf[1], zf[2], zf[3]};
+                continue;
             }
             *(uint2*)&tile0[ml * OP + nl] = uint2{(unsigned)z[0] | ((unsigned)z[1] << 16),
                                                  (unsigned)z[2] | ((unsigned)z[3] << 16)};
@@ -212,6 +233,44 @@ __global__ __launch_bounds__(256) void k_adapter_gemm(
         const int ml = c / RC, nc = (c % RC) * 8;
         const int64_t m = row0 + ml;
         if (m >= m_rows) continue;
+        if constexpr (MIX) {
+            // y = z * gamma + residual in fp32, stored as fp32 or rounded once
+            // (the fp32 sum, then the cast)
+            float y[8];
+            const f32x4 p0 = *(const f32x4*)&tilef[ml * OPF + nc], p1 = *(const f32x4*)&tilef[ml * OPF + nc + 4];
+            const int64_t off = m * n_out + col0 + nc;
+            if (mix & MIX_RES_F32) {
+                const f32x4 r0 = *(const f32x4*)((const float*)res + off);
+                const f32x4 r1 = *(const f32x4*)((const float*)res + off + 4);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    y[j] = p0[j] + r0[j];
+                    y[4 + j] = p1[j] + r1[j];
+                }
+            } else {
+                const u32x4 rr = *(const u32x4*)((const T*)res + off);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4& pp = q < 2 ? p0 : p1;
+                    y[2 * q] = pp[(2 * q) & 3] + (float)__builtin_bit_cast(T, (u16)(rr[q] & 0xffffu));
+                    y[2 * q + 1] = pp[(2 * q + 1) & 3] + (float)__builtin_bit_cast(T, (u16)(rr[q] >> 16));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[j] = f32_rounded(y[j]);
+            if (mix & MIX_OUT_F32) {
+                *(f32x4*)((float*)out0 + off) = f32x4{y[0], y[1], y[2], y[3]};
+                *(f32x4*)((float*)out0 + off + 4) = f32x4{y[4], y[5], y[6], y[7]};
+            } else {
+                u32x4 o;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    o[q] = (unsigned)__builtin_bit_cast(u16, (T)y[2 * q]) |
+                           ((unsigned)__builtin_bit_cast(u16, (T)y[2 * q + 1]) << 16);
+                *(u32x4*)(out0 + off) = o;
+            }
+            continue;
+        }
         const u32x4 v0 = *(const u32x4*)&tile0[ml * OP + nc];
         if constexpr (EPI == EPI_DOWN_GELU) {
             *(u32x4*)(out0 + m * n_out + col0 + nc) = v0;
@@ -219,7 +278,7 @@ __global__ __launch_bounds__(256) void k_adapter_gemm(
             const int64_t r = rm.split(m, sp);
             *(u32x4*)((sp ? out1 : out2) + r * n_out + col0 + nc) = *(const u32x4*)&tile1[ml * OP + nc];
         } else {
-            const u32x4 rr = *(const u32x4*)(res + m * n_out + col0 + nc);
+            const u32x4 rr = *(const u32x4*)((const T*)res + m * n_out + col0 + nc);
             u32x4 y;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -248,26 +307,35 @@ static int adapter_check(const char* what, int64_t batch, int64_t n_tokens, int6
     return SVTAD_OK;
 }
 
-template <typename T, int EPI, int FN, int BK, int FM = 4>
+template <typename T, int EPI, int FN, int BK, int FM = 4, bool MIX = false>
 static void launch_tiles(const void* a0, const void* a1, const void* w, const void* bias,
                          const void* gamma, const void* res, void* o0, void* o1, void* o2,
-                         int64_t rows, int k, int n, RowMap rm, hipStream_t s) {
+                         int64_t rows, int k, int n, RowMap rm, int mix, hipStream_t s) {
     constexpr int BM = 32 * FM, BN = 32 * FN;
     const int nct = n / BN;
     const int64_t tiles = cdiv(rows, BM) * nct;
-    hipLaunchKernelGGL((k_adapter_gemm<T, EPI, FM, FN, BK>), dim3((unsigned)tiles), dim3(256), 0, s,
-                       (const T*)a0, (const T*)a1, (const T*)w, (const T*)bias, (const T*)gamma,
-                       (const T*)res, (T*)o0, (T*)o1, (T*)o2, rows, k, n, rm, nct, tiles);
+    hipLaunchKernelGGL((k_adapter_gemm<T, EPI, FM, FN, BK, MIX>), dim3((unsigned)tiles), dim3(256), 0, s,
+                       (const T*)a0, (const T*)a1, (const T*)w, (const T*)bias, gamma, res, (T*)o0, (T*)o1,
+                       (T*)o2, rows, k, n, rm, nct, tiles, mix);
 }
 
 // 64 x 64 tiles (enough workgroups per CU to cover the load latency), 64-deep
-// stages when k allows
+// stages when k allows; `mix` != 0 selects the mixed-dtype up epilogue
 template <typename T, int EPI>
 static void launch_adapter(const void* a0, const void* a1, const void* w, const void* bias,
                            const void* gamma, const void* res, void* o0, void* o1, void* o2,
-                           int64_t rows, int k, int n, RowMap rm, hipStream_t s) {
-    if (k % 64 == 0) launch_tiles<T, EPI, 2, 64, 2>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, s);
-    else launch_tiles<T, EPI, 2, 32, 2>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, s);
+                           int64_t rows, int k, int n, RowMap rm, hipStream_t s, int mix = 0) {
+    if constexpr (EPI == EPI_UP_SCALE_RES) {
+        if (mix) {
+            if (k % 64 == 0)
+                launch_tiles<T, EPI, 2, 64, 2, true>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, mix, s);
+            else
+                launch_tiles<T, EPI, 2, 32, 2, true>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, mix, s);
+            return;
+        }
+    }
+    if (k % 64 == 0) launch_tiles<T, EPI, 2, 64, 2>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, 0, s);
+    else launch_tiles<T, EPI, 2, 32, 2>(a0, a1, w, bias, gamma, res, o0, o1, o2, rows, k, n, rm, 0, s);
 }
 
 // Column sums out[c] = sum_r a[r][c] (the bias gradients of the adapter's
@@ -355,22 +423,25 @@ constexpr int kGammaParts = 64;
 // (NULL outputs are skipped): w_sc = T(w * gamma), g_sc = T(g * gamma),
 // gs_sc = T(gs * gamma), each product in fp32 and rounded once, as PyTorch's
 // elementwise multiply rounds it.
-template <typename T>
-__global__ __launch_bounds__(256) void k_gamma_part(const T* __restrict__ w, const T* __restrict__ g,
+// With G = float (g32) g is fp32 (the unrounded weight-gradient sums): the
+// dot products use it as is and g_sc = T(g * gamma) is its only rounding.
+template <typename T, typename G = T>
+__global__ __launch_bounds__(256) void k_gamma_part(const T* __restrict__ w, const G* __restrict__ g,
                                                     int64_t chunks, const T* __restrict__ b,
                                                     const T* __restrict__ gs, int64_t chunks_b,
-                                                    float* __restrict__ part, const T* __restrict__ gamma,
-                                                    T* __restrict__ w_sc, T* __restrict__ g_sc,
+                                                    float* __restrict__ part, const void* __restrict__ gamma,
+                                                    bool gamma32, T* __restrict__ w_sc, T* __restrict__ g_sc,
                                                     T* __restrict__ gs_sc) {
     __shared__ float red[256];
     const int tid = threadIdx.x;
-    const float gm = gamma ? (float)gamma[0] : 0.f;
+    const float gm = !gamma ? 0.f : gamma32 ? *(const float*)gamma : (float)*(const T*)gamma;
     auto scale8 = [&](const u32x4 a) {
         u32x4 o;
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-            const T lo = (T)((float)__builtin_bit_cast(T, (u16)(a[h] & 0xffffu)) * gm);
-            const T hi = (T)((float)__builtin_bit_cast(T, (u16)(a[h] >> 16)) * gm);
+            // fp32 product, then the cast (PyTorch's multiply and .to())
+            const T lo = (T)f32_rounded((float)__builtin_bit_cast(T, (u16)(a[h] & 0xffffu)) * gm);
+            const T hi = (T)f32_rounded((float)__builtin_bit_cast(T, (u16)(a[h] >> 16)) * gm);
             o[h] = (unsigned)__builtin_bit_cast(u16, lo) | ((unsigned)__builtin_bit_cast(u16, hi) << 16);
         }
         return o;
@@ -388,10 +459,27 @@ __global__ __launch_bounds__(256) void k_gamma_part(const T* __restrict__ w, con
     };
     for (int64_t c = c0 + tid; c < c1; c += 256) {
         if (c < chunks) {
-            const u32x4 wv = *(const u32x4*)(w + c * 8), gv = *(const u32x4*)(g + c * 8);
-            dot8(wv, gv);
-            if (w_sc) *(u32x4*)(w_sc + c * 8) = scale8(wv);
-            if (g_sc) *(u32x4*)(g_sc + c * 8) = scale8(gv);
+            const u32x4 wv = *(const u32x4*)(w + c * 8);
+            if constexpr (sizeof(G) == 4) {
+                const f32x4 g0 = *(const f32x4*)(g + c * 8), g1 = *(const f32x4*)(g + c * 8 + 4);
+                u32x4 gs8;
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const float glo = h < 2 ? g0[2 * h] : g1[2 * h - 4];
+                    const float ghi = h < 2 ? g0[2 * h + 1] : g1[2 * h - 3];
+                    acc += (float)__builtin_bit_cast(T, (u16)(wv[h] & 0xffffu)) * glo;
+                    acc += (float)__builtin_bit_cast(T, (u16)(wv[h] >> 16)) * ghi;
+                    gs8[h] = (unsigned)__builtin_bit_cast(u16, (T)f32_rounded(glo * gm)) |
+                             ((unsigned)__builtin_bit_cast(u16, (T)f32_rounded(ghi * gm)) << 16);
+                }
+                if (w_sc) *(u32x4*)(w_sc + c * 8) = scale8(wv);
+                if (g_sc) *(u32x4*)(g_sc + c * 8) = gs8;
+            } else {
+                const u32x4 gv = *(const u32x4*)(g + c * 8);
+                dot8(wv, gv);
+                if (w_sc) *(u32x4*)(w_sc + c * 8) = scale8(wv);
+                if (g_sc) *(u32x4*)(g_sc + c * 8) = scale8(gv);
+            }
         } else {
             const u32x4 bv = *(const u32x4*)(b + (c - chunks) * 8), sv = *(const u32x4*)(gs + (c - chunks) * 8);
             dot8(bv, sv);
@@ -439,9 +527,26 @@ extern "C" int svtad_adapter_up(const void* a_special, const void* a_patch, cons
                                 const void* bias, const void* gamma, const void* residual, void* out,
                                 int64_t batch, int64_t n_tokens, int64_t n_special, int k, int n,
                                 int dtype, void* stream) {
+    return svtad_adapter_up_mixed(a_special, a_patch, weight, bias, gamma, residual, out, batch, n_tokens,
+                                  n_special, k, n, dtype, dtype, dtype, dtype, stream);
+}
+
+extern "C" int svtad_adapter_up_mixed(const void* a_special, const void* a_patch, const void* weight,
+                                      const void* bias, const void* gamma, const void* residual, void* out,
+                                      int64_t batch, int64_t n_tokens, int64_t n_special, int k, int n,
+                                      int dtype, int gamma_dtype, int residual_dtype, int out_dtype,
+                                      void* stream) {
     int st = adapter_check("adapter_up: needs f16/bf16, k % 32 == 0, n % 64 == 0, 0 <= n_special <= n_tokens",
                            batch, n_tokens, n_special, k, n, dtype);
     if (st) return st;
+    auto is_t_or_f32 = [&](int d) { return d == dtype || d == SVTAD_F32; };
+    if (!is_t_or_f32(gamma_dtype) || !is_t_or_f32(residual_dtype) || !is_t_or_f32(out_dtype))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "adapter_up: gamma, residual and out take dtype or f32");
+    if (gamma_dtype == dtype && (residual_dtype != dtype || out_dtype != dtype))
+        return set_error(SVTAD_ERR_UNSUPPORTED,
+                         "adapter_up: an f32 residual or output needs an f32 gamma (the reference's dtype promotion)");
+    const int mix = (gamma_dtype == SVTAD_F32 ? MIX_GAMMA_F32 : 0) | (residual_dtype == SVTAD_F32 ? MIX_RES_F32 : 0) |
+                    (out_dtype == SVTAD_F32 ? MIX_OUT_F32 : 0);
     const int64_t rows = batch * n_tokens;
     if (rows == 0) return SVTAD_OK;
     if (!weight || !gamma || !residual || !out || (n_special > 0 && !a_special) ||
@@ -454,10 +559,10 @@ extern "C" int svtad_adapter_up(const void* a_special, const void* a_patch, cons
     hipStream_t s = (hipStream_t)stream;
     if (dtype == SVTAD_F16)
         launch_adapter<f16, EPI_UP_SCALE_RES>(a_special, a_patch, weight, bias, gamma, residual, out, nullptr,
-                                              nullptr, rows, k, n, rm, s);
+                                              nullptr, rows, k, n, rm, s, mix);
     else
         launch_adapter<bf16, EPI_UP_SCALE_RES>(a_special, a_patch, weight, bias, gamma, residual, out, nullptr,
-                                               nullptr, rows, k, n, rm, s);
+                                               nullptr, rows, k, n, rm, s, mix);
     return launch_status();
 }
 
@@ -470,8 +575,17 @@ extern "C" size_t svtad_linear_wgrad_workspace_bytes(int64_t n, int c_g, int c_x
 extern "C" int svtad_linear_wgrad(const void* g, const int32_t* rows, const void* x, void* out, void* workspace,
                                   size_t workspace_bytes, int64_t n, int64_t n_g_rows, int c_g, int c_x,
                                   int dtype, void* stream) {
+    return svtad_linear_wgrad_mixed(g, rows, x, out, workspace, workspace_bytes, n, n_g_rows, c_g, c_x, dtype,
+                                    dtype, stream);
+}
+
+extern "C" int svtad_linear_wgrad_mixed(const void* g, const int32_t* rows, const void* x, void* out,
+                                        void* workspace, size_t workspace_bytes, int64_t n, int64_t n_g_rows,
+                                        int c_g, int c_x, int dtype, int out_dtype, void* stream) {
     if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
         return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: needs f16/bf16");
+    if (out_dtype != dtype && out_dtype != SVTAD_F32)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "linear_wgrad: out takes dtype or f32");
     if (n < 0 || n_g_rows < 0 || c_g <= 0 || c_x <= 0 || (!rows && n_g_rows < n))
         return set_error(SVTAD_ERR_INVALID, "linear_wgrad: bad sizes");
     const BwPlan p = plan_wgrad(n, c_g, c_x);
@@ -485,7 +599,7 @@ extern "C" int svtad_linear_wgrad(const void* g, const int32_t* rows, const void
     if (workspace_bytes < p.ws_bytes)
         return set_error(SVTAD_ERR_WORKSPACE, "linear_wgrad: workspace smaller than svtad_linear_wgrad_workspace_bytes()");
     const int st = wgrad_mfma(dtype, p, g, rows, x, out, workspace, workspace_bytes, n, rows ? n_g_rows : n, c_g,
-                              c_x, (hipStream_t)stream);
+                              c_x, out_dtype == SVTAD_F32, (hipStream_t)stream);
     if (st) return st;
     return launch_status();
 }
@@ -558,11 +672,16 @@ extern "C" int svtad_gelu_backward_split(const void* grad_special, const void* g
 // is a launch of its own after that GEMM.
 namespace svtad {
 
+//
+// With an fp32 gate (`gate32`, the reference chain under autocast, where the
+// gate is an fp32 parameter) the product and the sum are fp32 and the sum is
+// rounded to T once, which is the cast SparseConv2d applies to its fp32 input
+// there: patch[i] = T(float(patch[i]) + float(special[src[i]]) * gate).
 template <typename T>
 __global__ __launch_bounds__(256) void k_heatmap_add(T* __restrict__ patch, const T* __restrict__ special,
-                                                     const int32_t* __restrict__ src, const T* __restrict__ gate,
-                                                     int64_t rows, int64_t n_special_rows, int cols) {
-    // two roundings, as the unfused chain: no fused multiply-add
+                                                     const int32_t* __restrict__ src, const void* __restrict__ gate,
+                                                     int64_t rows, int64_t n_special_rows, int cols, bool gate32) {
+    // products and sums rounded as the unfused chain: no fused multiply-add
 #pragma clang fp contract(off)
     const int cpr = cols / 8;
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -571,7 +690,7 @@ __global__ __launch_bounds__(256) void k_heatmap_add(T* __restrict__ patch, cons
     const int c = (int)(e - i * cpr) * 8;
     const int32_t r = src[i];
     if (r < 0 || r >= n_special_rows) return;
-    const float g = (float)gate[0];
+    const float g = gate32 ? *(const float*)gate : (float)*(const T*)gate;
     u32x4* const pp = (u32x4*)(patch + i * cols + c);
     const u32x4 pv = *pp;
     const u32x4 hv = *(const u32x4*)(special + (int64_t)r * cols + c);
@@ -583,8 +702,9 @@ __global__ __launch_bounds__(256) void k_heatmap_add(T* __restrict__ patch, cons
         for (int h = 0; h < 2; ++h) {
             const T pt = __builtin_bit_cast(T, (u16)(pv[q] >> (16 * h)));
             const T ht = __builtin_bit_cast(T, (u16)(hv[q] >> (16 * h)));
-            const T prod = (T)((float)ht * g);
-            w |= (unsigned)__builtin_bit_cast(u16, (T)((float)pt + (float)prod)) << (16 * h);
+            const float prod32 = f32_rounded((float)ht * g);
+            const float prod = gate32 ? prod32 : (float)(T)prod32;
+            w |= (unsigned)__builtin_bit_cast(u16, (T)f32_rounded((float)pt + prod)) << (16 * h);
         }
         o[q] = w;
     }
@@ -595,8 +715,18 @@ __global__ __launch_bounds__(256) void k_heatmap_add(T* __restrict__ patch, cons
 
 extern "C" int svtad_heatmap_add(void* patch, const void* special, const int32_t* src_rows, const void* gate,
                                  int64_t rows, int64_t n_special_rows, int cols, int dtype, void* stream) {
+    return svtad_heatmap_add_mixed(patch, special, src_rows, gate, rows, n_special_rows, cols, dtype, dtype,
+                                   stream);
+}
+
+extern "C" int svtad_heatmap_add_mixed(void* patch, const void* special, const int32_t* src_rows,
+                                       const void* gate, int64_t rows, int64_t n_special_rows, int cols,
+                                       int dtype, int gate_dtype, void* stream) {
     if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
         return set_error(SVTAD_ERR_UNSUPPORTED, "heatmap_add: needs f16/bf16");
+    if (gate_dtype != dtype && gate_dtype != SVTAD_F32)
+        return set_error(SVTAD_ERR_UNSUPPORTED, "heatmap_add: the gate takes dtype or f32");
+    const bool gate32 = gate_dtype == SVTAD_F32;
     if (rows < 0 || n_special_rows < 0 || cols <= 0 || cols % 8 != 0)
         return set_error(SVTAD_ERR_INVALID, "heatmap_add: needs rows >= 0 and cols a positive multiple of 8");
     if (rows == 0) return SVTAD_OK;
@@ -608,10 +738,10 @@ extern "C" int svtad_heatmap_add(void* patch, const void* special, const int32_t
     const dim3 grid((unsigned)cdiv(threads, 256));
     if (dtype == SVTAD_F16)
         hipLaunchKernelGGL(k_heatmap_add<f16>, grid, dim3(256), 0, (hipStream_t)stream, (f16*)patch,
-                           (const f16*)special, src_rows, (const f16*)gate, rows, n_special_rows, cols);
+                           (const f16*)special, src_rows, gate, rows, n_special_rows, cols, gate32);
     else
         hipLaunchKernelGGL(k_heatmap_add<bf16>, grid, dim3(256), 0, (hipStream_t)stream, (bf16*)patch,
-                           (const bf16*)special, src_rows, (const bf16*)gate, rows, n_special_rows, cols);
+                           (const bf16*)special, src_rows, gate, rows, n_special_rows, cols, gate32);
     return launch_status();
 }
 
@@ -620,8 +750,19 @@ extern "C" size_t svtad_gamma_grad_workspace_bytes(void) { return (size_t)kGamma
 extern "C" int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,
                                 int64_t count_b, void* out, const void* gamma, void* w_scaled, void* g_scaled,
                                 void* gs_scaled, void* workspace, size_t workspace_bytes, int dtype, void* stream) {
+    return svtad_gamma_grad_mixed(w, g, count, b, gs, count_b, out, gamma, w_scaled, g_scaled, gs_scaled, workspace,
+                                  workspace_bytes, dtype, dtype, dtype, stream);
+}
+
+extern "C" int svtad_gamma_grad_mixed(const void* w, const void* g, int64_t count, const void* b, const void* gs,
+                                      int64_t count_b, void* out, const void* gamma, void* w_scaled,
+                                      void* g_scaled, void* gs_scaled, void* workspace, size_t workspace_bytes,
+                                      int dtype, int g_dtype, int gamma_dtype, void* stream) {
     if (dtype != SVTAD_F16 && dtype != SVTAD_BF16)
         return set_error(SVTAD_ERR_UNSUPPORTED, "gamma_grad: needs f16/bf16");
+    if ((gamma_dtype != dtype && gamma_dtype != SVTAD_F32) || (g_dtype != dtype && g_dtype != SVTAD_F32))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "gamma_grad: g and gamma take dtype or f32");
+    const bool gamma32 = gamma_dtype == SVTAD_F32;
     if (count < 0 || count_b < 0 || count % 8 != 0 || count_b % 8 != 0 || (!b != !gs))
         return set_error(SVTAD_ERR_INVALID, "gamma_grad: counts must be multiples of 8; b and gs go together");
     if (!out || !workspace || (count > 0 && (!w || !g)) || (count_b > 0 && !b))
@@ -636,14 +777,20 @@ extern "C" int svtad_gamma_grad(const void* w, const void* g, int64_t count, con
         return set_error(SVTAD_ERR_WORKSPACE, "gamma_grad: workspace smaller than svtad_gamma_grad_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;
     const int64_t nb = b ? count_b / 8 : 0;
-    if (dtype == SVTAD_F16)
-        hipLaunchKernelGGL((k_gamma_part<f16>), dim3(kGammaParts), dim3(256), 0, s, (const f16*)w, (const f16*)g,
-                           count / 8, (const f16*)b, (const f16*)gs, nb, (float*)workspace, (const f16*)gamma,
-                           (f16*)w_scaled, (f16*)g_scaled, (f16*)gs_scaled);
-    else
-        hipLaunchKernelGGL((k_gamma_part<bf16>), dim3(kGammaParts), dim3(256), 0, s, (const bf16*)w, (const bf16*)g,
-                           count / 8, (const bf16*)b, (const bf16*)gs, nb, (float*)workspace, (const bf16*)gamma,
-                           (bf16*)w_scaled, (bf16*)g_scaled, (bf16*)gs_scaled);
-    split_reduce(dtype, workspace, 1, kGammaParts, out, s);
+    const bool g32 = g_dtype == SVTAD_F32;
+#define SVTAD_GAMMA_LAUNCH(T, G)                                                                              \
+    hipLaunchKernelGGL((k_gamma_part<T, G>), dim3(kGammaParts), dim3(256), 0, s, (const T*)w, (const G*)g,     \
+                       count / 8, (const T*)b, (const T*)gs, nb, (float*)workspace, gamma, gamma32, (T*)w_scaled, \
+                       (T*)g_scaled, (T*)gs_scaled)
+    if (dtype == SVTAD_F16) {
+        if (g32) SVTAD_GAMMA_LAUNCH(f16, float);
+        else SVTAD_GAMMA_LAUNCH(f16, f16);
+    } else {
+        if (g32) SVTAD_GAMMA_LAUNCH(bf16, float);
+        else SVTAD_GAMMA_LAUNCH(bf16, bf16);
+    }
+#undef SVTAD_GAMMA_LAUNCH
+    // the gradient takes gamma's dtype (an fp32 parameter's gradient is fp32)
+    split_reduce(gamma_dtype, workspace, 1, kGammaParts, out, s);
     return launch_status();
 }

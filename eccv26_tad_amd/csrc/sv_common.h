@@ -21,6 +21,15 @@ template <> __device__ __forceinline__ float to_acc<float, bf16>(bf16 v) { retur
 // Round-to-nearest-even conversion from the accumulator to the storage type.
 template <typename T, typename A> __device__ __forceinline__ T from_acc(A v) { return (T)v; }
 
+// x as a stored fp32 value. The empty asm makes the value opaque, so the
+// compiler cannot merge the operation that produced x with a later
+// conversion to f16 (v_fma_mix*: one rounding of the exact result where the
+// sequence of PyTorch ops rounds to fp32 first, then to f16).
+__device__ __forceinline__ float f32_rounded(float x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
 // Source row of neighbor entry (i, k): -1 when missing, out of range, or
 // negative. tpb > 0 adds the per-row batch offset (i / tpb) * tpb.
 __device__ __forceinline__ int64_t src_row(const int32_t* __restrict__ nbr, int64_t i, int k,

@@ -133,6 +133,7 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
 // launched) as bw_mfma.
 BwPlan plan_wgrad(int64_t n, int c_in, int c_out);
 int wgrad_mfma(int dtype, const BwPlan& p, const void* g, const int32_t* rows, const void* x, void* out,
-               void* ws, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out, hipStream_t s);
+               void* ws, size_t ws_bytes, int64_t n, int64_t n_src, int c_in, int c_out, bool out_f32,
+               hipStream_t s);
 
 }  // namespace svtad

@@ -707,11 +707,17 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> op_adapter_down(const at::Tensor&
 }
 
 // adapter_up(a_special [B, S, k], a_patch [B * (N - S), k], weight [n, k], bias [n] or None,
-//            gamma [1], residual [B, N, n]) -> out [B, N, n]
+//            gamma [1], residual [B, N, n], out_float32=False) -> out [B, N, n]
+// a_special, a_patch, weight and bias share the compute dtype T (f16 / bf16).
+// gamma and the residual are T, or float32 (the reference under autocast,
+// where gamma is a float32 parameter): then z * gamma is an fp32 product and
+// the add is fp32, and out is float32 with out_float32, else rounded once to
+// T. With a T gamma, residual and out are T.
 at::Tensor op_adapter_up(const at::Tensor& sp_in, const at::Tensor& pa_in, const at::Tensor& w_in,
                          const c10::optional<at::Tensor>& bias, const at::Tensor& gamma_in,
-                         const at::Tensor& res_in) {
-    adapter_common(res_in, w_in, "residual");
+                         const at::Tensor& res_in, bool out_float32) {
+    check_gpu(res_in, "residual");
+    adapter_common(pa_in, w_in, "a_patch");
     TORCH_CHECK(res_in.dim() == 3, "residual must be [B, N, C]");
     const int64_t B = res_in.size(0), N = res_in.size(1), n = res_in.size(2), k = w_in.size(1);
     TORCH_CHECK(w_in.size(0) == n, "weight must be (", n, ", k)");
@@ -719,17 +725,23 @@ at::Tensor op_adapter_up(const at::Tensor& sp_in, const at::Tensor& pa_in, const
     const int64_t S = sp_in.size(1);
     TORCH_CHECK(S <= N && pa_in.dim() == 2 && pa_in.size(0) == B * (N - S) && pa_in.size(1) == k,
                 "a_patch must be [B * (N - S), k]");
-    TORCH_CHECK(sp_in.scalar_type() == res_in.scalar_type() && pa_in.scalar_type() == res_in.scalar_type() &&
-                    gamma_in.scalar_type() == res_in.scalar_type(),
-                "a_special, a_patch, gamma and residual must share the dtype");
+    const at::ScalarType t = pa_in.scalar_type();
+    TORCH_CHECK(sp_in.scalar_type() == t, "a_special and a_patch must share the dtype");
+    auto t_or_f32 = [&](const at::Tensor& v) { return v.scalar_type() == t || v.scalar_type() == at::kFloat; };
+    TORCH_CHECK(t_or_f32(gamma_in) && t_or_f32(res_in), "gamma and residual must be of the input dtype or float32");
+    const bool g32 = gamma_in.scalar_type() == at::kFloat;
+    TORCH_CHECK(g32 || (res_in.scalar_type() == t && !out_float32),
+                "a float32 residual or output needs a float32 gamma");
     TORCH_CHECK(gamma_in.numel() == 1 && gamma_in.is_cuda(), "gamma must be one element on the GPU");
     at::Tensor sp = sp_in.contiguous(), pa = pa_in.contiguous(), w = w_in.contiguous(),
                res = res_in.contiguous(), gm = gamma_in.contiguous();
     c10::DeviceGuard g(res.device());
-    at::Tensor out = at::empty({B, N, n}, res.options());
-    check_status(svtad_adapter_up(sp.numel() ? sp.data_ptr() : nullptr, pa.numel() ? pa.data_ptr() : nullptr,
-                                  w.data_ptr(), opt_ptr(bias, n, res), gm.data_ptr(), res.data_ptr(),
-                                  out.data_ptr(), B, N, S, (int)k, (int)n, dtype_code(res), stream_of(res)),
+    at::Tensor out = at::empty({B, N, n}, res.options().dtype(out_float32 ? at::kFloat : t));
+    const int dt = dtype_code(pa);
+    check_status(svtad_adapter_up_mixed(sp.numel() ? sp.data_ptr() : nullptr, pa.numel() ? pa.data_ptr() : nullptr,
+                                        w.data_ptr(), opt_ptr(bias, n, pa), gm.data_ptr(), res.data_ptr(),
+                                        out.data_ptr(), B, N, S, (int)k, (int)n, dt, dtype_code(gm),
+                                        dtype_code(res), dtype_code(out), stream_of(res)),
                  "adapter_up");
     return out;
 }
@@ -743,23 +755,27 @@ at::Tensor op_heatmap_add_(at::Tensor patch, const at::Tensor& special_in, const
     check_gpu(special_in, "special");
     check_gpu(src_in, "src_rows");
     check_gpu(gate_in, "gate");
-    TORCH_CHECK(special_in.scalar_type() == patch.scalar_type() && gate_in.scalar_type() == patch.scalar_type(),
-                "special, gate and patch must share the dtype");
+    TORCH_CHECK(special_in.scalar_type() == patch.scalar_type() &&
+                    (gate_in.scalar_type() == patch.scalar_type() || gate_in.scalar_type() == at::kFloat),
+                "special and patch must share the dtype; gate is of that dtype or float32");
     const int64_t rows = patch.size(0), cols = patch.size(1);
     TORCH_CHECK(special_in.size(-1) == cols, "special must have ", cols, " columns");
     TORCH_CHECK(src_in.scalar_type() == at::kInt && src_in.numel() == rows, "src_rows must be int32 [rows]");
     TORCH_CHECK(gate_in.numel() == 1, "gate must be one element");
     at::Tensor sp = special_in.contiguous(), src = src_in.contiguous(), gate = gate_in.contiguous();
     c10::DeviceGuard g(patch.device());
-    check_status(svtad_heatmap_add(patch.data_ptr(), sp.numel() ? sp.data_ptr() : nullptr, src.data_ptr<int32_t>(),
-                                   gate.data_ptr(), rows, n_rows(sp), (int)cols, dtype_code(patch), stream_of(patch)),
+    check_status(svtad_heatmap_add_mixed(patch.data_ptr(), sp.numel() ? sp.data_ptr() : nullptr,
+                                         src.data_ptr<int32_t>(), gate.data_ptr(), rows, n_rows(sp), (int)cols,
+                                         dtype_code(patch), dtype_code(gate), stream_of(patch)),
                  "heatmap_add_");
     return patch;
 }
 
-// linear_wgrad(g [*, c_g], rows int32 [n] or empty, x [n, c_x]) -> out [c_g, c_x]
+// linear_wgrad(g [*, c_g], rows int32 [n] or empty, x [n, c_x], out_float32=False) -> out [c_g, c_x]
+// (in x's dtype, or the unrounded fp32 sums with out_float32)
 // (out = g[rows]^T x, or g^T x with the first n rows of g when rows is empty)
-at::Tensor op_linear_wgrad(const at::Tensor& g_in, const at::Tensor& rows_in, const at::Tensor& x_in) {
+at::Tensor op_linear_wgrad(const at::Tensor& g_in, const at::Tensor& rows_in, const at::Tensor& x_in,
+                           bool out_float32) {
     adapter_common(g_in, g_in, "g");
     check_gpu(x_in, "x");
     TORCH_CHECK(x_in.scalar_type() == g_in.scalar_type(), "g and x dtypes differ");
@@ -776,12 +792,12 @@ at::Tensor op_linear_wgrad(const at::Tensor& g_in, const at::Tensor& rows_in, co
     }
     at::Tensor g = g_in.contiguous(), x = x_in.contiguous();
     c10::DeviceGuard guard(x.device());
-    at::Tensor out = at::empty({c_g, c_x}, x.options());
+    at::Tensor out = at::empty({c_g, c_x}, x.options().dtype(out_float32 ? at::kFloat : x.scalar_type()));
     const size_t ws = svtad_linear_wgrad_workspace_bytes(n, (int)c_g, (int)c_x, dtype_code(x));
     at::Tensor work = at::empty({(int64_t)std::max<size_t>(ws, 1)}, x.options().dtype(at::kByte));
-    check_status(svtad_linear_wgrad(g.data_ptr(), with_rows ? rows.data_ptr<int32_t>() : nullptr, x.data_ptr(),
-                                    out.data_ptr(), work.data_ptr(), ws, n, g.size(0), (int)c_g, (int)c_x,
-                                    dtype_code(x), stream_of(x)),
+    check_status(svtad_linear_wgrad_mixed(g.data_ptr(), with_rows ? rows.data_ptr<int32_t>() : nullptr,
+                                          x.data_ptr(), out.data_ptr(), work.data_ptr(), ws, n, g.size(0),
+                                          (int)c_g, (int)c_x, dtype_code(x), dtype_code(out), stream_of(x)),
                  "linear_wgrad");
     return out;
 }
@@ -869,15 +885,19 @@ at::Tensor op_gamma_grad(const at::Tensor& w_in, const at::Tensor& g_in, const c
 // up_proj_grads(w, g, b or None, gs or None, gamma [1]) ->
 //   (grad_gamma [1], w * gamma, g * gamma, gs * gamma or empty): the gamma
 //   gradient and the gamma-scaled tensors of the adapter's up-projection
-//   backward in one pass
+//   backward in one pass. gamma is of w's dtype or float32 (the reference's
+//   autocast training); grad_gamma has gamma's dtype, the scaled tensors w's.
+//   g may be float32 (linear_wgrad's unrounded sums): g * gamma is then its
+//   only rounding.
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> op_up_proj_grads(
     const at::Tensor& w_in, const at::Tensor& g_in, const c10::optional<at::Tensor>& b_in,
     const c10::optional<at::Tensor>& gs_in, const at::Tensor& gamma_in) {
     check_gpu(w_in, "w");
     check_gpu(g_in, "g");
     check_gpu(gamma_in, "gamma");
-    TORCH_CHECK(w_in.scalar_type() == g_in.scalar_type() && gamma_in.scalar_type() == w_in.scalar_type(),
-                "w, g and gamma dtypes differ");
+    TORCH_CHECK((g_in.scalar_type() == w_in.scalar_type() || g_in.scalar_type() == at::kFloat) &&
+                    (gamma_in.scalar_type() == w_in.scalar_type() || gamma_in.scalar_type() == at::kFloat),
+                "g and gamma must be of w's dtype or float32");
     TORCH_CHECK(w_in.scalar_type() == at::kHalf || w_in.scalar_type() == at::kBFloat16,
                 "up_proj_grads takes float16 / bfloat16, got ", w_in.scalar_type());
     TORCH_CHECK(w_in.numel() == g_in.numel() && gamma_in.numel() == 1, "w and g must match; gamma one element");
@@ -892,16 +912,16 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> op_up_proj_grads(
         gs = gs_in->contiguous();
     }
     c10::DeviceGuard guard(w.device());
-    at::Tensor out = at::empty({1}, w.options());
-    at::Tensor w_sc = at::empty_like(w), g_sc = at::empty_like(g);
+    at::Tensor out = at::empty({1}, gm.options());  // the gradient of gamma has gamma's dtype
+    at::Tensor w_sc = at::empty_like(w), g_sc = at::empty_like(g, g.options().dtype(w.scalar_type()));
     at::Tensor gs_sc = b.defined() ? at::empty_like(gs) : at::empty({0}, w.options());
     const size_t wsb = svtad_gamma_grad_workspace_bytes();
     at::Tensor work = at::empty({(int64_t)wsb}, w.options().dtype(at::kByte));
-    check_status(svtad_gamma_grad(w.data_ptr(), g.data_ptr(), w.numel(), b.defined() ? b.data_ptr() : nullptr,
-                                  gs.defined() ? gs.data_ptr() : nullptr, b.defined() ? b.numel() : 0,
-                                  out.data_ptr(), gm.data_ptr(), w_sc.data_ptr(), g_sc.data_ptr(),
-                                  b.defined() ? gs_sc.data_ptr() : nullptr, work.data_ptr(), wsb, dtype_code(w),
-                                  stream_of(w)),
+    check_status(svtad_gamma_grad_mixed(w.data_ptr(), g.data_ptr(), w.numel(), b.defined() ? b.data_ptr() : nullptr,
+                                        gs.defined() ? gs.data_ptr() : nullptr, b.defined() ? b.numel() : 0,
+                                        out.data_ptr(), gm.data_ptr(), w_sc.data_ptr(), g_sc.data_ptr(),
+                                        b.defined() ? gs_sc.data_ptr() : nullptr, work.data_ptr(), wsb,
+                                        dtype_code(w), dtype_code(g), dtype_code(gm), stream_of(w)),
                  "up_proj_grads");
     return {out, w_sc, g_sc, gs_sc};
 }
@@ -976,11 +996,11 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("x"), py::arg("weight"), py::arg("bias"), py::arg("n_special"));
     m.def("adapter_up", &op_adapter_up, "Adapter up_proj on cat(special, patch) * gamma + residual",
           py::arg("a_special"), py::arg("a_patch"), py::arg("weight"), py::arg("bias"), py::arg("gamma"),
-          py::arg("residual"));
+          py::arg("residual"), py::arg("out_float32") = false);
     m.def("heatmap_add_", &op_heatmap_add_, "In place: patch[i] += special[src_rows[i]] * gate (adapter heatmap injection)",
           py::arg("patch"), py::arg("special"), py::arg("src_rows"), py::arg("gate"));
     m.def("linear_wgrad", &op_linear_wgrad, "Linear-layer weight gradient g[rows]^T x (split rows, ordered sum)",
-          py::arg("g"), py::arg("rows"), py::arg("x"));
+          py::arg("g"), py::arg("rows"), py::arg("x"), py::arg("out_float32") = false);
     m.def("column_sums", &op_column_sums, "Column sums of a [rows, cols] matrix (ordered, fp32 accumulation)",
           py::arg("a"));
     m.def("gelu_backward_split", &op_gelu_backward_split,

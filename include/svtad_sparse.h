@@ -141,7 +141,9 @@ int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* we
  * exceed it are rejected with SVTAD_ERR_UNSUPPORTED (square weights up to
  * C = 512 fit). Calls no hipMalloc/hipFree. All calls on one GPU share its
  * array: calls that overlap on one GPU (different streams, or host threads
- * without ordering) race.
+ * without ordering) race. The first call on a device looks up the array's
+ * device address (hipGetSymbolAddress); make that first call eagerly, before
+ * a HIP graph capture of later calls on that device.
  */
 size_t svtad_fwd_noalloc_max_workspace_bytes(void);
 int svtad_fwd_noalloc(const void* x, const int32_t* nbr, const void* weight, const void* bias,
@@ -365,6 +367,27 @@ int svtad_adapter_up(const void* a_special, const void* a_patch, const void* wei
                      void* stream);
 
 /*
+ * svtad_adapter_up with gamma, the residual and the output each in `dtype` or
+ * in SVTAD_F32 (gamma_dtype, residual_dtype, out_dtype): the up projection of
+ * the reference adapter under torch.autocast with float32 parameters
+ * (opentad/cores/train_engine.py:672, vit_sparse_adapter_poguise.py:652-653),
+ * where up_proj runs in the autocast dtype and `* self.gamma` promotes to
+ * float32:
+ *   z[m, :]   = T(c[m, :] W^T + bias)
+ *   p         = float(z) * gamma[0]                 (gamma f32: fp32 product)
+ *             = float(T(float(z) * gamma[0]))       (gamma of dtype)
+ *   out[m, :] = p + float(residual[m, :])           (f32 out: stored as is;
+ *                                                    out of dtype: rounded once)
+ * An f32 residual or output needs an f32 gamma (with gamma, residual and out
+ * all of `dtype` this is svtad_adapter_up). f32 residual and out rows are
+ * n floats, 16-byte aligned. One launch.
+ */
+int svtad_adapter_up_mixed(const void* a_special, const void* a_patch, const void* weight,
+                           const void* bias, const void* gamma, const void* residual, void* out,
+                           int64_t batch, int64_t n_tokens, int64_t n_special, int k, int n, int dtype,
+                           int gamma_dtype, int residual_dtype, int out_dtype, void* stream);
+
+/*
  * A linear layer's weight gradient (the backward of the adapter's nn.Linear
  * layers, vit_sparse_adapter_poguise.py:305,652; PyTorch computes it as
  * grad_out^T @ input):
@@ -380,6 +403,13 @@ size_t svtad_linear_wgrad_workspace_bytes(int64_t n, int c_g, int c_x, int dtype
 int svtad_linear_wgrad(const void* g, const int32_t* rows, const void* x, void* out, void* workspace,
                        size_t workspace_bytes, int64_t n, int64_t n_g_rows, int c_g, int c_x, int dtype,
                        void* stream);
+/* svtad_linear_wgrad with `out` in `dtype` or SVTAD_F32 (out_dtype): the
+ * fp32 sums stored unrounded, for a caller that scales them before rounding
+ * (the adapter's up projection, whose gradient the reference rounds once,
+ * after the gamma scale). */
+int svtad_linear_wgrad_mixed(const void* g, const int32_t* rows, const void* x, void* out, void* workspace,
+                             size_t workspace_bytes, int64_t n, int64_t n_g_rows, int c_g, int c_x, int dtype,
+                             int out_dtype, void* stream);
 
 /*
  * Column sums out[c] = sum_r a[r, c] of a [rows, cols] matrix (the bias
@@ -422,6 +452,19 @@ int svtad_heatmap_add(void* patch, const void* special, const int32_t* src_rows,
                       int64_t rows, int64_t n_special_rows, int cols, int dtype, void* stream);
 
 /*
+ * svtad_heatmap_add with the gate in `dtype` or SVTAD_F32 (gate_dtype). An
+ * f32 gate is the reference chain under torch.autocast with float32
+ * parameters (vit_sparse_adapter_poguise.py:355), where `sampled * gate` and
+ * the add are float32 and SparseConv2d casts the sum to the autocast dtype
+ * (sparse_conv_layer.py:191-202):
+ *   patch[i, c] = T(float(patch[i, c]) + float(special[src_rows[i], c]) * gate[0])
+ * One launch on `stream`.
+ */
+int svtad_heatmap_add_mixed(void* patch, const void* special, const int32_t* src_rows, const void* gate,
+                            int64_t rows, int64_t n_special_rows, int cols, int dtype, int gate_dtype,
+                            void* stream);
+
+/*
  * Gradient of the adapter's gamma, replacing the autograd of `* self.gamma`
  * (vit_sparse_adapter_poguise.py:652-653): out[0] = sum_i w[i] g[i] +
  * sum_j b[j] gs[j], with w the up projection's weight, g = go^T c its
@@ -439,6 +482,21 @@ size_t svtad_gamma_grad_workspace_bytes(void);
 int svtad_gamma_grad(const void* w, const void* g, int64_t count, const void* b, const void* gs,
                      int64_t count_b, void* out, const void* gamma, void* w_scaled, void* g_scaled,
                      void* gs_scaled, void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
+/*
+ * svtad_gamma_grad with g in `dtype` or SVTAD_F32 (g_dtype) and gamma in
+ * `dtype` or SVTAD_F32 (gamma_dtype). An f32 g is the unrounded weight
+ * gradient (svtad_linear_wgrad_mixed with an f32 output): the dot products
+ * use it as is and g_scaled = T(g * gamma) is its single rounding, as the
+ * reference rounds that gradient once. An f32 gamma is the float32 gamma of
+ * the reference's autocast training (vit_sparse_adapter_poguise.py:652-653):
+ * `out` (one element) is written in gamma_dtype. The other scaled copies
+ * stay in `dtype`, each an fp32 product rounded once. Two launches.
+ */
+int svtad_gamma_grad_mixed(const void* w, const void* g, int64_t count, const void* b, const void* gs,
+                           int64_t count_b, void* out, const void* gamma, void* w_scaled, void* g_scaled,
+                           void* gs_scaled, void* workspace, size_t workspace_bytes, int dtype, int g_dtype,
+                           int gamma_dtype, void* stream);
 
 #ifdef __cplusplus
 }
