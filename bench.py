@@ -89,6 +89,26 @@ def pmc_traffic(kernel_key):
     return None
 
 
+def time_kernel(fn, reps, warm=3):
+    """Per-launch duration of a single-kernel call fn(): ``(median, mean)``
+    in ms over ``reps`` launches, each bracketed by its own pair of HIP
+    events on torch's current stream (the stream the extension launches
+    on), so a launch's time includes its dispatch but not the host's."""
+    import torch
+
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for s, e in evs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    t = sorted(s.elapsed_time(e) for s, e in evs)
+    return t[len(t) // 2], sum(t) / len(t)
+
+
 def time_events(fn, reps, warm=3):
     """Average ms per call of fn() from HIP events on torch's current stream,
     the stream the extension launches on."""
@@ -136,6 +156,9 @@ class Problem:
 
     def bwd_in(self):
         return self.ops.bwd_in_packed(self.go, self.table, self.w, self.pb, self.n, C, 0)
+
+    def bwd_in_gemm(self):  # the gathered GEMM of bwd_in alone (no orphan-pass launch)
+        return self.ops.bwd_in_gemm(self.go, self.table, self.pb, C, 0)
 
     def bwd_w(self):
         return self.ops.bwd_w_bias(self.go, self.x, self.table, C, 0, True)
@@ -379,9 +402,12 @@ def large_channel_measure(dev, reps):
     autograd step as config 2 (weight pack, forward with fp32 bias, combined
     backward). Config 4: ViT-L adapter, C = 256 bf16, B2 x T96 x 16x16, top-k
     keeps 10 / 25 / 55 %. Config 5: C = 512 bf16, B4 x T128 x 16x16, ragged
-    per-frame keeps ~ U(5 %, 15 %) (global table). Reported per case: step
-    µs and dense-K TFLOP/s (three GEMM passes of 2 * 9 * N * C^2) as a
-    fraction of the bf16 MFMA peak."""
+    per-frame keeps ~ U(5 %, 15 %) (global table). Reported per case: the
+    table's hit rate E / 9N, step µs, and TFLOP/s as a fraction of the bf16
+    MFMA peak on two bases: dense-K (three GEMM passes of 2 * 9 * N * C^2,
+    the products the implicit GEMM issues, zero rows of missing neighbors
+    included) and useful (2 * E * C^2 per pass, E = valid table entries);
+    and the forward and backward-input gathered GEMMs timed alone."""
     import torch
 
     import eccv26_tad_amd as sv
@@ -406,9 +432,19 @@ def large_channel_measure(dev, reps):
 
         t = time_events(step, reps)
         f = 3 * 2 * 9 * n * c * c
-        row = {"config": name, "channels": c, "n": n, "us": round(t * 1e3, 2),
+        e = int((table >= 0).sum())  # valid (row, offset) entries
+        fu = 3 * 2 * e * c * c
+        pf, pb = ops.pack_weight(w, True, True)
+        t_fwd = time_kernel(lambda: ops.fwd_packed(x, table, w, pf, b, 0, 1), reps)[0]
+        t_bin = time_kernel(lambda: ops.bwd_in_gemm(go, table, pb, c, 0), reps)[0]
+        row = {"config": name, "channels": c, "n": n, "hit_rate": round(e / (9 * n), 4), "us": round(t * 1e3, 2),
                "tflops_9n": round(f / (t * 1e-3) / 1e12, 1),
-               "mfma_frac": round(f / (t * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4)}
+               "mfma_frac": round(f / (t * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4),
+               "tflops_useful": round(fu / (t * 1e-3) / 1e12, 1),
+               "mfma_frac_useful": round(fu / (t * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4),
+               "fwd_us": round(t_fwd * 1e3, 2), "bwd_in_gemm_us": round(t_bin * 1e3, 2),
+               "fwd_mfma_frac_useful": round(2 * e * c * c / (t_fwd * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4),
+               "fwd_mfma_frac_9n": round(2 * 9 * n * c * c / (t_fwd * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4)}
         out.append(row)
         log(f"bench: large-channel {row}")
 
@@ -667,22 +703,29 @@ def main():
     except Exception as exc:  # reported, not fatal
         log(f"bench: graph replay skipped: {exc}")
 
-    # per-pass timing. fwd is one kernel (gathered GEMM); bwd_in adds the
-    # orphan pass; bwd_w is the partial-sum kernel (timed alone through
-    # bwd_w_partials) plus the split reduction; bwd is the step's backward
-    # (bwd_in + bwd_w in one call, the orphan pass inside the reduction). The
-    # roofline names the longer of the two single-kernel timings.
+    # per-pass timing (back-to-back calls). fwd is one kernel (gathered
+    # GEMM); bwd_in adds the orphan-pass launch to its GEMM (bwd_in_gemm);
+    # bwd_w is the partial-sum kernel (bwd_w_partials) plus the split
+    # reduction; bwd is the step's backward (bwd_in + bwd_w in one call, the
+    # orphan pass inside the reduction).
     phases = {p: time_events(getattr(prob, p), max(args.steps, 20))
-              for p in ("pack", "fwd", "bwd_in", "bwd_w", "bwd_w_partials", "bwd")}
-    dom = max(("fwd", "bwd_w_partials"), key=phases.get)
+              for p in ("pack", "fwd", "bwd_in", "bwd_in_gemm", "bwd_w", "bwd_w_partials", "bwd")}
+    # The roofline names the longest single kernel of the step among the
+    # three GEMM-shaped kernels: its duration is the mean over back-to-back
+    # launches between one pair of HIP events (what a kernel trace's
+    # average duration measures); each launch bracketed by its own events
+    # (dispatch latency included) is reported beside it.
+    kernels = {p: phases[p] for p in ("fwd", "bwd_in_gemm", "bwd_w_partials")}
+    isolated = {p: time_kernel(getattr(prob, p), max(args.steps, 50)) for p in kernels}
+    dom = max(kernels, key=kernels.get)
     # algorithmic flops of one GEMM pass: the valid (row, offset) entries E
     # of the table times 2 * C_in * C_out (the dense-K count 9 * N, which
     # includes the products with missing neighbors' zero rows, is reported
     # beside it)
     f_pass = 2 * prob.valid * C * C
     f_pass_9n = 2 * 9 * n * C * C
-    t_dom = phases[dom] * 1e-3
-    by_dom = by["fwd" if dom == "fwd" else "bwd_w"]
+    t_dom = kernels[dom] * 1e-3
+    by_dom = by[{"fwd": "fwd", "bwd_in_gemm": "bwd_in", "bwd_w_partials": "bwd_w"}[dom]]
     mfma_t = f_pass / (MFMA_PEAK_TFLOPS[dname] * 1e12)
     hbm_t = by_dom / (HBM_PEAK_GBS * 1e9)
     if mfma_t >= hbm_t:
@@ -696,13 +739,17 @@ def main():
         roof["basis"] = "useful flops 2*E*C^2 per launch, E = valid table entries"
         roof["achieved_9n"] = round(f_pass_9n / t_dom / 1e12, 3)
         roof["frac_9n"] = round(roof["achieved_9n"] / roof["peak"], 5)
-    key = "k_gg_wideIDF16_Li0" if dom == "fwd" else "k_bw_big"
+    key = {"fwd": "k_gg_wideIDF16_Li0", "bwd_in_gemm": "k_gg_wideIDF16_Li1", "bwd_w_partials": "k_bw_big"}[dom]
     roof["traffic"] = pmc_traffic(key) if abs(args.keep - 0.55) < 1e-9 else None
     if roof["traffic"] is not None:
         roof["traffic_source"] = TRAFFIC_PROFILE
-    roof["kernel"] = {"fwd": "k_gg_wide (forward gathered GEMM)",
+        roof["traffic_algorithmic"] = int(by_dom)
+    roof["kernel"] = {"fwd": "k_gg_wide MODE 0 (forward gathered GEMM)",
+                      "bwd_in_gemm": "k_gg_wide MODE 1 (backward-input gathered GEMM)",
                       "bwd_w_partials": "k_bw_big (backward-weight partial sums)"}[dom]
-    roof["kernel_us"] = round(phases[dom] * 1e3, 2)
+    roof["kernel_us"] = round(kernels[dom] * 1e3, 2)
+    roof["kernel_us_all"] = {p: {"back_to_back": round(v * 1e3, 2),
+                                 "isolated_median": round(isolated[p][0] * 1e3, 2)} for p, v in kernels.items()}
 
     dense = None if args.no_dense else dense_ms(dev, dtype, 20)
 

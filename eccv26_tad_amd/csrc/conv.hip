@@ -258,6 +258,23 @@ extern "C" int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, con
     return launch_status();
 }
 
+extern "C" int svtad_bwd_in_gemm(const void* grad_out, const int32_t* nbr, void* packed_bwd, void* grad_in,
+                                 int64_t n, int c_in, int c_out, int64_t tokens_per_batch, int dtype,
+                                 void* stream) {
+    int st = check_common("bwd_in_gemm", n, c_in, c_out, tokens_per_batch, dtype);
+    if (st) return st;
+    if (!gg_mfma_packed_ok(dtype, n, c_out, c_in))
+        return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_in_gemm: shape/dtype has no packed layout");
+    if (n == 0) return SVTAD_OK;
+    if (!grad_out || !nbr || !packed_bwd || !grad_in) return set_error(SVTAD_ERR_INVALID, "bwd_in_gemm: null pointer");
+    if (!al16(grad_out) || !al16(packed_bwd) || !al16(grad_in))
+        return set_error(SVTAD_ERR_INVALID, "bwd_in_gemm: grad_out, packed weight and grad_in must be 16-byte aligned");
+    uint32_t* flag = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
+    gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in, n, c_out, c_in, tokens_per_batch,
+            nullptr, true, flag, (hipStream_t)stream);
+    return launch_status();
+}
+
 extern "C" size_t svtad_bwd_w_workspace_bytes(int64_t n, int c_in, int c_out, int dtype) {
     if (check_common("bwd_w_workspace_bytes", n, c_in, c_out, 0, dtype)) return 0;
     return plan_bw(n, c_in, c_out, dtype).ws_bytes;

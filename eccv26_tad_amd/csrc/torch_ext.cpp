@@ -257,6 +257,27 @@ at::Tensor op_bwd_in_packed(const at::Tensor& go_in, const at::Tensor& nbr_in, c
     return gi;
 }
 
+// bwd_in_gemm(grad_output, neighbor_indices, packed_bwd, C_in, tokens_per_batch) -> [n, C_in]:
+// backward-input's gathered GEMM alone (timing; equals bwd_in_packed for
+// tables whose entries all have their symmetric partner)
+at::Tensor op_bwd_in_gemm(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& packed,
+                          int64_t c_in, int64_t tpb) {
+    check_gpu(go_in, "grad_output");
+    at::Tensor go = rows_view(go_in);
+    const int64_t n = n_rows(go), c_out = go.size(-1);
+    const int dt = dtype_code(go);
+    TORCH_CHECK(packed.numel() > 0 &&
+                    (size_t)packed.numel() == svtad_bwd_in_workspace_bytes((int)c_in, (int)c_out, dt),
+                "packed_bwd does not match C_in x C_out in grad_output's dtype");
+    at::Tensor nbr = table_i32(nbr_in, n);
+    c10::DeviceGuard g(go.device());
+    at::Tensor gi = at::empty({n, c_in}, go.options());
+    check_status(svtad_bwd_in_gemm(go.data_ptr(), nbr.data_ptr<int32_t>(), packed.data_ptr(), gi.data_ptr(), n,
+                                   (int)c_in, (int)c_out, tpb, dt, stream_of(go)),
+                 "bwd_in_gemm");
+    return gi;
+}
+
 // bwd_w_bias(grad_output, x, neighbor_indices, C_in, tokens_per_batch, with_bias)
 // -> (grad_weight [9, C_in, C_out] in x's dtype, grad_bias [C_out] or empty)
 std::tuple<at::Tensor, at::Tensor> op_bwd_w_bias(const at::Tensor& go_in, const at::Tensor& x_in,
@@ -956,6 +977,8 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.def("bwd_packed", &op_bwd_packed, "bwd_in_packed + bwd_w_bias in one call",
           py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
           py::arg("packed_bwd"), py::arg("C_in"), py::arg("tokens_per_batch"), py::arg("with_bias"));
+    m.def("bwd_in_gemm", &op_bwd_in_gemm, "Backward-input gathered GEMM only (timing)", py::arg("grad_output"),
+          py::arg("neighbor_indices"), py::arg("packed_bwd"), py::arg("C_in"), py::arg("tokens_per_batch"));
     m.def("bwd_w_partials", &op_bwd_w_partials, "Backward-weight partial sums only (timing)",
           py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("C_in"),
           py::arg("tokens_per_batch"), py::arg("with_bias"));

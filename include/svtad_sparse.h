@@ -132,6 +132,17 @@ int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* we
                         int64_t tokens_per_batch, int dtype, void* stream);
 
 /*
+ * Timing entry point (no counterpart in the reference): the gathered GEMM of
+ * svtad_bwd_in_packed alone, without the launch of the pass for entries
+ * whose symmetric partner is absent. grad_in equals svtad_bwd_in_packed's
+ * for tables in which every entry has its partner (every table built from a
+ * keep mask); the kernel still sets the flag in packed_bwd otherwise. For
+ * measuring that kernel's duration by itself. One launch.
+ */
+int svtad_bwd_in_gemm(const void* grad_out, const int32_t* nbr, void* packed_bwd, void* grad_in, int64_t n,
+                      int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream);
+
+/*
  * Allocation-free forward. No counterpart in the reference: for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Computes exactly what svtad_fwd computes,
