@@ -397,7 +397,7 @@ def depthwise_measure(dev, reps, keeps=None):
             "dense_us": round(dense * 1e3, 2), "sweep": rows}
 
 
-def large_channel_measure(dev, reps):
+def large_channel_measure(dev, reps, cases=None):
     """Benchmark configs 4 and 5, the matrix-core path at large widths: the same
     autograd step as config 2 (weight pack, forward with fp32 bias, combined
     backward). Config 4: ViT-L adapter, C = 256 bf16, B2 x T96 x 16x16, top-k
@@ -435,8 +435,8 @@ def large_channel_measure(dev, reps):
         e = int((table >= 0).sum())  # valid (row, offset) entries
         fu = 3 * 2 * e * c * c
         pf, pb = ops.pack_weight(w, True, True)
-        t_fwd = time_kernel(lambda: ops.fwd_packed(x, table, w, pf, b, 0, 1), reps)[0]
-        t_bin = time_kernel(lambda: ops.bwd_in_gemm(go, table, pb, c, 0), reps)[0]
+        t_fwd = time_events(lambda: ops.fwd_packed(x, table, w, pf, b, 0, 1), max(reps, 20))
+        t_bin = time_events(lambda: ops.bwd_in_gemm(go, table, pb, c, 0), max(reps, 20))
         row = {"config": name, "channels": c, "n": n, "hit_rate": round(e / (9 * n), 4), "us": round(t * 1e3, 2),
                "tflops_9n": round(f / (t * 1e-3) / 1e12, 1),
                "mfma_frac": round(f / (t * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4),
@@ -449,12 +449,16 @@ def large_channel_measure(dev, reps):
         log(f"bench: large-channel {row}")
 
     for kr in (0.10, 0.25, 0.55):
+        if cases and f"c4_{int(round(kr * 100)):02d}" not in cases:
+            continue
         gm = torch.Generator().manual_seed(SEED + 2)
         nc = 96 * 16 * 16
         k = math.ceil(kr * nc)
         m = torch.zeros(2, nc, dtype=torch.uint8)
         m.scatter_(1, torch.topk(torch.rand(2, nc, generator=gm), k, dim=1).indices, 1)
         case(f"c4 keep {kr}", m.view(2, 96, 16, 16).to(dev), 256)
+    if cases and "c5" not in cases:
+        return out
     gm = torch.Generator().manual_seed(SEED + 3)
     m = torch.zeros(4 * 128, 256, dtype=torch.uint8)
     for f in range(4 * 128):
@@ -599,6 +603,8 @@ def main():
                          "WRITE_SIZE counters) and exit")
     ap.add_argument("--one-keep", action="store_true",
                     help="with --only depthwise: time the --keep rate alone (for counter runs)")
+    ap.add_argument("--large-cases", default=None,
+                    help="with --only large: comma-separated subset of c4_10,c4_25,c4_55,c5")
     ap.add_argument("--only", choices=("adapter", "prune", "depthwise", "large"), default=None,
                     help="only time the fused adapter or the prune step, print its JSON and exit "
                          "(for kernel traces of those paths)")
@@ -636,7 +642,8 @@ def main():
         print(json.dumps({"depthwise": depthwise_measure(dev, args.steps, keeps)}), flush=True)
         return
     if args.only == "large":
-        print(json.dumps({"large_channel": large_channel_measure(dev, args.steps)}), flush=True)
+        cases = set(args.large_cases.split(",")) if args.large_cases else None
+        print(json.dumps({"large_channel": large_channel_measure(dev, args.steps, cases)}), flush=True)
         return
 
     log(f"bench: building problem keep={args.keep}")
