@@ -1418,9 +1418,10 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bwd_fused(
     }
 }
 
-// The reduction of the partials; with a job (oj.gi != NULL) its workgroups
-// also run the orphan pass of a backward-input computed before it (flag-gated
-// as in k_orphans), which saves that pass a launch of its own.
+// The reduction of the partials; with a job (oj.gi != NULL) its first
+// workgroup also runs the pass for entries without a symmetric partner of a
+// backward-input computed before it (flag-gated as in k_orphans,
+// orphan_exact), which saves that pass a launch of its own.
 template <typename T>
 __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ part,
                                                    const float* __restrict__ part_b, int splits,
@@ -1436,10 +1437,10 @@ __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ par
     else if (gb)
         bw_reduce_bias<T>(((int64_t)blockIdx.x - quad_blocks) * 256 + threadIdx.x, part_b,
                           n_off == 9 ? 2 * splits : splits, c_out, gb);
-    if (!oj.gi || (oj.flag && *oj.flag == 0u)) return;
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < oj.n * 9; e += (int64_t)gridDim.x * 256)
-        orphan_entry<T, false>(e, (const T*)oj.go, oj.nbr, (const T*)oj.w, (T*)oj.gi, oj.n, oj.c_in,
-                               oj.c_out, oj.tpb);
+    if (!oj.gi || (oj.flag && *oj.flag == 0u) || blockIdx.x != 0) return;
+    // the exact pass for entries without a symmetric partner: one workgroup
+    orphan_exact<T, false, 256>((const T*)oj.go, oj.nbr, (const T*)oj.w, (T*)oj.gi, oj.n, oj.c_in, oj.c_out,
+                                oj.tpb);
 }
 
 // ---------------------------------------------------------------------------

@@ -116,9 +116,11 @@ __global__ __launch_bounds__(256) void k_gg_valu(const T* __restrict__ src,
 
 // ---------------------------------------------------------------------------
 // Orphan pass of bwd_in: entries (i,k) -> j whose transpose (j, 8-k) -> i is
-// not in the table are not covered by the transposed gather; add them here
-// (after the gather kernel has stored gi) with atomics. Tables built from a
-// keep mask have none, so the pass only reads the table.
+// not in the table are not covered by the transposed gather; the rows they
+// reach are recomputed here (after the gather kernel has stored gi) by one
+// workgroup, in fp32 with one rounding and a fixed order (orphan_exact).
+// Tables built from a keep mask have none: with the flag the launch returns
+// at once, without it the workgroup only scans the table.
 // ---------------------------------------------------------------------------
 template <typename T, bool DEPTHWISE>
 __global__ __launch_bounds__(256) void k_orphans(const T* __restrict__ go,
@@ -127,8 +129,7 @@ __global__ __launch_bounds__(256) void k_orphans(const T* __restrict__ go,
                                                  int64_t n, int c_in, int c_out, int64_t tpb,
                                                  const uint32_t* __restrict__ flag) {
     if (flag && *flag == 0u) return;  // no entry without a symmetric partner
-    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n * 9; e += (int64_t)gridDim.x * 256)
-        orphan_entry<T, DEPTHWISE>(e, go, nbr, w, gi, n, c_in, c_out, tpb);
+    orphan_exact<T, DEPTHWISE, 256>(go, nbr, w, gi, n, c_in, c_out, tpb);
 }
 
 // ---------------------------------------------------------------------------
@@ -603,8 +604,9 @@ __global__ __launch_bounds__(512) void k_dw_bwd_vec(const T* __restrict__ go, co
 }
 
 // The split reduction of k_dw_bwd_vec's partials (as k_split_reduce, weight
-// then bias from one partial row of 10 c), then the depthwise orphan pass
-// over the whole table when any split's flag word is set.
+// then bias from one partial row of 10 c), then, when any split's flag word
+// is set, the depthwise pass for entries without a symmetric partner in the
+// first workgroup (orphan_exact).
 template <typename T, typename A>
 __global__ __launch_bounds__(1024) void k_dw_bwd_reduce(const A* __restrict__ ws, int64_t count, int splits,
                                                         T* __restrict__ gw, int64_t stride, int64_t count0,
@@ -640,9 +642,8 @@ __global__ __launch_bounds__(1024) void k_dw_bwd_reduce(const A* __restrict__ ws
     }
     int f = 0;
     for (int q = threadIdx.x; q < splits; q += 1024) f |= flags[q] != 0u ? 1 : 0;
-    if (__syncthreads_or(f) == 0) return;
-    for (int64_t q = (int64_t)blockIdx.x * 1024 + threadIdx.x; q < n * 9; q += (int64_t)gridDim.x * 1024)
-        orphan_entry<T, true>(q, go, nbr, w, gi, n, c, c, tpb);
+    if (__syncthreads_or(f) == 0 || blockIdx.x != 0) return;
+    orphan_exact<T, true, 1024>(go, nbr, w, gi, n, c, c, tpb);
 }
 
 // ---------------------------------------------------------------------------
@@ -711,9 +712,8 @@ template <typename T>
 static void launch_orphans(bool dw, const void* go, const int32_t* nbr, const void* w, void* gi,
                            int64_t n, int c_in, int c_out, int64_t tpb, const uint32_t* flag,
                            hipStream_t s) {
-    // with a flag the pass is almost always a no-op: a small grid-stride grid
-    const int64_t blocks = cdiv(n * 9, 256);
-    dim3 grid((unsigned)(flag ? std::min<int64_t>(blocks, 256) : blocks));
+    // one workgroup (the pass is exact and ordered, orphan_exact)
+    dim3 grid(1);
     if (dw)
         hipLaunchKernelGGL((k_orphans<T, true>), grid, dim3(256), 0, s, (const T*)go, nbr,
                            (const T*)w, (T*)gi, n, c_in, c_out, tpb, flag);

@@ -91,8 +91,12 @@ int svtad_fwd(const void* x, const int32_t* nbr, const void* weight, const void*
 
 /*
  * Backward-input: gi[src(i,k),ci] += sum_co go[i,co] * w[k,ci,co], as a
- * scatter-free gather over the transposed table (entries whose transpose is
- * not in the table are added afterwards with atomics).
+ * scatter-free gather over the transposed table. The rows that receive an
+ * entry whose transpose is not in the table ("one-way" entries; none in
+ * tables built from a keep mask) are recomputed afterwards by one
+ * workgroup, in fp32 with one rounding and a fixed order, so the result is
+ * deterministic; with more than 2048 one-way entries they are added with
+ * atomics instead (one rounding each, order unfixed).
  * Replaces `bwd_in` / launch_bwd_in (2d_sparse_v3_bind.cpp:10,
  * 2d_sparse_v3.cu:824-835). gi is fully written (no pre-zeroing needed).
  * `workspace` must hold svtad_bwd_in_workspace_bytes() bytes (may be NULL

@@ -80,3 +80,30 @@ def kaiming_weight(rng: np.random.Generator, ci: int, co: int) -> np.ndarray:
     bound = 1.0 / math.sqrt(fan_in)  # gain*sqrt(3/fan_in) with a=sqrt(5)
     t = rng.uniform(-bound, bound, size=(co, ci, 3, 3)).astype(np.float32)
     return np.ascontiguousarray(t.reshape(co, ci, 9).transpose(2, 1, 0))
+
+
+def assert_rounded_once(got, exact, abs_sum, dt):
+    """got (float16 / bfloat16 / float32) against the exact result (fp64):
+    every element within one unit in the last place of the exact value
+    rounded to got's dtype, plus an fp32 accumulation allowance of 2^-20 x
+    the element's sum of absolute terms (abs_sum): a single rounding of an
+    fp32 sum. Rounding after each of several contributions, as an atomic
+    pass into the 16-bit output does, drifts by more."""
+    import torch
+
+    g = got.detach().cpu().double()
+    ex = torch.from_numpy(np.ascontiguousarray(exact)).double()
+    allow = torch.from_numpy(np.ascontiguousarray(abs_sum)).double() * 2.0 ** -20
+    if dt in (torch.float32, torch.float64):
+        bar = 1e-5 if dt == torch.float32 else 1e-12
+        assert float((g - ex).abs().max()) <= bar * float(ex.abs().max())
+        return
+    mant = 10 if dt == torch.float16 else 7
+    r = ex.to(dt).double()
+    ulp = torch.ldexp(torch.ones_like(r), torch.frexp(r.abs().clamp_min(2.0 ** -14)).exponent - 1 - mant)
+    bad = (g - r).abs() > ulp + allow
+    if bad.any():
+        idx = tuple(int(v) for v in bad.nonzero()[0])
+        print("  off by more than one ulp:", int(bad.sum()), "first at", idx, "got", float(g[idx]), "exact",
+              float(ex[idx]), "ulp", float(ulp[idx]), flush=True)
+    assert not bad.any()

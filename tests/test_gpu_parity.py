@@ -11,6 +11,7 @@ import sys
 import numpy as np
 import pytest
 
+from tests.helpers import assert_rounded_once as _assert_rounded_once
 from tests.helpers import kaiming_weight, random_mask, topk_mask
 
 pytestmark = pytest.mark.gpu
@@ -264,9 +265,29 @@ def test_asymmetric_table_orphans(dev, oracle, dname):
     X, W, G = (_t(a, dev, dt) for a in (x, w, go))
     T = _t(t, dev, _dt("int32"))
     tol = TOL[dname]
+    import torch
+
     assert _err_ok(oracle, _np32(ops.fwd(X, T, W, co, 0)), oracle.fwd(x, t, w), tol, "fwd")
-    assert _err_ok(oracle, _np32(ops.bwd_in(G, T, W, n, ci, 0)), oracle.bwd_in(go, t, w), tol, "bwd_in")
+    gi = ops.bwd_in(G, T, W, n, ci, 0)
+    assert _err_ok(oracle, _np32(gi), oracle.bwd_in(go, t, w), tol, "bwd_in")
     assert _err_ok(oracle, _np32(ops.bwd_w(G, X, T, ci, 0)), oracle.bwd_w(go, x, t), tol, "bwd_w")
+    # rows reached by one-way entries are recomputed in fp32 in a fixed
+    # order and rounded once: two runs agree bit for bit, and every element
+    # is the correctly rounded exact value or one of its two neighbors
+    assert torch.equal(gi, ops.bwd_in(G, T, W, n, ci, 0))
+    _assert_rounded_once(gi, oracle.bwd_in(go, t, w), oracle.bwd_in(np.abs(go), t, np.abs(w)), dt)
+
+
+def _one_way_entries(t):
+    """Entries (i, k) -> j of a global table whose partner (j, 8-k) -> i is absent."""
+    n = t.shape[0]
+    cnt = 0
+    for i in range(n):
+        for k in range(9):
+            j = int(t[i, k])
+            if 0 <= j < n and int(t[j, 8 - k]) != i:
+                cnt += 1
+    return cnt
 
 
 @pytest.mark.parametrize("dname", ["float16", "bfloat16"])
@@ -304,6 +325,18 @@ def test_orphan_flag_wide_path(dev, oracle, c, dname):
     for T, ref in ((Ta, ref_a), (Ts, ref_s)):
         assert _err_ok(oracle, _np32(ops.bwd_in_packed(G, T, W, pb2, n, c, 0)), ref, tol, "bwd_in_packed")
         assert _err_ok(oracle, _np32(ops.bwd_in(G, T, W, n, c, 0)), ref, tol, "bwd_in")
+    # the rows reached by one-way links: one rounding, the same bits on every
+    # run, through each path (packed, per-call, and the combined backward
+    # whose reduction runs the pass)
+    import torch
+
+    a1 = ops.bwd_in_packed(G, Ta, W, pb2, n, c, 0)
+    assert torch.equal(a1, ops.bwd_in_packed(G, Ta, W, pb2, n, c, 0))
+    assert torch.equal(a1, ops.bwd_in(G, Ta, W, n, c, 0))
+    gi, _, _ = ops.bwd_packed(G, X, Ta, W, pb2, c, 0, True)
+    assert torch.equal(gi, a1)
+    go_r, w_r = _rounded(go, dt), _rounded(w, dt)  # what the GPU computed with
+    _assert_rounded_once(a1, oracle.bwd_in(go_r, asym, w_r), oracle.bwd_in(np.abs(go_r), asym, np.abs(w_r)), dt)
 
 
 @pytest.mark.parametrize("ci,co,dname", [(192, 192, "float16"), (64, 64, "bfloat16"),
@@ -685,6 +718,13 @@ def test_depthwise_one_pass_backward(dev, oracle, dname, c, tpb):
     assert _err_ok(oracle, gia.cpu().double().numpy(), oracle.dw_bwd_in(go, asym, w), tol, "gia")
     assert _err_ok(oracle, gwa.cpu().double().numpy(), oracle.dw_bwd_w(go, x, asym), tol, "gwa")
     assert _err_ok(oracle, gba.cpu().double().numpy(), oracle.bias_grad(go), tol, "gba")
+    # the rows reached by the one-way entries: one rounding, the same bits
+    # on every run and through the separate backward-input call
+    n_oneway = _one_way_entries(asym)
+    _say(f"  {n_oneway} one-way entries")
+    assert 0 < n_oneway <= 2048
+    assert torch.equal(gia, ops.dw_bwd(G, X, Ta, W, 0, True)[0])
+    _assert_rounded_once(gia, oracle.dw_bwd_in(go, asym, w), oracle.dw_bwd_in(np.abs(go), asym, np.abs(w)), dt)
     # a symmetric table again after the asymmetric one (flag words rewritten)
     gi4, _, _ = ops.dw_bwd(G, X, T, W, tpb_v, True)
     assert torch.equal(gi4, gi)

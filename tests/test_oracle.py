@@ -252,3 +252,46 @@ def test_prune_step_equals_row_loop_and_closed_form(oracle, seed):
     x2, i2, t2 = oracle.ref_prune_step(x, idx, None, None, S)
     np.testing.assert_array_equal(x2, x_new)
     assert i2 is None and t2 is None
+
+
+@pytest.mark.parametrize("dname", ["float16", "bfloat16"])
+def test_rounded_once_check_rejects_per_contribution_rounding(oracle, dname):
+    """The GPU tests' single-rounding check (helpers.assert_rounded_once),
+    pinned on the CPU: backward-input of a random asymmetric table whose rows
+    receive several contributions, summed in fp32 and rounded once, passes;
+    the same sums rounded to the 16-bit dtype after every contribution (what
+    an atomic pass into the output does) fail."""
+    import torch
+
+    from tests.helpers import assert_rounded_once, kaiming_weight
+
+    dt = getattr(torch, dname)
+    rng = np.random.default_rng(13)
+    n, ci, co = 150, 32, 24
+    t = rng.integers(-1, n, size=(n, 9)).astype(np.int32)
+    t[rng.random((n, 9)) < 0.3] = -1
+
+    def rd(a):
+        return torch.from_numpy(a).to(dt).float().numpy()
+
+    w = rd(kaiming_weight(rng, ci, co))
+    go = rd(rng.standard_normal((n, co)).astype(np.float32))
+    exact = oracle.bwd_in(go, t, w)
+    abs_sum = oracle.bwd_in(np.abs(go), t, np.abs(w))
+    contribs = [[] for _ in range(n)]
+    for i in range(n):
+        for k in range(9):
+            j = int(t[i, k])
+            if 0 <= j < n:
+                contribs[j].append(go[i].astype(np.float32) @ w[k].T.astype(np.float32))
+    once = torch.zeros((n, ci), dtype=dt)
+    each = torch.zeros((n, ci), dtype=dt)
+    for j in range(n):
+        acc = np.zeros(ci, np.float32)
+        for c in contribs[j]:
+            acc = (acc + c).astype(np.float32)
+            each[j] = (each[j].float() + torch.from_numpy(c)).to(dt)
+        once[j] = torch.from_numpy(acc).to(dt)
+    assert_rounded_once(once, exact, abs_sum, dt)
+    with pytest.raises(AssertionError):
+        assert_rounded_once(each, exact, abs_sum, dt)
