@@ -144,6 +144,9 @@ class Problem:
         self.b = ((torch.rand(C, generator=g) * 2 - 1) * bound).to(dev, dtype)
         self.go = torch.randn(self.n, C, generator=g).to(dev, dtype)
         self.valid = int((self.table >= 0).sum())
+        # the builder's symmetric record: the autograd backward passes it to
+        # the backward ops (no partner checks)
+        self.sym = sv.is_symmetric_table(self.table)
 
         self.pf, self.pb = self.ops.pack_weight(self.w, True, True)
 
@@ -155,10 +158,10 @@ class Problem:
         return self.ops.fwd_packed(self.x, self.table, self.w, self.pf, self.b, 0, 1)
 
     def bwd_in(self):
-        return self.ops.bwd_in_packed(self.go, self.table, self.w, self.pb, self.n, C, 0)
+        return self.ops.bwd_in_packed(self.go, self.table, self.w, self.pb, self.n, C, 0, symmetric=self.sym)
 
     def bwd_in_gemm(self):  # the gathered GEMM of bwd_in alone (no orphan-pass launch)
-        return self.ops.bwd_in_gemm(self.go, self.table, self.pb, C, 0)
+        return self.ops.bwd_in_gemm(self.go, self.table, self.pb, C, 0, symmetric=self.sym)
 
     def bwd_w(self):
         return self.ops.bwd_w_bias(self.go, self.x, self.table, C, 0, True)
@@ -167,12 +170,18 @@ class Problem:
         return self.ops.bwd_w_partials(self.go, self.x, self.table, C, 0, True)
 
     def bwd(self):  # the autograd backward: bwd_in + bwd_w in one call
+        return self.ops.bwd_packed(self.go, self.x, self.table, self.w, self.pb, C, 0, True, symmetric=self.sym)
+
+    def bwd_checked(self):  # bwd with the partner checks (a table without the record)
         return self.ops.bwd_packed(self.go, self.x, self.table, self.w, self.pb, C, 0, True)
+
+    def bwd_in_gemm_checked(self):
+        return self.ops.bwd_in_gemm(self.go, self.table, self.pb, C, 0)
 
     def step(self):
         pf, pb = self.ops.pack_weight(self.w, True, True)
         y = self.ops.fwd_packed(self.x, self.table, self.w, pf, self.b, 0, 1)
-        gi, gw, gb = self.ops.bwd_packed(self.go, self.x, self.table, self.w, pb, C, 0, True)
+        gi, gw, gb = self.ops.bwd_packed(self.go, self.x, self.table, self.w, pb, C, 0, True, symmetric=self.sym)
         return y, gi, gw, gb
 
 
@@ -375,15 +384,18 @@ def depthwise_measure(dev, reps, keeps=None):
         b = (torch.rand(C, generator=g) * 0.2 - 0.1).to(dev, torch.float16)
         go = torch.randn(n, C, generator=g).to(dev, torch.float16)
         hit = float((table >= 0).sum()) / (9 * n)
+        sym = sv.is_symmetric_table(table)
 
         def step():  # the calls SparseDepthwiseConv2d's autograd makes
             y = ops.dw_fwd(x, table, w, b, 0)
-            gi, gw, gb = ops.dw_bwd(go, x, table, w, 0, True)
+            gi, gw, gb = ops.dw_bwd(go, x, table, w, 0, True, symmetric=sym)
             return y, gi, gw, gb
 
         t = time_events(step, reps)
-        parts = {"fwd": lambda: ops.dw_fwd(x, table, w, b, 0), "bwd": lambda: ops.dw_bwd(go, x, table, w, 0, True),
-                 "bwd_in": lambda: ops.dw_bwd_in(go, table, w, 0),
+        parts = {"fwd": lambda: ops.dw_fwd(x, table, w, b, 0),
+                 "bwd": lambda: ops.dw_bwd(go, x, table, w, 0, True, symmetric=sym),
+                 "bwd_checked": lambda: ops.dw_bwd(go, x, table, w, 0, True),
+                 "bwd_in": lambda: ops.dw_bwd_in(go, table, w, 0, symmetric=sym),
                  "bwd_w": lambda: ops.dw_bwd_w(go, x, table, 0, True)}
         pt = {k2: round(time_events(f, reps) * 1e3, 2) for k2, f in parts.items()}
         # fwd: x, y, table; bwd_in: go, gi, table; bwd_w: go, x, table; weights and bias
@@ -424,11 +436,12 @@ def large_channel_measure(dev, reps, cases=None):
         w = ((torch.rand(9, c, c, generator=g) * 2 - 1) * bound).to(dev, torch.bfloat16)
         b = ((torch.rand(c, generator=g) * 2 - 1) * bound).to(dev, torch.bfloat16)
         go = torch.randn(n, c, generator=g).to(dev, torch.bfloat16)
+        sym = sv.is_symmetric_table(table)
 
         def step():
             pf, pb = ops.pack_weight(w, True, True)
             y = ops.fwd_packed(x, table, w, pf, b, 0, 1)
-            return y, ops.bwd_packed(go, x, table, w, pb, c, 0, True)
+            return y, ops.bwd_packed(go, x, table, w, pb, c, 0, True, symmetric=sym)
 
         t = time_events(step, reps)
         f = 3 * 2 * 9 * n * c * c
@@ -436,7 +449,7 @@ def large_channel_measure(dev, reps, cases=None):
         fu = 3 * 2 * e * c * c
         pf, pb = ops.pack_weight(w, True, True)
         t_fwd = time_events(lambda: ops.fwd_packed(x, table, w, pf, b, 0, 1), max(reps, 20))
-        t_bin = time_events(lambda: ops.bwd_in_gemm(go, table, pb, c, 0), max(reps, 20))
+        t_bin = time_events(lambda: ops.bwd_in_gemm(go, table, pb, c, 0, symmetric=sym), max(reps, 20))
         row = {"config": name, "channels": c, "n": n, "hit_rate": round(e / (9 * n), 4), "us": round(t * 1e3, 2),
                "tflops_9n": round(f / (t * 1e-3) / 1e12, 1),
                "mfma_frac": round(f / (t * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS["bf16"], 4),
@@ -714,9 +727,11 @@ def main():
     # GEMM); bwd_in adds the orphan-pass launch to its GEMM (bwd_in_gemm);
     # bwd_w is the partial-sum kernel (bwd_w_partials) plus the split
     # reduction; bwd is the step's backward (bwd_in + bwd_w in one call, the
-    # orphan pass inside the reduction).
+    # orphan pass inside the reduction); the *_checked passes are the same
+    # calls without the table's symmetric record (partner checks on).
     phases = {p: time_events(getattr(prob, p), max(args.steps, 20))
-              for p in ("pack", "fwd", "bwd_in", "bwd_in_gemm", "bwd_w", "bwd_w_partials", "bwd")}
+              for p in ("pack", "fwd", "bwd_in", "bwd_in_gemm", "bwd_w", "bwd_w_partials", "bwd", "bwd_checked",
+                        "bwd_in_gemm_checked")}
     # The roofline names the longest single kernel of the step among the
     # three GEMM-shaped kernels: its duration is the mean over back-to-back
     # launches between one pair of HIP events (what a kernel trace's

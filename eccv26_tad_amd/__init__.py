@@ -38,6 +38,8 @@ from .neighbor import (  # noqa: E402
     build_neighbor_table,
     get_initial_neighbor_indices,
     global_neighbor_table,
+    is_symmetric_table,
+    mark_symmetric_table,
     prune_tokens,
     set_debug_sparse,
     remap_neighbor_table,
@@ -67,6 +69,7 @@ __all__ = [
     "SparseDepthwiseConv2d", "SparseDepthwiseConv2dFunction",
     "build_neighbor_table", "get_initial_neighbor_indices", "prune_tokens", "remap_neighbor_table",
     "transpose_neighbor_table", "validate_neighbor_table", "global_neighbor_table", "set_debug_sparse",
+    "is_symmetric_table", "mark_symmetric_table",
     "remap_legacy_sparse_conv_weights",
     "dense_conv_tokens", "keep_mask_from_indices", "sparse_weight_from_conv2d",
     "conv2d_weight_from_sparse", "SparseConvAdapter", "AdapterDownFunction", "AdapterUpFunction", "SparseConvAdapterFunction",

@@ -94,7 +94,7 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import opentad_sparse_ops as _ops
-from .neighbor import global_neighbor_table
+from .neighbor import _keep_symmetric, global_neighbor_table, is_symmetric_table
 from .sparse_conv_layer import (BIAS_AFTER, BIAS_FP32, BIAS_NONE, IMPLICIT_GEMM_MIN_CIN, SparseConv2d)
 
 _FUSED_DTYPES = (torch.float16, torch.bfloat16)
@@ -257,6 +257,7 @@ class SparseConvAdapterFunction(Function):
     def forward(ctx, x, w_d, b_d, w_c, b_c, w_u, b_u, gamma, nbr, n_special, tpb, hm_rows=None, hm_gate=None,
                 packed=None, cd=None):
         S = int(n_special)
+        ctx.symmetric = is_symmetric_table(nbr)
         cd = x.dtype if cd is None else cd
         # autocast's casts (none when everything is already in cd); gamma and
         # the heatmap gate keep their dtype, as in the reference chain
@@ -310,7 +311,8 @@ class SparseConvAdapterFunction(Function):
         g_pa = dc[:, S:].reshape(-1, k)
         # SparseConv2D
         need_bc = b_c is not None and need[4]
-        gi_pa, gw_c, gb_c = _ops.bwd_packed(g_pa, pa, nbr, w_c, pb, w_c.shape[1], tpb, need_bc)
+        gi_pa, gw_c, gb_c = _ops.bwd_packed(g_pa, pa, nbr, w_c, pb, w_c.shape[1], tpb, need_bc,
+                                            symmetric=ctx.symmetric)
         g_gate = None
         if hm_rows is not None:
             # backward of patches + special[hm_rows] * gate: the gather's
@@ -472,6 +474,7 @@ class SparseConvAdapter(nn.Module):
             nbr = neighbor_indices.reshape(-1, 9)
             if nbr.dtype != torch.int32:
                 nbr = nbr.to(torch.int32)
+            nbr = _keep_symmetric(neighbor_indices, nbr)
         conv = self.sparse_conv
         if not self.use_attn:
             hm_rows = hm_gate = None

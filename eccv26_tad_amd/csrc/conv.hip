@@ -236,10 +236,28 @@ extern "C" int svtad_fwd_packed(const void* x, const int32_t* nbr, const void* p
     return launch_status();
 }
 
+// table_flags of the *_ex entry points: only SVTAD_TABLE_SYMMETRIC is defined
+static int check_table_flags(const char* what, unsigned flags) {
+    if (flags & ~(unsigned)SVTAD_TABLE_SYMMETRIC) {
+        char msg[96];
+        snprintf(msg, sizeof msg, "%s: unknown table_flags bits 0x%x", what, flags);
+        return set_error(SVTAD_ERR_INVALID, msg);
+    }
+    return SVTAD_OK;
+}
+
 extern "C" int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* weight,
                                    void* packed_bwd, void* grad_in, int64_t n, int c_in,
                                    int c_out, int64_t tokens_per_batch, int dtype, void* stream) {
+    return svtad_bwd_in_packed_ex(grad_out, nbr, weight, packed_bwd, grad_in, n, c_in, c_out, tokens_per_batch,
+                                  dtype, 0u, stream);
+}
+
+extern "C" int svtad_bwd_in_packed_ex(const void* grad_out, const int32_t* nbr, const void* weight,
+                                      void* packed_bwd, void* grad_in, int64_t n, int c_in, int c_out,
+                                      int64_t tokens_per_batch, int dtype, unsigned table_flags, void* stream) {
     int st = check_common("bwd_in_packed", n, c_in, c_out, tokens_per_batch, dtype);
+    if (!st) st = check_table_flags("bwd_in_packed", table_flags);
     if (st) return st;
     if (!gg_mfma_packed_ok(dtype, n, c_out, c_in))
         return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_in_packed: shape/dtype has no packed layout");
@@ -251,17 +269,21 @@ extern "C" int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, con
     hipStream_t s = (hipStream_t)stream;
     // the orphan flag follows the packed layout (cleared by svtad_pack_weight)
     uint32_t* flag = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
+    const bool sym = table_flags & SVTAD_TABLE_SYMMETRIC;
     const bool flagged = gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in,
-                                 n, c_out, c_in, tokens_per_batch, nullptr, true, flag, s);
-    orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch,
-            flagged ? flag : nullptr, s);
+                                 n, c_out, c_in, tokens_per_batch, nullptr, true, flag, s, sym);
+    // a symmetric table has no entries without a partner: no pass for them
+    if (!sym)
+        orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch,
+                flagged ? flag : nullptr, s);
     return launch_status();
 }
 
 extern "C" int svtad_bwd_in_gemm(const void* grad_out, const int32_t* nbr, void* packed_bwd, void* grad_in,
                                  int64_t n, int c_in, int c_out, int64_t tokens_per_batch, int dtype,
-                                 void* stream) {
+                                 unsigned table_flags, void* stream) {
     int st = check_common("bwd_in_gemm", n, c_in, c_out, tokens_per_batch, dtype);
+    if (!st) st = check_table_flags("bwd_in_gemm", table_flags);
     if (st) return st;
     if (!gg_mfma_packed_ok(dtype, n, c_out, c_in))
         return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_in_gemm: shape/dtype has no packed layout");
@@ -271,7 +293,7 @@ extern "C" int svtad_bwd_in_gemm(const void* grad_out, const int32_t* nbr, void*
         return set_error(SVTAD_ERR_INVALID, "bwd_in_gemm: grad_out, packed weight and grad_in must be 16-byte aligned");
     uint32_t* flag = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
     gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in, n, c_out, c_in, tokens_per_batch,
-            nullptr, true, flag, (hipStream_t)stream);
+            nullptr, true, flag, (hipStream_t)stream, table_flags & SVTAD_TABLE_SYMMETRIC);
     return launch_status();
 }
 
@@ -323,7 +345,16 @@ extern "C" int svtad_bwd_packed(const void* grad_out, const void* x, const int32
                                 void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n,
                                 int c_in, int c_out, int64_t tokens_per_batch, int dtype,
                                 void* stream) {
+    return svtad_bwd_packed_ex(grad_out, x, nbr, weight, packed_bwd, grad_in, grad_w, grad_bias, workspace,
+                               workspace_bytes, n, c_in, c_out, tokens_per_batch, dtype, 0u, stream);
+}
+
+extern "C" int svtad_bwd_packed_ex(const void* grad_out, const void* x, const int32_t* nbr, const void* weight,
+                                   void* packed_bwd, void* grad_in, void* grad_w, void* grad_bias, void* workspace,
+                                   size_t workspace_bytes, int64_t n, int c_in, int c_out,
+                                   int64_t tokens_per_batch, int dtype, unsigned table_flags, void* stream) {
     int st = check_common("bwd_packed", n, c_in, c_out, tokens_per_batch, dtype);
+    if (!st) st = check_table_flags("bwd_packed", table_flags);
     if (st) return st;
     if (!gg_mfma_packed_ok(dtype, n, c_out, c_in))
         return set_error(SVTAD_ERR_UNSUPPORTED, "bwd_packed: shape/dtype has no packed layout");
@@ -337,11 +368,12 @@ extern "C" int svtad_bwd_packed(const void* grad_out, const void* x, const int32
     if (workspace_bytes < p.ws_bytes)
         return set_error(SVTAD_ERR_WORKSPACE, "bwd_packed: workspace smaller than svtad_bwd_w_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;
+    const bool sym = table_flags & SVTAD_TABLE_SYMMETRIC;
     // grad_in and the partials in one launch where neither fills the chip
     if (p.path == 1 && n > 0) {
         uint32_t* f = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
         st = bwd_fused_mfma(dtype, p, grad_out, x, nbr, weight, packed_bwd, f, grad_in, grad_w, grad_bias,
-                            workspace, workspace_bytes, n, c_in, c_out, tokens_per_batch, s);
+                            workspace, workspace_bytes, n, c_in, c_out, tokens_per_batch, s, sym);
         if (st < 0) return st;
         if (st == 1) return launch_status();
     }
@@ -350,20 +382,21 @@ extern "C" int svtad_bwd_packed(const void* grad_out, const void* x, const int32
     if (n > 0) {
         uint32_t* f = (uint32_t*)((char*)packed_bwd + gg_mfma_workspace(dtype, c_out, c_in));
         if (gg_mfma(dtype, MODE_BWDIN, grad_out, nbr, packed_bwd, nullptr, 0, grad_in, n, c_out,
-                    c_in, tokens_per_batch, nullptr, true, f, s))
+                    c_in, tokens_per_batch, nullptr, true, f, s, sym))
             flag = f;
     }
     // 2. grad_w / grad_bias; the reduction also runs the orphan pass of step 1
+    // (none for a symmetric table)
     const OrphanJob job{grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, flag};
     bool taken = false;
     if (p.path == 1) {
         st = bw_mfma(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, workspace_bytes, n, c_in, c_out,
-                     tokens_per_batch, n > 0 ? &job : nullptr, &taken, s);
+                     tokens_per_batch, n > 0 && !sym ? &job : nullptr, &taken, s);
         if (st) return st;
     } else
         bw_valu(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c_in, c_out,
                 tokens_per_batch, s);
-    if (n > 0 && !taken)
+    if (n > 0 && !taken && !sym)
         orphans(dtype, false, grad_out, nbr, weight, grad_in, n, c_in, c_out, tokens_per_batch, flag, s);
     return launch_status();
 }
@@ -382,14 +415,22 @@ extern "C" int svtad_dw_fwd(const void* x, const int32_t* nbr, const void* weigh
 extern "C" int svtad_dw_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight,
                                void* grad_in, int64_t n, int c, int64_t tokens_per_batch, int dtype,
                                void* stream) {
+    return svtad_dw_bwd_in_ex(grad_out, nbr, weight, grad_in, n, c, tokens_per_batch, dtype, 0u, stream);
+}
+
+extern "C" int svtad_dw_bwd_in_ex(const void* grad_out, const int32_t* nbr, const void* weight, void* grad_in,
+                                  int64_t n, int c, int64_t tokens_per_batch, int dtype, unsigned table_flags,
+                                  void* stream) {
     int st = check_common("dw_bwd_in", n, c, c, tokens_per_batch, dtype);
+    if (!st) st = check_table_flags("dw_bwd_in", table_flags);
     if (st) return st;
     if (n == 0) return SVTAD_OK;
     if (!grad_out || !nbr || !weight || !grad_in)
         return set_error(SVTAD_ERR_INVALID, "dw_bwd_in: null pointer");
     hipStream_t s = (hipStream_t)stream;
-    dw_gather(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, grad_in, n, c, tokens_per_batch, s);
-    orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, nullptr, s);
+    const bool sym = table_flags & SVTAD_TABLE_SYMMETRIC;
+    dw_gather(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, grad_in, n, c, tokens_per_batch, s, sym);
+    if (!sym) orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, nullptr, s);
     return launch_status();
 }
 
@@ -405,7 +446,16 @@ extern "C" size_t svtad_dw_bwd_workspace_bytes(int64_t n, int c, int dtype) {
 extern "C" int svtad_dw_bwd(const void* grad_out, const void* x, const int32_t* nbr, const void* weight,
                             void* grad_in, void* grad_w, void* grad_bias, void* workspace, size_t workspace_bytes,
                             int64_t n, int c, int64_t tokens_per_batch, int dtype, void* stream) {
+    return svtad_dw_bwd_ex(grad_out, x, nbr, weight, grad_in, grad_w, grad_bias, workspace, workspace_bytes, n, c,
+                           tokens_per_batch, dtype, 0u, stream);
+}
+
+extern "C" int svtad_dw_bwd_ex(const void* grad_out, const void* x, const int32_t* nbr, const void* weight,
+                               void* grad_in, void* grad_w, void* grad_bias, void* workspace, size_t workspace_bytes,
+                               int64_t n, int c, int64_t tokens_per_batch, int dtype, unsigned table_flags,
+                               void* stream) {
     int st = check_common("dw_bwd", n, c, c, tokens_per_batch, dtype);
+    if (!st) st = check_table_flags("dw_bwd", table_flags);
     if (st) return st;
     const BwPlan p = plan_dw_bw(n, c, dtype);
     if (!grad_w || !workspace || !weight || (n > 0 && (!grad_out || !x || !nbr || !grad_in)))
@@ -414,13 +464,14 @@ extern "C" int svtad_dw_bwd(const void* grad_out, const void* x, const int32_t* 
         return set_error(SVTAD_ERR_WORKSPACE, "dw_bwd: workspace smaller than svtad_dw_bwd_workspace_bytes()");
     hipStream_t s = (hipStream_t)stream;
     uint32_t* flags = (uint32_t*)((char*)workspace + cdiv(p.ws_bytes, 16) * 16);
+    const bool sym = table_flags & SVTAD_TABLE_SYMMETRIC;
     if (n > 0 && dw_bwd_fused(dtype, p, grad_out, x, nbr, weight, grad_in, grad_w, grad_bias, workspace, flags, n,
-                              c, tokens_per_batch, s))
+                              c, tokens_per_batch, s, sym))
         return launch_status();
     // shapes / alignments the one-pass kernels do not take: the two passes
     if (n > 0) {
-        dw_gather(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, grad_in, n, c, tokens_per_batch, s);
-        orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, nullptr, s);
+        dw_gather(dtype, MODE_BWDIN, grad_out, nbr, weight, nullptr, grad_in, n, c, tokens_per_batch, s, sym);
+        if (!sym) orphans(dtype, true, grad_out, nbr, weight, grad_in, n, c, c, tokens_per_batch, nullptr, s);
     }
     dw_bw(dtype, p, grad_out, x, nbr, grad_w, grad_bias, workspace, n, c, tokens_per_batch, s);
     return launch_status();

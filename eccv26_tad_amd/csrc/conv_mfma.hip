@@ -265,7 +265,7 @@ template <typename T, int MODE, int CR, int FM, int FN, int D, int WS>
 __device__ __forceinline__ void gg_wide_tile(
     GgWideLds<CR, FM, FN, WS>& L, int64_t tile, const T* __restrict__ src, const int32_t* __restrict__ nbr,
     const T* __restrict__ wb, const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n,
-    int n_out, int64_t tpb, int n_col_tiles, uint32_t* __restrict__ orphan_flag) {
+    int n_out, int64_t tpb, int n_col_tiles, uint32_t* __restrict__ orphan_flag, bool sym) {
     constexpr int BM = FM * 16;
     constexpr int BN = 4 * FN * 16;
     constexpr int NC = CR / KS;
@@ -314,8 +314,12 @@ __device__ __forceinline__ void gg_wide_tile(
     for (int q = 0; q < TPER; ++q) {
         const int e = tid + q * NT;
         tv[q] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_tab, e < tile_ents ? (uint32_t)(row0 * 9 + e) * 4u : kOOB, 0, 0);
+        pv[q] = -1;
     }
-    if (MODE != MODE_FWD) {
+    // sym: the caller's promise that every entry has its partner (as in every
+    // table built from a keep mask), so no partner loads, and the row offsets
+    // wait for one round trip to memory instead of two
+    if (MODE != MODE_FWD && !sym) {
 #pragma unroll
         for (int q = 0; q < TPER; ++q) {
             const int e = tid + q * NT;
@@ -367,7 +371,7 @@ __device__ __forceinline__ void gg_wide_tile(
                     // (i, 8-k) -> p, accepted when its partner (p, k) -> i
                     // exists; one without a partner is left to the orphan
                     // pass, which the flag arms
-                    if (src_of(pv[q], p) == i) r = p;
+                    if (sym || src_of(pv[q], p) == i) r = p;
                     else if (orphan_flag) *orphan_flag = 1u;
                 }
             }
@@ -652,10 +656,10 @@ template <typename T, int MODE, int CR, int FM, int FN, int D, int WS>
 __global__ __launch_bounds__(256 * WS) void k_gg_wide(
     const T* __restrict__ src, const int32_t* __restrict__ nbr, const T* __restrict__ wb,
     const void* __restrict__ bias, int bias_mode, T* __restrict__ out, int64_t n, int n_out,
-    int64_t tpb, int n_col_tiles, int64_t n_tiles, uint32_t* __restrict__ orphan_flag) {
+    int64_t tpb, int n_col_tiles, int64_t n_tiles, uint32_t* __restrict__ orphan_flag, bool sym) {
     __shared__ GgWideLds<CR, FM, FN, WS> lds;
     gg_wide_tile<T, MODE, CR, FM, FN, D, WS>(lds, xcd_tile(blockIdx.x, n_tiles), src, nbr, wb, bias, bias_mode,
-                                             out, n, n_out, tpb, n_col_tiles, orphan_flag);
+                                             out, n, n_out, tpb, n_col_tiles, orphan_flag, sym);
 }
 
 // Weight in MFMA fragment order for the gathered GEMMs. For reduction step cs
@@ -1402,7 +1406,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bwd_fused(
     const T* __restrict__ go, const int32_t* __restrict__ nbr, const T* __restrict__ wb, T* __restrict__ gi,
     int n_in, int n_col_tiles, uint32_t* __restrict__ orphan_flag, const T* __restrict__ x,
     float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n, int64_t tpb, int64_t rows_per_split,
-    int n_ci_tiles, int n_co_tiles, int64_t n_bw, int64_t n_blocks) {
+    int n_ci_tiles, int n_co_tiles, int64_t n_bw, int64_t n_blocks, bool sym) {
     typedef GgWideLds<CR, GFM, GFN, GWS> GL;
     typedef BwBigLds<FM, FN, WGM, WGN> BL;
     static_assert(256 * GWS <= bw_big_threads(FM, FN, WGM, WGN), "tile role threads");
@@ -1414,7 +1418,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bwd_fused(
     } else {
         if (threadIdx.x >= 256 * GWS) return;
         gg_wide_tile<T, MODE_BWDIN, CR, GFM, GFN, GD, GWS>(*(GL*)lds, lin - n_bw, go, nbr, wb, nullptr, 0, gi, n,
-                                                         n_in, tpb, n_col_tiles, orphan_flag);
+                                                         n_in, tpb, n_col_tiles, orphan_flag, sym);
     }
 }
 
@@ -1500,7 +1504,7 @@ int cu_count() {
 template <typename T, int MODE, int CR, int FM, int FN, int D>
 static void launch_wide(const void* src, const int32_t* nbr, const void* wb, const void* bias,
                         int bias_mode, void* out, int64_t n, int n_out, int64_t tpb, uint32_t* flag,
-                        hipStream_t s) {
+                        bool sym, hipStream_t s) {
     constexpr int BN = 4 * FN * 16;
     // two wave sets (two waves per SIMD, at most 256 registers each) when
     // their LDS fits and the accumulators, weight ring and row fragments
@@ -1513,7 +1517,7 @@ static void launch_wide(const void* src, const int32_t* nbr, const void* wb, con
     const int64_t tiles = cdiv(n, 16 * FM) * n_col;
     hipLaunchKernelGGL((k_gg_wide<T, MODE, CR, FM, FN, D, WS>), dim3((unsigned)tiles), dim3(256 * WS),
                        0, s, (const T*)src, nbr, (const T*)wb, bias, bias_mode, (T*)out, n, n_out,
-                       tpb, n_col, tiles, flag);
+                       tpb, n_col, tiles, flag, sym);
 }
 
 // Row fragments per workgroup. The kernels hold one workgroup per CU
@@ -1536,7 +1540,7 @@ static int pick_fm(int64_t n, int n_col, const int* have, int count) {
 template <typename T, int MODE, int CR, int FN, int D>
 static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, const void* bias,
                            int bias_mode, void* out, int64_t n, int n_out, int64_t tpb,
-                           uint32_t* flag, hipStream_t s) {
+                           uint32_t* flag, bool sym, hipStream_t s) {
     const int n_col = (int)cdiv(n_out, 4 * FN * 16);
     if constexpr (CR == 192 || CR == 256) {
         // at CR = 256, FM = 8 leaves room for one wave set only (one wave per
@@ -1550,7 +1554,7 @@ static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, 
             // a third of the weight and the grid holds about as many tiles
             // (measured 10.8 -> 8.2 us at 3136 rows, 14.4 -> 11.5 us at 7840).
             if (fm <= 2) {
-                launch_wide<T, MODE, CR, 3, 1, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
+                launch_wide<T, MODE, CR, 3, 1, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
                 return;
             }
         }
@@ -1558,25 +1562,25 @@ static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, 
             // the same at C = 256: 128-column tiles of three row fragments
             // (measured 14.4 -> 11.7 us at 4916 rows)
             if (fm <= 2) {
-                launch_wide<T, MODE, CR, 3, 2, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
+                launch_wide<T, MODE, CR, 3, 2, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
                 return;
             }
         }
         switch (fm) {
-            case 1: launch_wide<T, MODE, CR, 1, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
-            case 2: launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
-            case 3: launch_wide<T, MODE, CR, 3, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
-            case 4: launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
-            case 5: launch_wide<T, MODE, CR, 5, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
-            case 6: launch_wide<T, MODE, CR, 6, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
-            default: launch_wide<T, MODE, CR, 8, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); return;
+            case 1: launch_wide<T, MODE, CR, 1, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); return;
+            case 2: launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); return;
+            case 3: launch_wide<T, MODE, CR, 3, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); return;
+            case 4: launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); return;
+            case 5: launch_wide<T, MODE, CR, 5, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); return;
+            case 6: launch_wide<T, MODE, CR, 6, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); return;
+            default: launch_wide<T, MODE, CR, 8, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); return;
         }
     } else {
         static const int have[] = {2, 4};
         if (pick_fm(n, n_col, have, 2) == 2)
-            launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
+            launch_wide<T, MODE, CR, 2, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
         else
-            launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s);
+            launch_wide<T, MODE, CR, 4, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
     }
 }
 
@@ -1584,7 +1588,7 @@ static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, 
 template <typename T, int MODE>
 static bool gg_dispatch(const void* src, const int32_t* nbr, const void* w, const void* bias,
                         int bias_mode, void* out, int64_t n, int c_red, int n_out, int64_t tpb,
-                        void* ws, bool prepacked, uint32_t* flag, hipStream_t s) {
+                        void* ws, bool prepacked, uint32_t* flag, bool sym, hipStream_t s) {
     const WideCfg* wc = wide_cfg(c_red, n_out);
     // buffer loads address operands with 32-bit byte offsets
     const bool fits = n * c_red * 2 < (int64_t)INT32_MAX && 9LL * c_red * n_out * 2 < (int64_t)INT32_MAX;
@@ -1598,7 +1602,7 @@ static bool gg_dispatch(const void* src, const int32_t* nbr, const void* w, cons
         }
 #define SVTAD_WIDE_CASE(CR, FM, FN, D)                                                           \
     if (wc->cr == CR) {                                                                          \
-        launch_wide_fm<T, MODE, CR, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, s); \
+        launch_wide_fm<T, MODE, CR, FN, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s); \
         return flag != nullptr;                                                                  \
     }
         SVTAD_WIDE_CASE(64, 8, 1, 2)
@@ -1621,13 +1625,13 @@ static bool gg_dispatch(const void* src, const int32_t* nbr, const void* w, cons
 
 bool gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
-             int64_t tpb, void* ws, bool prepacked, uint32_t* orphan_flag, hipStream_t s) {
+             int64_t tpb, void* ws, bool prepacked, uint32_t* orphan_flag, hipStream_t s, bool sym) {
     if (dtype == SVTAD_F16) {
-        if (mode == MODE_FWD) return gg_dispatch<f16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, nullptr, s);
-        return gg_dispatch<f16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, orphan_flag, s);
+        if (mode == MODE_FWD) return gg_dispatch<f16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, nullptr, false, s);
+        return gg_dispatch<f16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, orphan_flag, sym, s);
     }
-    if (mode == MODE_FWD) return gg_dispatch<bf16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, nullptr, s);
-    return gg_dispatch<bf16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, orphan_flag, s);
+    if (mode == MODE_FWD) return gg_dispatch<bf16, MODE_FWD>(src, nbr, w, bias, bias_mode, out, n, c_red, n_out, tpb, ws, prepacked, nullptr, false, s);
+    return gg_dispatch<bf16, MODE_BWDIN>(src, nbr, w, nullptr, 0, out, n, c_red, n_out, tpb, ws, prepacked, orphan_flag, sym, s);
 }
 
 bool gg_mfma_packed_ok(int dtype, int64_t n, int c_red, int n_out) {
@@ -1838,12 +1842,12 @@ static int fused_env(FusedChoice* c) {
 template <typename T, int C, int GFM, int GFN, int BFM, int BFN, int BWM, int BWN>
 static void launch_fused(const void* go, const int32_t* nbr, const void* wb, void* gi, uint32_t* flag,
                          const void* x, float* part, float* part_b, int64_t n, int64_t tpb, int64_t rps,
-                         int64_t n_gg, int64_t n_bw, hipStream_t s) {
+                         int64_t n_gg, int64_t n_bw, bool sym, hipStream_t s) {
     constexpr int NCI = C / (16 * BWM * BFM), NCO = C / (16 * BWN * BFN);
     static_assert(NCI * 16 * BWM * BFM == C && NCO * 16 * BWN * BFN == C, "whole tiles");
     hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, BFM, BFN, BWM, BWN>), dim3((unsigned)(n_gg + n_bw)),
                        dim3(bw_big_threads(BFM, BFN, BWM, BWN)), 0, s, (const T*)go, nbr, (const T*)wb, (T*)gi, C,
-                       C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, NCI, NCO, n_bw, n_gg + n_bw);
+                       C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, NCI, NCO, n_bw, n_gg + n_bw, sym);
 }
 
 // Units per split of the one-launch backward's large-tile configuration at
@@ -1926,7 +1930,8 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
 
 int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, const int32_t* nbr,
                    const void* w, const void* packed_bwd, uint32_t* flag, void* gi, void* gw, void* gb,
-                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s) {
+                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s,
+                   bool sym) {
     if (!aligned16(go) || !aligned16(x) || !aligned16(packed_bwd) || !aligned16(gi)) return 0;
     FusedChoice ch{0, 0, 0};
     BwPlan p;
@@ -1945,10 +1950,10 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
         launched = true;                                                                                  \
         if (dtype == SVTAD_F16)                                                                           \
             launch_fused<f16, C, FM, FN, BFM, BFN, BWM, BWN>(go, nbr, packed_bwd, gi, flag, x, part,     \
-                                                             part_b, n, tpb, p.rows_per_split, gg, bw, s); \
+                                                             part_b, n, tpb, p.rows_per_split, gg, bw, sym, s); \
         else                                                                                              \
             launch_fused<bf16, C, FM, FN, BFM, BFN, BWM, BWN>(go, nbr, packed_bwd, gi, flag, x, part,    \
-                                                              part_b, n, tpb, p.rows_per_split, gg, bw, s); \
+                                                              part_b, n, tpb, p.rows_per_split, gg, bw, sym, s); \
     }
     SVTAD_FUSED_CASE(192, 3, 1, 6, 3, 2, 4)
     SVTAD_FUSED_CASE(192, 3, 3, 6, 3, 2, 4)

@@ -336,7 +336,7 @@ template <typename T> struct Vec16 {
 template <typename T, int MODE>
 __global__ __launch_bounds__(256) void k_dw_vec(const T* __restrict__ src, const int32_t* __restrict__ nbr,
                                                 const T* __restrict__ w, const T* __restrict__ bias,
-                                                T* __restrict__ out, int64_t n, int c, int64_t tpb) {
+                                                T* __restrict__ out, int64_t n, int c, int64_t tpb, bool sym) {
     constexpr int VEC = Vec16<T>::N;
     typedef typename Acc<T>::type A;
     const int cpr = c / VEC;
@@ -362,8 +362,9 @@ __global__ __launch_bounds__(256) void k_dw_vec(const T* __restrict__ src, const
         int64_t r = tv[k] >= 0 ? (int64_t)tv[k] + shift : -1;
         if (r >= n) r = -1;
         // backward-input gathers row r through offset k only when r's entry
-        // (r, k) points back to i (the transposed table, as src_row_t)
-        if (MODE != MODE_FWD && r >= 0 && src_row(nbr, r, k, n, tpb) != i) r = -1;
+        // (r, k) points back to i (the transposed table, as src_row_t); sym:
+        // the caller promises it does
+        if (MODE != MODE_FWD && !sym && r >= 0 && src_row(nbr, r, k, n, tpb) != i) r = -1;
         v[k] = bload16(rs, r >= 0 ? (uint32_t)((r * c + ch) * (int64_t)sizeof(T)) : kOOB);
     }
     A acc[VEC];
@@ -523,7 +524,7 @@ __global__ __launch_bounds__(512) void k_dw_bwd_vec(const T* __restrict__ go, co
                                                     const int32_t* __restrict__ nbr, const T* __restrict__ w,
                                                     T* __restrict__ gi, typename Acc<T>::type* __restrict__ ws,
                                                     uint32_t* __restrict__ flags, int64_t n, int c, int64_t tpb,
-                                                    int64_t rows_per_split) {
+                                                    int64_t rows_per_split, bool sym) {
     constexpr int VEC = Vec16<T>::N;
     typedef typename Acc<T>::type A;
     __shared__ __align__(16) A red[5 * 512 * VEC];
@@ -556,7 +557,7 @@ __global__ __launch_bounds__(512) void k_dw_bwd_vec(const T* __restrict__ go, co
             const int64_t i = c0 + r;
             sx[e] = (int)src_row(nbr, i, k, n, tpb);
             const int64_t j = src_row(nbr, i, 8 - k, n, tpb);
-            const bool ok = j >= 0 && src_row(nbr, j, k, n, tpb) == i;
+            const bool ok = j >= 0 && (sym || src_row(nbr, j, k, n, tpb) == i);
             orphan |= (j >= 0 && !ok) ? 1 : 0;
             st[e] = ok ? (int)j : -1;
         }
@@ -761,15 +762,15 @@ void bw_valu(int dtype, const BwPlan& p, const void* go, const void* x, const in
 
 template <typename T>
 static void launch_dw(int mode, const void* src, const int32_t* nbr, const void* w,
-                      const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s) {
+                      const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s, bool sym) {
     if (dw_vec_ok<T>(n, c, src, w, out) && (!bias || al16v(bias))) {
         const dim3 g((unsigned)cdiv(n * (c / Vec16<T>::N), 256));
         if (mode == MODE_FWD)
             hipLaunchKernelGGL((k_dw_vec<T, MODE_FWD>), g, dim3(256), 0, s, (const T*)src, nbr, (const T*)w,
-                               (const T*)bias, (T*)out, n, c, tpb);
+                               (const T*)bias, (T*)out, n, c, tpb, false);
         else
             hipLaunchKernelGGL((k_dw_vec<T, MODE_BWDIN>), g, dim3(256), 0, s, (const T*)src, nbr, (const T*)w,
-                               (const T*)nullptr, (T*)out, n, c, tpb);
+                               (const T*)nullptr, (T*)out, n, c, tpb, sym);
         return;
     }
     dim3 grid((unsigned)cdiv(n * c, 256));
@@ -782,12 +783,12 @@ static void launch_dw(int mode, const void* src, const int32_t* nbr, const void*
 }
 
 void dw_gather(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
-               const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s) {
+               const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s, bool sym) {
     switch (dtype) {
-        case SVTAD_F32: launch_dw<float>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
-        case SVTAD_F16: launch_dw<f16>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
-        case SVTAD_BF16: launch_dw<bf16>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
-        case SVTAD_F64: launch_dw<double>(mode, src, nbr, w, bias, out, n, c, tpb, s); break;
+        case SVTAD_F32: launch_dw<float>(mode, src, nbr, w, bias, out, n, c, tpb, s, sym); break;
+        case SVTAD_F16: launch_dw<f16>(mode, src, nbr, w, bias, out, n, c, tpb, s, sym); break;
+        case SVTAD_BF16: launch_dw<bf16>(mode, src, nbr, w, bias, out, n, c, tpb, s, sym); break;
+        case SVTAD_F64: launch_dw<double>(mode, src, nbr, w, bias, out, n, c, tpb, s, sym); break;
     }
 }
 
@@ -818,11 +819,11 @@ static void launch_dw_bw(const BwPlan& p, const void* go, const void* x, const i
 template <typename T>
 static bool launch_dw_bwd(const BwPlan& p, const void* go, const void* x, const int32_t* nbr, const void* w,
                           void* gi, void* gw, void* gb, void* ws, uint32_t* flags, int64_t n, int c, int64_t tpb,
-                          hipStream_t s) {
+                          hipStream_t s, bool sym) {
     typedef typename Acc<T>::type A;
     if (!dw_vec_ok<T>(n, c, go, x, gi) || !al16v(w)) return false;
     hipLaunchKernelGGL((k_dw_bwd_vec<T>), dim3((unsigned)p.splits), dim3(512), 0, s, (const T*)go, (const T*)x,
-                       nbr, (const T*)w, (T*)gi, (A*)ws, flags, n, c, tpb, p.rows_per_split);
+                       nbr, (const T*)w, (T*)gi, (A*)ws, flags, n, c, tpb, p.rows_per_split, sym);
     const int64_t count = gb ? 10LL * c : 9LL * c;
     hipLaunchKernelGGL((k_dw_bwd_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, 64))), dim3(1024),
                        0, s, (const A*)ws, count, p.splits, (T*)gw, 10LL * c, 9LL * c, (T*)gb, (const uint32_t*)flags,
@@ -832,12 +833,12 @@ static bool launch_dw_bwd(const BwPlan& p, const void* go, const void* x, const 
 
 bool dw_bwd_fused(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, const void* w,
                   void* gi, void* gw, void* gb, void* ws, uint32_t* flags, int64_t n, int c, int64_t tpb,
-                  hipStream_t s) {
+                  hipStream_t s, bool sym) {
     switch (dtype) {
-        case SVTAD_F32: return launch_dw_bwd<float>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
-        case SVTAD_F16: return launch_dw_bwd<f16>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
-        case SVTAD_BF16: return launch_dw_bwd<bf16>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
-        case SVTAD_F64: return launch_dw_bwd<double>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s);
+        case SVTAD_F32: return launch_dw_bwd<float>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s, sym);
+        case SVTAD_F16: return launch_dw_bwd<f16>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s, sym);
+        case SVTAD_BF16: return launch_dw_bwd<bf16>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s, sym);
+        case SVTAD_F64: return launch_dw_bwd<double>(p, go, x, nbr, w, gi, gw, gb, ws, flags, n, c, tpb, s, sym);
     }
     return false;
 }

@@ -35,18 +35,21 @@ void orphans(int dtype, bool dw, const void* go, const int32_t* nbr, const void*
 void bw_valu(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
              void* gw, void* gb, void* ws, int64_t n, int c_in, int c_out, int64_t tpb,
              hipStream_t s);
+// sym (backward-input only): every entry has its partner, so the vectorized
+// kernel loads no partners.
 void dw_gather(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
-               const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s);
+               const void* bias, void* out, int64_t n, int c, int64_t tpb, hipStream_t s, bool sym = false);
 void dw_bw(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, void* gw,
            void* gb, void* ws, int64_t n, int c, int64_t tpb, hipStream_t s);
 // Depthwise backward-input and backward-weight / bias in one pass over the
 // rows plus one reduction launch (which also runs the orphan pass when a
 // split's flag word says so). ws holds the [splits][10][c] partials, flags
 // one word per split. Returns false (nothing launched) when the vectorized
-// kernels do not apply.
+// kernels do not apply. sym: every entry has its partner (no partner loads;
+// the flag words stay 0).
 bool dw_bwd_fused(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr, const void* w,
                   void* gi, void* gw, void* gb, void* ws, uint32_t* flags, int64_t n, int c, int64_t tpb,
-                  hipStream_t s);
+                  hipStream_t s, bool sym = false);
 
 // out[e] = T(sum_s part[s][e]) for e < count; partials in the accumulator type.
 void split_reduce(int dtype, const void* part, int64_t count, int splits, void* out, hipStream_t s);
@@ -65,10 +68,13 @@ constexpr size_t kOrphanFlagBytes = 256;
 // with prepacked, the fragment-ordered weight itself. For the backward-input
 // mode, orphan_flag (may be NULL) is the flag word after the packed weight;
 // the return value says whether the kernel that ran maintains it (if not,
-// the orphan pass must run without the flag).
+// the orphan pass must run without the flag). sym is the caller's promise that
+// every table entry (i, 8-k) -> p has its partner (p, k) -> i, as in every
+// table built from a keep mask: the backward-input wide kernel then loads no
+// partners (and never arms the flag).
 bool gg_mfma(int dtype, int mode, const void* src, const int32_t* nbr, const void* w,
              const void* bias, int bias_mode, void* out, int64_t n, int c_red, int n_out,
-             int64_t tpb, void* ws, bool prepacked, uint32_t* orphan_flag, hipStream_t s);
+             int64_t tpb, void* ws, bool prepacked, uint32_t* orphan_flag, hipStream_t s, bool sym = false);
 // Whether the fragment-ordered (prepacked) entry points handle this shape.
 bool gg_mfma_packed_ok(int dtype, int64_t n, int c_red, int n_out);
 // Fragment-ordered weights for the forward (wf_fwd) and backward-input
@@ -123,7 +129,8 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
                    BwPlan* p_out);
 int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, const int32_t* nbr,
                    const void* w, const void* packed_bwd, uint32_t* flag, void* gi, void* gw, void* gb,
-                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s);
+                   void* ws, size_t ws_bytes, int64_t n, int c_in, int c_out, int64_t tpb, hipStream_t s,
+                   bool sym = false);
 
 // A linear layer's weight gradient out[ci][co] = sum_i g[rows[i]][ci] x[i][co]
 // (rows NULL: row i of g), i < n, on the backward-weight partial kernel with

@@ -229,11 +229,17 @@ at::Tensor op_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const at
     return gi;
 }
 
+// table_flags from the `symmetric` keyword of the backward ops: the caller's
+// promise that every table entry has its partner (SVTAD_TABLE_SYMMETRIC)
+static unsigned table_flags(bool symmetric) { return symmetric ? (unsigned)SVTAD_TABLE_SYMMETRIC : 0u; }
+
 // bwd_in_packed(grad_output, neighbor_indices, weight, packed_bwd, n_kept, C_in,
-// tokens_per_batch): bwd_in with a weight packed by pack_weight (falls back to
-// bwd_in when packed_bwd is empty or the shape has no packed path).
+// tokens_per_batch, symmetric=False): bwd_in with a weight packed by
+// pack_weight (falls back to bwd_in when packed_bwd is empty or the shape has
+// no packed path).
 at::Tensor op_bwd_in_packed(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
-                            const at::Tensor& packed, int64_t n_kept, int64_t c_in, int64_t tpb) {
+                            const at::Tensor& packed, int64_t n_kept, int64_t c_in, int64_t tpb,
+                            bool symmetric) {
     if (packed.numel() == 0) return op_bwd_in(go_in, nbr_in, w_in, n_kept, c_in, tpb);
     check_gpu(go_in, "grad_output");
     at::Tensor go = rows_view(go_in);
@@ -249,9 +255,9 @@ at::Tensor op_bwd_in_packed(const at::Tensor& go_in, const at::Tensor& nbr_in, c
     at::Tensor nbr = table_i32(nbr_in, n_kept);
     c10::DeviceGuard g(go.device());
     at::Tensor gi = at::empty({n_kept, c_in}, go.options());
-    const int st = svtad_bwd_in_packed(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
-                                       packed.data_ptr(), gi.data_ptr(), n_kept, (int)c_in,
-                                       (int)c_out, tpb, dt, stream_of(go));
+    const int st = svtad_bwd_in_packed_ex(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                                          packed.data_ptr(), gi.data_ptr(), n_kept, (int)c_in,
+                                          (int)c_out, tpb, dt, table_flags(symmetric), stream_of(go));
     if (st == SVTAD_ERR_UNSUPPORTED) return op_bwd_in(go_in, nbr_in, w_in, n_kept, c_in, tpb);
     check_status(st, "bwd_in_packed");
     return gi;
@@ -261,7 +267,7 @@ at::Tensor op_bwd_in_packed(const at::Tensor& go_in, const at::Tensor& nbr_in, c
 // backward-input's gathered GEMM alone (timing; equals bwd_in_packed for
 // tables whose entries all have their symmetric partner)
 at::Tensor op_bwd_in_gemm(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& packed,
-                          int64_t c_in, int64_t tpb) {
+                          int64_t c_in, int64_t tpb, bool symmetric) {
     check_gpu(go_in, "grad_output");
     at::Tensor go = rows_view(go_in);
     const int64_t n = n_rows(go), c_out = go.size(-1);
@@ -273,7 +279,7 @@ at::Tensor op_bwd_in_gemm(const at::Tensor& go_in, const at::Tensor& nbr_in, con
     c10::DeviceGuard g(go.device());
     at::Tensor gi = at::empty({n, c_in}, go.options());
     check_status(svtad_bwd_in_gemm(go.data_ptr(), nbr.data_ptr<int32_t>(), packed.data_ptr(), gi.data_ptr(), n,
-                                   (int)c_in, (int)c_out, tpb, dt, stream_of(go)),
+                                   (int)c_in, (int)c_out, tpb, dt, table_flags(symmetric), stream_of(go)),
                  "bwd_in_gemm");
     return gi;
 }
@@ -315,7 +321,7 @@ std::tuple<at::Tensor, at::Tensor> op_bwd_w_bias(const at::Tensor& go_in, const 
 std::tuple<at::Tensor, at::Tensor, at::Tensor> op_bwd_packed(const at::Tensor& go_in, const at::Tensor& x_in,
                                                              const at::Tensor& nbr_in, const at::Tensor& w_in,
                                                              const at::Tensor& packed, int64_t c_in,
-                                                             int64_t tpb, bool with_bias) {
+                                                             int64_t tpb, bool with_bias, bool symmetric) {
     check_gpu(go_in, "grad_output");
     check_gpu(x_in, "x");
     at::Tensor go = rows_view(go_in);
@@ -323,7 +329,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> op_bwd_packed(const at::Tensor& g
     TORCH_CHECK(x.size(-1) == c_in, "x has ", x.size(-1), " channels, C_in = ", c_in);
     const int64_t n = n_rows(x), c_out = go.size(-1);
     auto separate = [&]() {
-        at::Tensor gi = op_bwd_in_packed(go_in, nbr_in, w_in, packed, n, c_in, tpb);
+        at::Tensor gi = op_bwd_in_packed(go_in, nbr_in, w_in, packed, n, c_in, tpb, symmetric);
         auto gwb = op_bwd_w_bias(go_in, x_in, nbr_in, c_in, tpb, with_bias);
         return std::make_tuple(gi, std::get<0>(gwb), std::get<1>(gwb));
     };
@@ -345,10 +351,10 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> op_bwd_packed(const at::Tensor& g
     at::Tensor gi = at::empty({n, c_in}, x.options());
     at::Tensor gw = at::empty({9, c_in, c_out}, x.options());
     at::Tensor gb = with_bias ? at::empty({c_out}, x.options()) : at::Tensor();
-    const int st = svtad_bwd_packed(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
-                                    packed.data_ptr(), gi.data_ptr(), gw.data_ptr(),
-                                    with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
-                                    (int)c_in, (int)c_out, tpb, dt, stream_of(x));
+    const int st = svtad_bwd_packed_ex(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                                       packed.data_ptr(), gi.data_ptr(), gw.data_ptr(),
+                                       with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
+                                       (int)c_in, (int)c_out, tpb, dt, table_flags(symmetric), stream_of(x));
     if (st == SVTAD_ERR_UNSUPPORTED) return separate();
     check_status(st, "bwd_packed");
     return {gi, gw, with_bias ? gb : at::empty({0}, x.options())};
@@ -413,7 +419,7 @@ at::Tensor op_dw_fwd(const at::Tensor& x_in, const at::Tensor& nbr_in, const at:
 }
 
 at::Tensor op_dw_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const at::Tensor& w_in,
-                        int64_t tpb) {
+                        int64_t tpb, bool symmetric) {
     check_gpu(go_in, "grad_output");
     at::Tensor go = rows_view(go_in);
     const int64_t c = go.size(-1), n = n_rows(go);
@@ -424,8 +430,8 @@ at::Tensor op_dw_bwd_in(const at::Tensor& go_in, const at::Tensor& nbr_in, const
     at::Tensor nbr = table_i32(nbr_in, n);
     c10::DeviceGuard g(go.device());
     at::Tensor gi = at::empty({n, c}, go.options());
-    const int st = svtad_dw_bwd_in(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
-                                   gi.data_ptr(), n, (int)c, tpb, dtype_code(go), stream_of(go));
+    const int st = svtad_dw_bwd_in_ex(go.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(), gi.data_ptr(), n,
+                                      (int)c, tpb, dtype_code(go), table_flags(symmetric), stream_of(go));
     check_status(st, "dw_bwd_in");
     return gi;
 }
@@ -458,7 +464,7 @@ std::tuple<at::Tensor, at::Tensor> op_dw_bwd_w(const at::Tensor& go_in, const at
 // dw_bwd_in and dw_bwd_w in one call (one pass over the rows + one reduction)
 std::tuple<at::Tensor, at::Tensor, at::Tensor> op_dw_bwd(const at::Tensor& go_in, const at::Tensor& x_in,
                                                          const at::Tensor& nbr_in, const at::Tensor& w_in,
-                                                         int64_t tpb, bool with_bias) {
+                                                         int64_t tpb, bool with_bias, bool symmetric) {
     check_gpu(go_in, "grad_output");
     at::Tensor go = rows_view(go_in);
     at::Tensor x = rows_view(x_in);
@@ -478,9 +484,9 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> op_dw_bwd(const at::Tensor& go_in
     at::Tensor gi = at::empty({n, c}, x.options());
     at::Tensor gw = at::empty({9, c}, x.options());
     at::Tensor gb = with_bias ? at::empty({c}, x.options()) : at::empty({0}, x.options());
-    const int st = svtad_dw_bwd(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(), gi.data_ptr(),
-                                gw.data_ptr(), with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(), ws_bytes, n,
-                                (int)c, tpb, dt, stream_of(x));
+    const int st = svtad_dw_bwd_ex(go.data_ptr(), x.data_ptr(), nbr.data_ptr<int32_t>(), w.data_ptr(),
+                                   gi.data_ptr(), gw.data_ptr(), with_bias ? gb.data_ptr() : nullptr, ws.data_ptr(),
+                                   ws_bytes, n, (int)c, tpb, dt, table_flags(symmetric), stream_of(x));
     check_status(st, "dw_bwd");
     return {gi, gw, gb};
 }
@@ -973,12 +979,14 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
           py::arg("tokens_per_batch"), py::arg("bias_mode"));
     m.def("bwd_in_packed", &op_bwd_in_packed, "bwd_in with a packed weight", py::arg("grad_output"),
           py::arg("neighbor_indices"), py::arg("weight"), py::arg("packed_bwd"), py::arg("n_kept"),
-          py::arg("C_in"), py::arg("tokens_per_batch"));
+          py::arg("C_in"), py::arg("tokens_per_batch"), py::arg("symmetric") = false);
     m.def("bwd_packed", &op_bwd_packed, "bwd_in_packed + bwd_w_bias in one call",
           py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
-          py::arg("packed_bwd"), py::arg("C_in"), py::arg("tokens_per_batch"), py::arg("with_bias"));
+          py::arg("packed_bwd"), py::arg("C_in"), py::arg("tokens_per_batch"), py::arg("with_bias"),
+          py::arg("symmetric") = false);
     m.def("bwd_in_gemm", &op_bwd_in_gemm, "Backward-input gathered GEMM only (timing)", py::arg("grad_output"),
-          py::arg("neighbor_indices"), py::arg("packed_bwd"), py::arg("C_in"), py::arg("tokens_per_batch"));
+          py::arg("neighbor_indices"), py::arg("packed_bwd"), py::arg("C_in"), py::arg("tokens_per_batch"),
+          py::arg("symmetric") = false);
     m.def("bwd_w_partials", &op_bwd_w_partials, "Backward-weight partial sums only (timing)",
           py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("C_in"),
           py::arg("tokens_per_batch"), py::arg("with_bias"));
@@ -988,10 +996,11 @@ PYBIND11_MODULE(opentad_sparse_ops, m) {
     m.def("dw_fwd", &op_dw_fwd, "Depthwise forward", py::arg("x"), py::arg("neighbor_indices"),
           py::arg("weight"), py::arg("bias"), py::arg("tokens_per_batch"));
     m.def("dw_bwd_in", &op_dw_bwd_in, "Depthwise backward input", py::arg("grad_output"),
-          py::arg("neighbor_indices"), py::arg("weight"), py::arg("tokens_per_batch"));
+          py::arg("neighbor_indices"), py::arg("weight"), py::arg("tokens_per_batch"),
+          py::arg("symmetric") = false);
     m.def("dw_bwd", &op_dw_bwd, "Depthwise backward input, weight and bias in one call",
           py::arg("grad_output"), py::arg("x"), py::arg("neighbor_indices"), py::arg("weight"),
-          py::arg("tokens_per_batch"), py::arg("with_bias"));
+          py::arg("tokens_per_batch"), py::arg("with_bias"), py::arg("symmetric") = false);
     m.def("dw_bwd_w", &op_dw_bwd_w, "Depthwise backward weight and bias", py::arg("grad_output"),
           py::arg("x"), py::arg("neighbor_indices"), py::arg("tokens_per_batch"),
           py::arg("with_bias"));

@@ -25,6 +25,39 @@ def set_debug_sparse(enabled: bool) -> None:
     DEBUG_SPARSE = bool(enabled)
 
 
+# A table built from a keep mask is symmetric: every entry (i, k) -> j has its
+# partner (j, 8-k) -> i. The builders below record that on the tensor they
+# return, with the tensor's version counter (shared with its views), so any
+# in-place change drops the record. The backward ops skip their partner checks
+# for a table that carries it (symmetric=True); every other table takes the
+# checked path, which gives the same results for symmetric tables.
+_SYM_ATTR = "_svtad_symmetric"
+
+
+def mark_symmetric_table(table: torch.Tensor) -> torch.Tensor:
+    """Record on ``table`` (returned) that every entry has its partner. For
+    tables known to be built from a keep mask; a wrong record gives wrong
+    backward-input gradients."""
+    setattr(table, _SYM_ATTR, table._version)
+    return table
+
+
+def is_symmetric_table(table) -> bool:
+    """Whether ``table`` carries the symmetric record and is unchanged since."""
+    if table is None:
+        return False
+    v = getattr(table, _SYM_ATTR, None)
+    return v is not None and v == table._version
+
+
+def _keep_symmetric(src, out):
+    """``out`` carries the record when ``src`` does (operations that keep the
+    property: dtype and shape changes, the global-index conversion)."""
+    if out is not None and is_symmetric_table(src):
+        mark_symmetric_table(out)
+    return out
+
+
 def build_neighbor_table(mask: torch.Tensor, batched: bool = False, n: int | None = None,
                          dtype: torch.dtype = torch.int32) -> torch.Tensor:
     """Table from a keep mask ``[B, T, H, W]`` (or any ``[..., H, W]``).
@@ -48,7 +81,7 @@ def build_neighbor_table(mask: torch.Tensor, batched: bool = False, n: int | Non
         if table.shape[0] % B:
             raise ValueError("batched=True needs the same number of kept cells per sample")
         table = table.view(B, table.shape[0] // B, 9)
-    return table
+    return mark_symmetric_table(table)
 
 
 def get_initial_neighbor_indices(h: int, w: int, T: int, device, B: int,
@@ -59,7 +92,7 @@ def get_initial_neighbor_indices(h: int, w: int, T: int, device, B: int,
     form, no mask, no host synchronisation."""
     like = torch.empty(0, device=device)
     table = _ops.grid_neighbor_table(B * T, h, w, dtype == torch.int64, like)
-    return table.view(B, T * h * w, 9)
+    return mark_symmetric_table(table.view(B, T * h * w, 9))
 
 
 def global_neighbor_table(neighbor_indices: torch.Tensor, tokens_per_batch: int) -> torch.Tensor:
@@ -68,21 +101,40 @@ def global_neighbor_table(neighbor_indices: torch.Tensor, tokens_per_batch: int)
     evaluated on the device. When the table's maximum is below
     ``tokens_per_batch`` (N of a ``[B, N, C]`` input) the entries are
     per-sample indices and row i's valid entries get ``(i // N) * N`` added;
-    otherwise they are global already. No host synchronisation."""
-    return _ops.table_to_global(neighbor_indices, int(tokens_per_batch))
+    otherwise they are global already. No host synchronisation. The result
+    keeps the input's symmetric record."""
+    return _keep_symmetric(neighbor_indices, _ops.table_to_global(neighbor_indices, int(tokens_per_batch)))
 
 
 def remap_neighbor_table(neighbor_indices: torch.Tensor, keep_idx: torch.Tensor) -> torch.Tensor:
     """Table after a prune: keep the rows ``keep_idx`` ``[B, N_new]`` (local
     indices, as from topk) of ``neighbor_indices`` ``[B, N_prev, 9]`` and map
     every global entry to its new global index, -1 for pruned
-    (vit_sparse_adapter_poguise.py:913-977). Output dtype follows the input."""
+    (vit_sparse_adapter_poguise.py:913-977). Output dtype follows the input.
+
+    The result keeps the input's symmetric record when each sample's keep
+    indices are distinct, as topk's are (a repeated index leaves a copied row
+    whose neighbors point to the other copy; the reference's scatter then
+    picks either copy). Under debug validation repeated indices drop the
+    record; otherwise the caller's keep indices are taken to be distinct."""
     dt = neighbor_indices.dtype
     t = neighbor_indices if dt == torch.int32 else neighbor_indices.to(torch.int32)
     out = _ops.remap_neighbor_table(t, keep_idx)
     if DEBUG_SPARSE:
         validate_neighbor_table(out, keep_idx.shape[1], "remap_neighbor_table")
-    return out if dt == torch.int32 else out.to(dt)
+    out = out if dt == torch.int32 else out.to(dt)
+    if _distinct_or_unchecked(keep_idx):
+        _keep_symmetric(neighbor_indices, out)
+    return out
+
+
+def _distinct_or_unchecked(keep_idx) -> bool:
+    """False when debug validation is on and a sample repeats a keep index
+    (the check reads a count back to the host); True otherwise."""
+    if not DEBUG_SPARSE or keep_idx.numel() == 0:
+        return True
+    srt = keep_idx.sort(dim=-1).values
+    return not bool((srt[..., 1:] == srt[..., :-1]).any().item())
 
 
 def prune_tokens(x: torch.Tensor, keep_idx: torch.Tensor, last_idx=None, neighbor_indices=None,
@@ -119,6 +171,8 @@ def prune_tokens(x: torch.Tensor, keep_idx: torch.Tensor, last_idx=None, neighbo
             validate_neighbor_table(t_new, keep_idx.shape[1], "prune_tokens")
         if dt != torch.int32:
             t_new = t_new.to(dt)
+        if _distinct_or_unchecked(keep_idx):  # as in remap_neighbor_table
+            _keep_symmetric(neighbor_indices, t_new)
     return x_new, idx_new, t_new
 
 

@@ -15,7 +15,7 @@ import torch.nn as nn
 from torch.autograd import Function
 
 from . import opentad_sparse_ops as _ops
-from .neighbor import global_neighbor_table
+from .neighbor import _keep_symmetric, global_neighbor_table, is_symmetric_table
 
 try:  # torch >= 2.4
     from torch.amp import custom_bwd as _custom_bwd, custom_fwd as _custom_fwd
@@ -83,12 +83,15 @@ class SparseConv2dFunction(Function):
 
     ``packed`` (not in the reference; optional) is ``(packed_fwd,
     packed_bwd)`` from ``pack_weight(weight, True, ...)``, ``packed_bwd`` None
-    when it was not requested; without it the weight is packed here."""
+    when it was not requested; without it the weight is packed here. The
+    backward skips the partner checks for a table that carries the
+    symmetric record of the table builders (``is_symmetric_table``)."""
 
     @staticmethod
     @custom_fwd
     def forward(ctx, x, neighbor_indices, weight, bias=None, tokens_per_batch=0, chunk_size=0, packed=None):
         _, C_in, C_out = weight.shape
+        ctx.symmetric = is_symmetric_table(neighbor_indices)
         if C_in % 4 != 0:
             raise ValueError(f"C_in ({C_in}) must be divisible by 4 for optimized kernel.")
         ctx.C_in = C_in
@@ -120,14 +123,15 @@ class SparseConv2dFunction(Function):
         if ctx.needs_input_grad[0] and ctx.needs_input_grad[2]:
             # both gradients in one call (the same kernels as the two calls
             # below, with one launch less)
-            gi, gw, gb = _ops.bwd_packed(go, x, neighbor_indices, weight, packed_bwd, C_in, tpb, need_b)
+            gi, gw, gb = _ops.bwd_packed(go, x, neighbor_indices, weight, packed_bwd, C_in, tpb, need_b,
+                                         symmetric=ctx.symmetric)
             grad_input = gi.view(x.shape) if x.dim() == 3 else gi
             grad_weight = gw
             grad_bias = gb if need_b else None
             return grad_input, None, grad_weight, grad_bias, None, None, None
         if ctx.needs_input_grad[0]:
             grad_input = _ops.bwd_in_packed(go, neighbor_indices, weight, packed_bwd,
-                                            x.numel() // x.shape[-1], C_in, tpb)
+                                            x.numel() // x.shape[-1], C_in, tpb, symmetric=ctx.symmetric)
             if x.dim() == 3:
                 grad_input = grad_input.view(x.shape)
         if ctx.needs_input_grad[2] or need_b:
@@ -147,13 +151,14 @@ def _table_and_tpb(x, neighbor_indices, tokens_per_batch):
     indices when the table's max is < N), evaluated on the device by
     ``global_neighbor_table``: the table comes back global, so the kernels run
     with tokens_per_batch = 0, and there is no host synchronisation (the
-    reference reads ``max()`` back)."""
+    reference reads ``max()`` back). The table keeps the input's symmetric
+    record."""
     if x.dim() == 3 and tokens_per_batch is None:
         return global_neighbor_table(neighbor_indices, x.shape[1]), 0
     nbr = neighbor_indices.reshape(-1, 9)
     if nbr.dtype != torch.int32:
         nbr = nbr.to(torch.int32)
-    return nbr, (tokens_per_batch or 0)
+    return _keep_symmetric(neighbor_indices, nbr), (tokens_per_batch or 0)
 
 
 def _autocast_cast(x, weight, bias):
@@ -237,6 +242,7 @@ class SparseDepthwiseConv2dFunction(Function):
     def forward(ctx, x, neighbor_indices, weight, bias=None, tokens_per_batch=0):
         ctx.save_for_backward(x, neighbor_indices, weight, bias)
         ctx.tokens_per_batch = tokens_per_batch
+        ctx.symmetric = is_symmetric_table(neighbor_indices)
         return _ops.dw_fwd(x, neighbor_indices, weight, bias, tokens_per_batch)
 
     @staticmethod
@@ -249,10 +255,10 @@ class SparseDepthwiseConv2dFunction(Function):
         need_b = bias is not None and ctx.needs_input_grad[3]
         if ctx.needs_input_grad[0] and ctx.needs_input_grad[2]:
             # all gradients in one pass over the rows plus one reduction
-            gi, gw, gb = _ops.dw_bwd(go, x, neighbor_indices, weight, tpb, need_b)
+            gi, gw, gb = _ops.dw_bwd(go, x, neighbor_indices, weight, tpb, need_b, symmetric=ctx.symmetric)
             return gi.view(x.shape), None, gw, gb if need_b else None, None
         if ctx.needs_input_grad[0]:
-            grad_input = _ops.dw_bwd_in(go, neighbor_indices, weight, tpb).view(x.shape)
+            grad_input = _ops.dw_bwd_in(go, neighbor_indices, weight, tpb, symmetric=ctx.symmetric).view(x.shape)
         if ctx.needs_input_grad[2] or need_b:
             gw, gb = _ops.dw_bwd_w(go, x, neighbor_indices, tpb, need_b)
             grad_weight = gw if ctx.needs_input_grad[2] else None

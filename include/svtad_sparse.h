@@ -65,6 +65,20 @@ enum svtad_bias_mode {
                               (implicit_gemm_v2.cu:290-297) without the conversion */
 };
 
+/*
+ * table_flags of the *_ex backward entry points (no counterpart in the
+ * reference, which checks nothing: its backward-input scatters every entry).
+ *   SVTAD_TABLE_SYMMETRIC: the caller promises that every entry
+ *     (i, k) -> j has its partner (j, 8-k) -> i. Every table built from a
+ *     keep mask has this property (svtad_table_build, svtad_table_grid,
+ *     svtad_table_fill), and svtad_remap_table / svtad_prune_step /
+ *     svtad_table_to_global keep it. The backward-input kernels then load no
+ *     partners and no pass for entries without one runs. Results are
+ *     identical to the unflagged call's for such tables; for a table without
+ *     the property they are wrong (every access stays in bounds).
+ */
+enum svtad_table_flags { SVTAD_TABLE_SYMMETRIC = 1 };
+
 /* Message of the last SVTAD_ERR_* returned on this host thread. */
 const char* svtad_last_error(void);
 const char* svtad_version(void);
@@ -134,6 +148,10 @@ int svtad_fwd_packed(const void* x, const int32_t* nbr, const void* packed_fwd, 
 int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* weight,
                         void* packed_bwd, void* grad_in, int64_t n, int c_in, int c_out,
                         int64_t tokens_per_batch, int dtype, void* stream);
+/* svtad_bwd_in_packed with table_flags (svtad_table_flags; 0 = the same call). */
+int svtad_bwd_in_packed_ex(const void* grad_out, const int32_t* nbr, const void* weight,
+                           void* packed_bwd, void* grad_in, int64_t n, int c_in, int c_out,
+                           int64_t tokens_per_batch, int dtype, unsigned table_flags, void* stream);
 
 /*
  * Timing entry point (no counterpart in the reference): the gathered GEMM of
@@ -141,10 +159,12 @@ int svtad_bwd_in_packed(const void* grad_out, const int32_t* nbr, const void* we
  * whose symmetric partner is absent. grad_in equals svtad_bwd_in_packed's
  * for tables in which every entry has its partner (every table built from a
  * keep mask); the kernel still sets the flag in packed_bwd otherwise. For
- * measuring that kernel's duration by itself. One launch.
+ * measuring that kernel's duration by itself. One launch. table_flags as for
+ * svtad_bwd_in_packed_ex.
  */
 int svtad_bwd_in_gemm(const void* grad_out, const int32_t* nbr, void* packed_bwd, void* grad_in, int64_t n,
-                      int c_in, int c_out, int64_t tokens_per_batch, int dtype, void* stream);
+                      int c_in, int c_out, int64_t tokens_per_batch, int dtype, unsigned table_flags,
+                      void* stream);
 
 /*
  * Allocation-free forward. No counterpart in the reference: for callers that
@@ -180,6 +200,11 @@ int svtad_bwd_packed(const void* grad_out, const void* x, const int32_t* nbr, co
                      void* packed_bwd, void* grad_in, void* grad_w, void* grad_bias,
                      void* workspace, size_t workspace_bytes, int64_t n, int c_in, int c_out,
                      int64_t tokens_per_batch, int dtype, void* stream);
+/* svtad_bwd_packed with table_flags (svtad_table_flags; 0 = the same call). */
+int svtad_bwd_packed_ex(const void* grad_out, const void* x, const int32_t* nbr, const void* weight,
+                        void* packed_bwd, void* grad_in, void* grad_w, void* grad_bias,
+                        void* workspace, size_t workspace_bytes, int64_t n, int c_in, int c_out,
+                        int64_t tokens_per_batch, int dtype, unsigned table_flags, void* stream);
 
 /*
  * Where neither backward grid fills the GPU (C_in = C_out = 192 or 256, f16 /
@@ -225,6 +250,9 @@ int svtad_dw_fwd(const void* x, const int32_t* nbr, const void* weight, const vo
                  void* out, int64_t n, int c, int64_t tokens_per_batch, int dtype, void* stream);
 int svtad_dw_bwd_in(const void* grad_out, const int32_t* nbr, const void* weight, void* grad_in,
                     int64_t n, int c, int64_t tokens_per_batch, int dtype, void* stream);
+/* svtad_dw_bwd_in with table_flags (svtad_table_flags; 0 = the same call). */
+int svtad_dw_bwd_in_ex(const void* grad_out, const int32_t* nbr, const void* weight, void* grad_in,
+                       int64_t n, int c, int64_t tokens_per_batch, int dtype, unsigned table_flags, void* stream);
 size_t svtad_dw_bwd_w_workspace_bytes(int64_t n, int c, int dtype);
 int svtad_dw_bwd_w(const void* grad_out, const void* x, const int32_t* nbr, void* grad_w,
                    void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n, int c,
@@ -243,6 +271,10 @@ size_t svtad_dw_bwd_workspace_bytes(int64_t n, int c, int dtype);
 int svtad_dw_bwd(const void* grad_out, const void* x, const int32_t* nbr, const void* weight, void* grad_in,
                  void* grad_w, void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n, int c,
                  int64_t tokens_per_batch, int dtype, void* stream);
+/* svtad_dw_bwd with table_flags (svtad_table_flags; 0 = the same call). */
+int svtad_dw_bwd_ex(const void* grad_out, const void* x, const int32_t* nbr, const void* weight, void* grad_in,
+                    void* grad_w, void* grad_bias, void* workspace, size_t workspace_bytes, int64_t n, int c,
+                    int64_t tokens_per_batch, int dtype, unsigned table_flags, void* stream);
 
 /*
  * Neighbor table from a keep mask [n_frames, h, w] (uint8, nonzero = kept),

@@ -404,3 +404,68 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     monkeypatch.delenv("SVTAD_BWD_FUSED")
     st, _ = _fused_plan(lib, -1, 192, 192, 1)
     assert st == -1
+
+
+def test_table_flags_checked_on_host(lib):
+    buf = ctypes.create_string_buffer(64)
+    aligned = ctypes.c_void_p((ctypes.addressof(buf) + 15) & ~15)
+    U = ctypes.c_uint
+    # unknown bits are rejected before any launch (0 and SVTAD_TABLE_SYMMETRIC = 1 are accepted)
+    st = lib.svtad_bwd_in_packed_ex(aligned, aligned, aligned, aligned, aligned, I64(4), 192, 192, I64(0), 1,
+                                    U(2), None)
+    assert st == -1 and b"table_flags" in lib.svtad_last_error()
+    st = lib.svtad_bwd_packed_ex(aligned, aligned, aligned, aligned, aligned, aligned, aligned, None, aligned,
+                                 ctypes.c_size_t(1 << 30), I64(4), 192, 192, I64(0), 1, U(0x10), None)
+    assert st == -1 and b"table_flags" in lib.svtad_last_error()
+    st = lib.svtad_dw_bwd_in_ex(aligned, aligned, aligned, aligned, I64(4), 64, I64(0), 1, U(4), None)
+    assert st == -1 and b"table_flags" in lib.svtad_last_error()
+    st = lib.svtad_dw_bwd_ex(aligned, aligned, aligned, aligned, aligned, aligned, None, aligned,
+                             ctypes.c_size_t(1 << 30), I64(4), 64, I64(0), 1, U(3), None)
+    assert st == -1 and b"table_flags" in lib.svtad_last_error()
+    st = lib.svtad_bwd_in_gemm(aligned, aligned, aligned, aligned, I64(4), 192, 192, I64(0), 1, U(8), None)
+    assert st == -1 and b"table_flags" in lib.svtad_last_error()
+    # empty inputs with valid flags are no-ops
+    assert lib.svtad_dw_bwd_in_ex(None, None, None, None, I64(0), 64, I64(0), 1, U(1), None) == 0
+    assert lib.svtad_bwd_in_packed_ex(None, None, None, None, None, I64(0), 192, 192, I64(0), 1, U(1), None) == 0
+
+
+def test_symmetric_record_follows_the_tensor_version():
+    import torch
+
+    from eccv26_tad_amd import is_symmetric_table, mark_symmetric_table
+    from eccv26_tad_amd.neighbor import _keep_symmetric
+
+    t = torch.full((6, 9), -1, dtype=torch.int32)
+    assert not is_symmetric_table(t) and not is_symmetric_table(None)
+    mark_symmetric_table(t)
+    assert is_symmetric_table(t)
+    # a change through a view drops it (views share the version counter)
+    v = t.view(2, 3, 9)
+    assert not is_symmetric_table(v)  # the view object itself carries no record
+    v[0, 0, 0] = 3
+    assert not is_symmetric_table(t)
+    # propagation: only from a recorded, unchanged source
+    u = mark_symmetric_table(torch.full((4, 9), -1, dtype=torch.int64))
+    w = _keep_symmetric(u, u.reshape(-1, 9).to(torch.int32))
+    assert is_symmetric_table(w)
+    assert not is_symmetric_table(_keep_symmetric(t, t.clone()))
+    # a copy of a recorded table carries nothing (the checked path)
+    assert not is_symmetric_table(u.clone())
+
+
+def test_repeated_keep_indices_drop_the_record_under_debug():
+    import torch
+
+    import eccv26_tad_amd.neighbor as nb
+
+    keep_ok = torch.tensor([[3, 1, 2], [0, 2, 1]])
+    keep_dup = torch.tensor([[3, 1, 3], [0, 2, 1]])
+    old = nb.DEBUG_SPARSE
+    try:
+        nb.set_debug_sparse(False)
+        assert nb._distinct_or_unchecked(keep_dup)  # unchecked: taken as distinct, as topk gives
+        nb.set_debug_sparse(True)
+        assert nb._distinct_or_unchecked(keep_ok)
+        assert not nb._distinct_or_unchecked(keep_dup)
+    finally:
+        nb.set_debug_sparse(old)
