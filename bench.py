@@ -601,6 +601,38 @@ def cpu_baseline(budget_s: float):
     }
 
 
+def replay_measure(dev, dtype, keep, steps, graph):
+    """The headline step (pack, forward, combined backward) at ``keep``,
+    eager or as replays of one HIP-graph capture of it, timed over ``steps``
+    between one pair of events. Run alone under a kernel trace, each mode
+    shows where its time goes: the kernels' durations, and the gaps between
+    them and between replays."""
+    import torch
+
+    p = Problem(keep, dev, dtype)
+    for _ in range(5):
+        p.step()
+    torch.cuda.synchronize()
+    fn = p.step
+    if graph:
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            for _ in range(3):
+                p.step()
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            p.step()
+        fn = g.replay
+    for _ in range(10):
+        fn()
+    torch.cuda.synchronize()
+    return {"mode": "graph" if graph else "eager", "keep": keep, "n": p.n, "steps": steps,
+            "us_per_step": round(time_events(fn, steps) * 1e3, 2)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -618,9 +650,11 @@ def main():
                     help="with --only depthwise: time the --keep rate alone (for counter runs)")
     ap.add_argument("--large-cases", default=None,
                     help="with --only large: comma-separated subset of c4_10,c4_25,c4_55,c5")
-    ap.add_argument("--only", choices=("adapter", "prune", "depthwise", "large"), default=None,
-                    help="only time the fused adapter or the prune step, print its JSON and exit "
-                         "(for kernel traces of those paths)")
+    ap.add_argument("--only", choices=("adapter", "prune", "depthwise", "large", "replay"), default=None,
+                    help="only time the fused adapter, the prune step, ... print its JSON and exit "
+                         "(for kernel traces of those paths); replay: the headline step at --keep, "
+                         "eager or (--graph) as HIP-graph replays")
+    ap.add_argument("--graph", action="store_true", help="with --only replay: time HIP-graph replays")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only; the SparseConv2D path has no "
@@ -657,6 +691,9 @@ def main():
     if args.only == "large":
         cases = set(args.large_cases.split(",")) if args.large_cases else None
         print(json.dumps({"large_channel": large_channel_measure(dev, args.steps, cases)}), flush=True)
+        return
+    if args.only == "replay":
+        print(json.dumps({"replay": replay_measure(dev, dtype, args.keep, args.steps, args.graph)}), flush=True)
         return
 
     log(f"bench: building problem keep={args.keep}")
