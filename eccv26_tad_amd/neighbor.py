@@ -37,8 +37,10 @@ _SYM_ATTR = "_svtad_symmetric"
 def mark_symmetric_table(table: torch.Tensor) -> torch.Tensor:
     """Record on ``table`` (returned) that every entry has its partner. For
     tables known to be built from a keep mask; a wrong record gives wrong
-    backward-input gradients."""
-    setattr(table, _SYM_ATTR, table._version)
+    backward-input gradients. An inference tensor (``torch.inference_mode``)
+    has no version counter and gets no record."""
+    if not table.is_inference():
+        setattr(table, _SYM_ATTR, table._version)
     return table
 
 

@@ -453,6 +453,17 @@ def test_symmetric_record_follows_the_tensor_version():
     assert not is_symmetric_table(u.clone())
 
 
+def test_inference_tensors_get_no_record():
+    import torch
+
+    from eccv26_tad_amd import is_symmetric_table, mark_symmetric_table
+
+    with torch.inference_mode():
+        t = mark_symmetric_table(torch.full((4, 9), -1, dtype=torch.int32))
+        assert not is_symmetric_table(t)
+    assert not is_symmetric_table(t)
+
+
 def test_repeated_keep_indices_drop_the_record_under_debug():
     import torch
 
