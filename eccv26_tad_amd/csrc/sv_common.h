@@ -117,8 +117,9 @@ __device__ __forceinline__ void orphan_entry(int64_t e, const T* __restrict__ go
 //     order, then the symmetric ones (offsets 0..8, the partner-checked
 //     transposed lookups that the gather also used), in fp32; gi[j] written
 //     once. A thread owns output channels tid, tid + NTH, ... (c_in <= 4 NTH).
-// More than kOrphanCap one-way entries: the atomic pass instead (each
-// contribution added into gi with its own rounding, order unfixed).
+// More than kOrphanCap one-way entries, or a table of more than 2^31 entries:
+// the atomic pass instead (each contribution added into gi with its own
+// rounding, order unfixed).
 constexpr int kOrphanCap = 2048;
 template <typename T, bool DEPTHWISE, int NTH>
 __device__ void orphan_exact(const T* __restrict__ go, const int32_t* __restrict__ nbr,
@@ -131,9 +132,13 @@ __device__ void orphan_exact(const T* __restrict__ go, const int32_t* __restrict
     __shared__ int wcnt[NW];
     __shared__ int total;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int64_t ne = n * 9;
+    if (ne > (int64_t)INT32_MAX) {  // entry numbers past 32 bits: the atomic pass
+        for (int64_t e = tid; e < ne; e += NTH) orphan_entry<T, DEPTHWISE>(e, go, nbr, w, gi, n, c_in, c_out, tpb);
+        return;
+    }
     if (tid == 0) total = 0;
     __syncthreads();
-    const int64_t ne = n * 9;
     for (int64_t e0 = 0; e0 < ne; e0 += NTH) {
         const int64_t e = e0 + tid;
         int64_t j = -1;
