@@ -711,6 +711,9 @@ def main():
 
     table_ms = time_events(lambda: sv.build_neighbor_table(prob.mask, n=n), 50)
     grid_ms = time_events(lambda: sv.get_initial_neighbor_indices(H, W, T, dev, B), 50)
+    # the launch floor: an empty kernel (torch.cuda._sleep(0), one workgroup)
+    # launched back to back, the least any launch of the step costs
+    floor_ms = time_events(lambda: torch.cuda._sleep(0), 200)
     if not torch.equal(sv.build_neighbor_table(prob.mask, n=n), prob.table):
         raise RuntimeError("one-launch table differs from the scan + fill table")
 
@@ -881,6 +884,7 @@ def main():
         "table_build_bytes": int(prob.mask.numel() + 36 * n),
         "table_build_gbs": round((prob.mask.numel() + 36 * n) / (table_ms * 1e-3) / 1e9, 1),
         "grid_table_us": round(grid_ms * 1e3, 2),
+        "launch_floor_us": round(floor_ms * 1e3, 2),
         "dense_us": round(dense * 1e3, 2) if dense is not None else None,
         "speedup_vs_dense": round(dense / ms, 3) if dense is not None else None,
         "roofline": roof,
