@@ -114,29 +114,18 @@ def remap_neighbor_table(neighbor_indices: torch.Tensor, keep_idx: torch.Tensor)
     every global entry to its new global index, -1 for pruned
     (vit_sparse_adapter_poguise.py:913-977). Output dtype follows the input.
 
-    The result keeps the input's symmetric record when each sample's keep
-    indices are distinct, as topk's are (a repeated index leaves a copied row
-    whose neighbors point to the other copy; the reference's scatter then
-    picks either copy). Under debug validation repeated indices drop the
-    record; otherwise the caller's keep indices are taken to be distinct."""
+    The result carries no symmetric record. It is symmetric only when each
+    sample's keep indices are distinct, as topk's are; a repeated index leaves
+    a copied row whose neighbors point back to one copy only. Checking that
+    would read a result back to the host, so the backward ops check the
+    partners of a remapped table instead (in the combined backward that adds
+    nothing measurable)."""
     dt = neighbor_indices.dtype
     t = neighbor_indices if dt == torch.int32 else neighbor_indices.to(torch.int32)
     out = _ops.remap_neighbor_table(t, keep_idx)
     if DEBUG_SPARSE:
         validate_neighbor_table(out, keep_idx.shape[1], "remap_neighbor_table")
-    out = out if dt == torch.int32 else out.to(dt)
-    if _distinct_or_unchecked(keep_idx):
-        _keep_symmetric(neighbor_indices, out)
-    return out
-
-
-def _distinct_or_unchecked(keep_idx) -> bool:
-    """False when debug validation is on and a sample repeats a keep index
-    (the check reads a count back to the host); True otherwise."""
-    if not DEBUG_SPARSE or keep_idx.numel() == 0:
-        return True
-    srt = keep_idx.sort(dim=-1).values
-    return not bool((srt[..., 1:] == srt[..., :-1]).any().item())
+    return out if dt == torch.int32 else out.to(dt)
 
 
 def prune_tokens(x: torch.Tensor, keep_idx: torch.Tensor, last_idx=None, neighbor_indices=None,
@@ -172,9 +161,7 @@ def prune_tokens(x: torch.Tensor, keep_idx: torch.Tensor, last_idx=None, neighbo
         if DEBUG_SPARSE:
             validate_neighbor_table(t_new, keep_idx.shape[1], "prune_tokens")
         if dt != torch.int32:
-            t_new = t_new.to(dt)
-        if _distinct_or_unchecked(keep_idx):  # as in remap_neighbor_table
-            _keep_symmetric(neighbor_indices, t_new)
+            t_new = t_new.to(dt)  # no symmetric record, as remap_neighbor_table
     return x_new, idx_new, t_new
 
 

@@ -462,21 +462,3 @@ def test_inference_tensors_get_no_record():
         t = mark_symmetric_table(torch.full((4, 9), -1, dtype=torch.int32))
         assert not is_symmetric_table(t)
     assert not is_symmetric_table(t)
-
-
-def test_repeated_keep_indices_drop_the_record_under_debug():
-    import torch
-
-    import eccv26_tad_amd.neighbor as nb
-
-    keep_ok = torch.tensor([[3, 1, 2], [0, 2, 1]])
-    keep_dup = torch.tensor([[3, 1, 3], [0, 2, 1]])
-    old = nb.DEBUG_SPARSE
-    try:
-        nb.set_debug_sparse(False)
-        assert nb._distinct_or_unchecked(keep_dup)  # unchecked: taken as distinct, as topk gives
-        nb.set_debug_sparse(True)
-        assert nb._distinct_or_unchecked(keep_ok)
-        assert not nb._distinct_or_unchecked(keep_dup)
-    finally:
-        nb.set_debug_sparse(old)

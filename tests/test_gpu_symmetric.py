@@ -13,8 +13,10 @@ partners and no pass for entries without one runs. Checked here:
   one-pass backward and backward-input (vectorized and scalar kernels,
   every dtype), and the float32 paths that ignore the flag;
 * the symmetric results against the fp64 oracle at the north-star bar;
-* the record through the builders, remap / prune, the global conversion and
-  the modules, and that an in-place change drops it.
+* the record on the builders' tables and the global conversion only (remap
+  and prune give none), through the modules, and that an in-place change
+  drops it; a remap with a repeated keep index (one-way entries) gives the
+  oracle's gradients.
 """
 
 from __future__ import annotations
@@ -137,7 +139,7 @@ def test_depthwise_backward_symmetric_is_bit_identical(dev, oracle, dname, c, ke
     assert err <= (TOL if dt in (torch.float16, torch.bfloat16) else 1e-5)
 
 
-def test_record_through_builders_and_prune(dev):
+def test_record_on_builders_only(dev):
     import torch
 
     import eccv26_tad_amd as sv
@@ -149,24 +151,60 @@ def test_record_through_builders_and_prune(dev):
               sv.build_neighbor_table(mask, batched=True), sv.build_neighbor_table(mask, dtype=torch.int64),
               sv.get_initial_neighbor_indices(6, 6, 4, dev, 2)):
         assert sv.is_symmetric_table(t)
+        # the recorded tables really are symmetric: the transpose equals the flipped table
+        tt, coll = sv.transpose_neighbor_table(t)
+        assert coll == 0
+        _eq(tt, t.reshape(-1, 9).flip(1).to(torch.int32), "transposed table vs column-flipped table")
     grid = sv.get_initial_neighbor_indices(6, 6, 4, dev, 2)  # [2, 144, 9] global
+    g = sv.global_neighbor_table(grid, 144)
+    assert sv.is_symmetric_table(g)
+    # remap and prune give no record (their keep indices are not checked)
     keep = torch.stack([torch.randperm(144, generator=torch.Generator().manual_seed(s))[:72] for s in (0, 1)])
     keep = keep.to(dev)
     t2 = sv.remap_neighbor_table(grid, keep)
-    assert sv.is_symmetric_table(t2)
     x = torch.randn(2, 1 + 144, 16, device=dev)
     _, _, t3 = sv.prune_tokens(x, keep, neighbor_indices=grid, num_key_tokens=1)
-    assert sv.is_symmetric_table(t3)
+    assert not sv.is_symmetric_table(t2) and not sv.is_symmetric_table(t3)
     _eq(t2, t3, "prune_tokens table vs remap_neighbor_table")
-    # the recorded tables really are symmetric: the transpose equals the flipped table
-    tt, coll = sv.transpose_neighbor_table(t2)
-    assert coll == 0
-    _eq(tt, t2.reshape(-1, 9).flip(1), "transposed table vs column-flipped table")
-    g = sv.global_neighbor_table(t2, 72)
-    assert sv.is_symmetric_table(g)
-    t2[0, 0, 0] = -1  # an in-place change drops the record (and the view's base's)
-    assert not sv.is_symmetric_table(t2)
-    assert not sv.is_symmetric_table(t2.clone())
+    grid[0, 0, 0] = -1  # an in-place change drops the record (and the view's base's)
+    assert not sv.is_symmetric_table(grid)
+    assert not sv.is_symmetric_table(grid.clone())
+
+
+@pytest.mark.parametrize("depthwise", [False, True])
+def test_repeated_keep_index_gradients(dev, oracle, depthwise):
+    """A keep set that repeats an index (not what topk gives) leaves a remapped
+    table whose copied row has no partners; its gradients still match the
+    oracle (the remap carries no symmetric record, so the backward checks)."""
+    import torch
+
+    import eccv26_tad_amd as sv
+
+    rng = np.random.default_rng(21)
+    grid = sv.get_initial_neighbor_indices(8, 8, 3, dev, 1)  # [1, 192, 9]
+    keep = torch.from_numpy(rng.permutation(192)[:96]).to(dev)
+    keep[10] = keep[11]  # a repeated index
+    t = sv.remap_neighbor_table(grid, keep.view(1, -1))
+    assert not sv.is_symmetric_table(t)
+    tn = t.reshape(-1, 9).cpu().numpy()
+    tt, coll = sv.transpose_neighbor_table(t)
+    assert coll > 0 or not torch.equal(tt, t.reshape(-1, 9).flip(1))  # really one-way entries
+    n, c = 96, 64
+    _say(f"repeated keep index: depthwise {depthwise}, n = {n}")
+    torch.manual_seed(0)
+    m = (sv.SparseDepthwiseConv2d(c) if depthwise else sv.SparseConv2d(c, c)).to(dev).half()
+    x = torch.from_numpy(rng.standard_normal((n, c)).astype(np.float32)).to(dev, torch.float16).requires_grad_(True)
+    y = m(x, t)
+    go = torch.from_numpy(rng.standard_normal((n, c)).astype(np.float32)).to(dev, torch.float16)
+    y.backward(go)
+    torch.cuda.synchronize()
+    w = m.weight.detach().double().cpu().numpy()
+    g = go.double().cpu().numpy()
+    # module weights are (9, C) / (9, C_in, C_out), the oracle's layouts
+    gi_ref = oracle.dw_bwd_in(g, tn, w) if depthwise else oracle.bwd_in(g, tn, w)
+    err = np.abs(x.grad.double().cpu().numpy() - gi_ref).max() / max(np.abs(gi_ref).max(), 1e-30)
+    _say(f"  grad_in max-scaled error {err:.2e}")
+    assert err <= TOL
 
 
 @pytest.mark.parametrize("depthwise", [False, True])
