@@ -983,7 +983,7 @@ __device__ __forceinline__ void transpose8(const u32x4* in, u32x4* out) {
 // quarter of the splits with all its loads in flight, and the quarters are
 // added in order g = 0..3 through LDS, so the order of the sum is fixed.
 // The partials are read once: non-temporal loads.
-template <typename T>
+template <typename T, int CP>
 __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __restrict__ part,
                                                 int splits, int n_off, int c_in, int c_out, int fm, int fn,
                                                 int wgm, int wgn, int n_ci_tiles, int n_co_tiles,
@@ -992,8 +992,9 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
     const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
     const int bm = wgm * fm * 16, bn = wgn * fn * 16;
     // a split's partials: one block of c_in * c_out per work unit (with the
-    // 9 offsets: offsets 0-3, the center's two halves, offsets 5-8)
-    const int units = n_off == 9 ? 10 : n_off;
+    // 9 offsets: offsets 0-3, the center's CP parts, offsets 5-8)
+    static_assert(CP == 2 || CP == 4, "center parts");
+    const int units = n_off == 9 ? 8 + CP : n_off;
     const int64_t per_off = (int64_t)c_in * c_out;
     const int64_t per_split = units * per_off;
     const int64_t quads = (int64_t)n_off * per_off / 4;
@@ -1004,18 +1005,20 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
     if (e < quads) {
         const int ko = (int)(e * 4 / per_off);
         const int64_t within = e * 4 - ko * per_off;
-        const int unit = n_off == 9 && ko > 4 ? ko + 1 : ko;
+        const int unit = n_off == 9 && ko > 4 ? ko + CP - 1 : ko;
         const float* pe = part + unit * per_off + within;
         if (n_off == 9 && ko == 4) {
-            // the center's two halves, added in order per split
-            for (int q = s0; q < s1; q += 4) {
+            // the center's parts, added in order per split (split-major):
+            // 8 loads in flight, 8 / CP splits of CP parts
+            for (int q = s0; q < s1; q += 8 / CP) {
                 f32x4 v[8];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < 8 / CP; ++u) {
                     const bool ok = q + u < s1;
-                    v[2 * u] = ok ? __builtin_nontemporal_load((const f32x4*)(pe + (int64_t)(q + u) * per_split)) : f32x4{0.f, 0.f, 0.f, 0.f};
-                    v[2 * u + 1] = ok ? __builtin_nontemporal_load((const f32x4*)(pe + per_off + (int64_t)(q + u) * per_split))
-                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int pt = 0; pt < CP; ++pt)
+                        v[u * CP + pt] = ok ? __builtin_nontemporal_load((const f32x4*)(pe + pt * per_off + (int64_t)(q + u) * per_split))
+                                            : f32x4{0.f, 0.f, 0.f, 0.f};
                 }
 #pragma unroll
                 for (int u = 0; u < 8; ++u) acc += v[u];
@@ -1121,12 +1124,15 @@ struct BwBigLds {
 // One work unit (split s, unit u, ci tile, co tile = lin) of the
 // backward-weight partials, run by all bw_big_threads threads of a workgroup
 // (k_bw_big, or the backward-weight role of k_bwd_fused) in the LDS block L.
-template <typename T, int FM, int FN, int WGM, int WGN>
+// With the 9 offsets the center offset's rows are split into CP (2 or 4)
+// units: a split holds 8 + CP units.
+template <typename T, int FM, int FN, int WGM, int WGN, int CP>
 __device__ __forceinline__ void bw_big_unit(
     BwBigLds<FM, FN, WGM, WGN>& L, int64_t lin, const T* __restrict__ go, const T* __restrict__ x,
     const int32_t* __restrict__ nbr, float* __restrict__ ws, float* __restrict__ ws_bias, int64_t n,
     int c_in, int c_out, int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int n_off,
     int64_t n_src) {
+    static_assert(CP == 2 || CP == 4, "center parts");
     constexpr int NT = bw_big_threads(FM, FN, WGM, WGN);
     constexpr int NMW = WGM * WGN;     // matrix waves
     constexpr int BM = WGM * FM * 16;  // ci
@@ -1150,22 +1156,24 @@ __device__ __forceinline__ void bw_big_unit(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    // work units of a split: with the 9 offsets, units 0-3 and 6-9 are the
-    // offsets 0-3 and 5-8 over the split's rows, and units 4 and 5 the center
-    // offset over the split's first and second half
-    const int units = n_off == 9 ? 10 : 1;
+    // work units of a split: with the 9 offsets, units 0-3 and 4+CP .. 7+CP
+    // are the offsets 0-3 and 5-8 over the split's rows, and units 4 ..
+    // 3+CP the center offset over consecutive parts of the split
+    // (rows_per_split is a multiple of 256, so each part is whole stages)
+    const int units = n_off == 9 ? 8 + CP : 1;
     const int tiles = units * n_ci_tiles * n_co_tiles;
     const int s = (int)(lin / tiles);
     int rem = (int)(lin - (int64_t)s * tiles);
     const int u = rem / (n_ci_tiles * n_co_tiles);
     rem -= u * n_ci_tiles * n_co_tiles;
-    const int k = n_off == 9 ? (u < 4 ? u : (u < 6 ? 4 : u - 1)) : 0;
+    const int k = n_off == 9 ? (u < 4 ? u : (u < 4 + CP ? 4 : u - CP + 1)) : 0;
     const bool center = n_off == 9 && k == 4;
     const bool compact = n_off == 9 && !center;  // uniform
     const int cit = rem / n_co_tiles, cot = rem % n_co_tiles;
     const int ci0 = cit * BM, co0 = cot * BN;
-    const int64_t r_begin = (int64_t)s * rows_per_split + (center ? (u - 4) * (rows_per_split / 2) : 0);
-    const int64_t r_len = center ? rows_per_split / 2 : rows_per_split;
+    const int64_t part_len = rows_per_split / CP;
+    const int64_t r_begin = (int64_t)s * rows_per_split + (center ? (u - 4) * part_len : 0);
+    const int64_t r_len = center ? part_len : rows_per_split;
     const int rows_raw = (int)max<int64_t>(0, min(n, r_begin + r_len) - r_begin);
     const bool do_bias = ws_bias != nullptr && (n_off == 9 ? center : true) && ci0 == 0;  // uniform
 
@@ -1376,7 +1384,7 @@ __device__ __forceinline__ void bw_big_unit(
                 float v = 0.f;
 #pragma unroll
                 for (int g = 0; g < BW_IROWS; ++g) v += red[g * BN + col];
-                if (co0 + col < c_out) ws_bias[((int64_t)s * 2 + (u - 4)) * c_out + co0 + col] = v;
+                if (co0 + col < c_out) ws_bias[((int64_t)s * CP + (u - 4)) * c_out + co0 + col] = v;
             }
         }
     }
@@ -1389,8 +1397,8 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
     int64_t tpb, int64_t rows_per_split, int n_ci_tiles, int n_co_tiles, int64_t n_blocks, int n_off,
     int64_t n_src) {
     __shared__ BwBigLds<FM, FN, WGM, WGN> lds;
-    bw_big_unit<T, FM, FN, WGM, WGN>(lds, xcd_tile(blockIdx.x, n_blocks), go, x, nbr, ws, ws_bias, n, c_in,
-                                     c_out, tpb, rows_per_split, n_ci_tiles, n_co_tiles, n_off, n_src);
+    bw_big_unit<T, FM, FN, WGM, WGN, 2>(lds, xcd_tile(blockIdx.x, n_blocks), go, x, nbr, ws, ws_bias, n, c_in,
+                                        c_out, tpb, rows_per_split, n_ci_tiles, n_co_tiles, n_off, n_src);
 }
 
 // Backward-input and the backward-weight partials in one launch, for shapes
@@ -1401,7 +1409,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bw_big(
 // a workgroup barrier waits only for waves that have not ended). The two
 // roles share one LDS block. The host launches it only when the grid fits
 // one workgroup per CU and the tile kernel's registers fit this launch's.
-template <typename T, int CR, int GFM, int GFN, int GD, int GWS, int FM, int FN, int WGM, int WGN>
+template <typename T, int CR, int GFM, int GFN, int GD, int GWS, int FM, int FN, int WGM, int WGN, int CP>
 __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bwd_fused(
     const T* __restrict__ go, const int32_t* __restrict__ nbr, const T* __restrict__ wb, T* __restrict__ gi,
     int n_in, int n_col_tiles, uint32_t* __restrict__ orphan_flag, const T* __restrict__ x,
@@ -1413,8 +1421,8 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bwd_fused(
     __shared__ __align__(16) char lds[sizeof(GL) > sizeof(BL) ? sizeof(GL) : sizeof(BL)];
     const int64_t lin = xcd_tile(blockIdx.x, n_blocks);
     if (lin < n_bw) {
-        bw_big_unit<T, FM, FN, WGM, WGN>(*(BL*)lds, lin, go, x, nbr, ws, ws_bias, n, n_in, CR, tpb,
-                                         rows_per_split, n_ci_tiles, n_co_tiles, 9, n);
+        bw_big_unit<T, FM, FN, WGM, WGN, CP>(*(BL*)lds, lin, go, x, nbr, ws, ws_bias, n, n_in, CR, tpb,
+                                             rows_per_split, n_ci_tiles, n_co_tiles, 9, n);
     } else {
         if (threadIdx.x >= 256 * GWS) return;
         gg_wide_tile<T, MODE_BWDIN, CR, GFM, GFN, GD, GWS>(*(GL*)lds, lin - n_bw, go, nbr, wb, nullptr, 0, gi, n,
@@ -1426,7 +1434,7 @@ __global__ __launch_bounds__(bw_big_threads(FM, FN, WGM, WGN)) void k_bwd_fused(
 // workgroup also runs the pass for entries without a symmetric partner of a
 // backward-input computed before it (flag-gated as in k_orphans,
 // orphan_exact), which saves that pass a launch of its own.
-template <typename T>
+template <typename T, int CP>
 __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ part,
                                                    const float* __restrict__ part_b, int splits,
                                                    int n_off, int c_in, int c_out, int fm, int fn, int wgm,
@@ -1436,11 +1444,11 @@ __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ par
     // workgroups [0, quad_blocks) reduce gw, the rest the bias
     const int64_t quad_blocks = ((int64_t)n_off * c_in * c_out / 4 + 63) / 64;
     if ((int64_t)blockIdx.x < quad_blocks)
-        bw_reduce_quads<T>(blockIdx.x, part, splits, n_off, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles,
-                           n_co_tiles, gw);
+        bw_reduce_quads<T, CP>(blockIdx.x, part, splits, n_off, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles,
+                               n_co_tiles, gw);
     else if (gb)
         bw_reduce_bias<T>(((int64_t)blockIdx.x - quad_blocks) * 256 + threadIdx.x, part_b,
-                          n_off == 9 ? 2 * splits : splits, c_out, gb);
+                          n_off == 9 ? CP * splits : splits, c_out, gb);
     if (!oj.gi || (oj.flag && *oj.flag == 0u) || blockIdx.x != 0) return;
     // the exact pass for entries without a symmetric partner: one workgroup
     orphan_exact<T, false, 256>((const T*)oj.go, oj.nbr, (const T*)oj.w, (T*)oj.gi, oj.n, oj.c_in, oj.c_out,
@@ -1783,19 +1791,25 @@ static int bw_dispatch(const BwPlan& p, const void* go, const void* x, const int
 }
 
 // Ordered reduction of the large-tile partials into gw / gb (k_bw_reduce),
-// which also runs the orphan job oj (may be NULL).
+// which also runs the orphan job oj (may be NULL); cparts is the units'
+// center split.
 static void bw_big_reduce(int dtype, const BigCfg& bc, int splits, const float* part, const float* part_b,
-                          void* gw, void* gb, int c_in, int c_out, const OrphanJob* oj, hipStream_t s) {
+                          void* gw, void* gb, int c_in, int c_out, const OrphanJob* oj, int cparts, hipStream_t s) {
     const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
     const int64_t blocks = cdiv((int64_t)9 * c_in * c_out / 4, 64) + (gb ? cdiv(c_out, 256) : 0);
     const dim3 grid((unsigned)blocks);
     const OrphanJob job = oj ? *oj : OrphanJob{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
-    if (dtype == SVTAD_F16)
-        hipLaunchKernelGGL((k_bw_reduce<f16>), grid, dim3(256), 0, s, part, gb ? part_b : nullptr, splits, 9,
-                           c_in, c_out, bc.fm, bc.fn, bc.wgm, bc.wgn, nci, nco, (f16*)gw, (f16*)gb, job);
-    else
-        hipLaunchKernelGGL((k_bw_reduce<bf16>), grid, dim3(256), 0, s, part, gb ? part_b : nullptr, splits, 9,
-                           c_in, c_out, bc.fm, bc.fn, bc.wgm, bc.wgn, nci, nco, (bf16*)gw, (bf16*)gb, job);
+#define SVTAD_REDUCE(T, CP)                                                                                  \
+    hipLaunchKernelGGL((k_bw_reduce<T, CP>), grid, dim3(256), 0, s, part, gb ? part_b : nullptr, splits, 9, c_in, \
+                       c_out, bc.fm, bc.fn, bc.wgm, bc.wgn, nci, nco, (T*)gw, (T*)gb, job)
+    if (dtype == SVTAD_F16) {
+        if (cparts == 4) SVTAD_REDUCE(f16, 4);
+        else SVTAD_REDUCE(f16, 2);
+    } else {
+        if (cparts == 4) SVTAD_REDUCE(bf16, 4);
+        else SVTAD_REDUCE(bf16, 2);
+    }
+#undef SVTAD_REDUCE
 }
 
 int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int32_t* nbr,
@@ -1814,7 +1828,7 @@ int bw_mfma(int dtype, const BwPlan& p, const void* go, const void* x, const int
     if (!gw) return SVTAD_OK;  // partials only
     BigCfg bc;
     if (big_cfg(c_in, c_out, &bc)) {
-        bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, oj, s);
+        bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, oj, 2, s);
         *oj_taken = oj != nullptr;
         return SVTAD_OK;
     }
@@ -1840,6 +1854,16 @@ static int fused_env(FusedChoice* c) {
     return 1;
 }
 
+// Center-offset units per split of the one-launch backward (two in the
+// separate backward-weight launch). Its grid must fit one round, so it runs
+// few, long splits, and at low keep the off-center units visit few rows. At
+// C = 256 (config 4 at 10 % keep: 2 splits of 2560 rows) the two center
+// halves of 20 stages each were by far the longest units, and four parts
+// took the step from 48.7 to 42.8 us. At C = 192 four parts measured slower
+// (10 / 25 / 40 % keep: 26.4 -> 27.6, 34.6 -> 35.4, 49.1 -> 50.5 us per
+// step), so it keeps two there.
+constexpr int fused_cparts(int c) { return c == 256 ? 4 : 2; }
+
 // C_in = C_out = C: backward-input tiles of GFM row fragments and GFN column
 // fragments per wave, backward-weight units on the large-tile configuration
 // (BFM, BFN, BWM, BWN) of that width.
@@ -1849,15 +1873,23 @@ static void launch_fused(const void* go, const int32_t* nbr, const void* wb, voi
                          int64_t n_gg, int64_t n_bw, bool sym, hipStream_t s) {
     constexpr int NCI = C / (16 * BWM * BFM), NCO = C / (16 * BWN * BFN);
     static_assert(NCI * 16 * BWM * BFM == C && NCO * 16 * BWN * BFN == C, "whole tiles");
-    hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, BFM, BFN, BWM, BWN>), dim3((unsigned)(n_gg + n_bw)),
+    constexpr int CP = fused_cparts(C);
+    hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, BFM, BFN, BWM, BWN, CP>), dim3((unsigned)(n_gg + n_bw)),
                        dim3(bw_big_threads(BFM, BFN, BWM, BWN)), 0, s, (const T*)go, nbr, (const T*)wb, (T*)gi, C,
                        C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, NCI, NCO, n_bw, n_gg + n_bw, sym);
 }
 
-// Units per split of the one-launch backward's large-tile configuration at
-// width c (10 work units per ci x co tile): c = 192 takes one 192 x 192 tile,
-// c = 256 two 128 x 256 tiles.
-static int fused_units(int c) { return c == 192 ? 10 : (c == 256 ? 20 : 0); }
+// Workgroups per split of the one-launch backward's large-tile configuration
+// at width c (8 + fused_cparts(c) work units per ci x co tile): c = 192
+// takes one 192 x 192 tile, c = 256 two 128 x 256 tiles.
+static int fused_units(int c) { return (8 + fused_cparts(c)) * (c == 192 ? 1 : (c == 256 ? 2 : 0)); }
+// Workspace bytes of the one-launch backward's partials for `splits` splits
+// (c_in = c_out): a c_in x c_out fp32 tile per work unit, then one bias row per
+// center unit.
+static size_t fused_ws_bytes(int64_t splits, int c_in, int c_out) {
+    const int p = fused_cparts(c_in);
+    return (size_t)splits * ((size_t)(8 + p) * c_in * c_out + (size_t)p * c_out) * 4;
+}
 
 int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, int* gfm, int* gfn,
                    BwPlan* p_out) {
@@ -1872,6 +1904,9 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
     if (env < 0) return 0;
     const int64_t cu = cu_count();
     auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (C / (64 * fn)); };
+    // the most splits whose partials fit the workspace plan_bw sized (p0)
+    int64_t fit = p0.splits;
+    while (fit > 0 && fused_ws_bytes(fit, c_in, c_out) > p0.ws_bytes) --fit;
     if (env == 0) {
         // C = 192: the tile shape the backward-input launch would take
         // (pick_fm), or a full-width tile of three row fragments in place of
@@ -1899,7 +1934,7 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         bool found = false;
         for (int q = 0; q < nc && !found; ++q) {
             const int64_t room = (cu - n_gg(cands[q].gfm, cands[q].gfn)) / U;
-            const int64_t sp = std::min<int64_t>(p0.splits, room);
+            const int64_t sp = std::min<int64_t>(fit, room);
             if (sp >= 1 && sp * 2560 >= n) {
                 ch = FusedChoice{cands[q].gfm, cands[q].gfn, (int)sp};
                 found = true;
@@ -1908,13 +1943,13 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         if (!found) return 0;
     } else {
         // a forced split count is clamped to what the launch accepts: at most
-        // the plan's count (the workspace is sized for it), and enough splits
+        // the count whose partials the workspace holds, and enough splits
         // that none exceeds the LDS row list (kMaxSplitRows)
         const int64_t lo = cdiv(n, (int64_t)kMaxSplitRows);
-        if (lo > p0.splits)
+        if (lo > fit)
             return set_error(SVTAD_ERR_INVALID, "bwd_packed: SVTAD_BWD_FUSED has no split count the workspace holds");
-        if (ch.splits <= 0) ch.splits = p0.splits;
-        ch.splits = (int)std::min<int64_t>(std::max<int64_t>(ch.splits, lo), p0.splits);
+        if (ch.splits <= 0) ch.splits = (int)fit;
+        ch.splits = (int)std::min<int64_t>(std::max<int64_t>(ch.splits, lo), fit);
         const bool ok192 = C == 192 && ((ch.gfm == 3 && ch.gfn == 1) || (ch.gfm == 3 && ch.gfn == 3) ||
                                         (ch.gfm == 4 && ch.gfn == 3));
         const bool ok256 = C == 256 && ch.gfm == 3 && ch.gfn == 2;
@@ -1941,12 +1976,11 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     BwPlan p;
     const int fp = bwd_fused_plan(dtype, p0, n, c_in, c_out, &ch.gfm, &ch.gfn, &p);
     if (fp != 1) return fp;
-    const size_t need = (size_t)p.splits * 10 * c_in * c_out * 4 + (gb ? (size_t)2 * p.splits * c_out * 4 : 0);
-    const int st = check_split_plan("bwd_packed", p, n, need, ws_bytes);
+    const int st = check_split_plan("bwd_packed", p, n, fused_ws_bytes(p.splits, c_in, c_out), ws_bytes);
     if (st) return st;
     auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (c_in / (64 * fn)); };
     float* part = (float*)ws;
-    float* part_b = gb ? part + (int64_t)p.splits * 10 * c_in * c_out : nullptr;
+    float* part_b = gb ? part + (int64_t)p.splits * (8 + fused_cparts(c_in)) * c_in * c_out : nullptr;
     const int64_t gg = n_gg(ch.gfm, ch.gfn), bw = (int64_t)fused_units(c_in) * p.splits;
     bool launched = false;
 #define SVTAD_FUSED_CASE(C, FM, FN, BFM, BFN, BWM, BWN)                                                   \
@@ -1970,7 +2004,7 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     const OrphanJob job{go, nbr, w, gi, n, c_in, c_out, tpb, flag};
     BigCfg bc;
     big_cfg(c_in, c_out, &bc);  // the configuration launch_fused used (6,3,2,4 / 4,4,2,4)
-    bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, &job, s);
+    bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, &job, fused_cparts(c_in), s);
     return 1;
 }
 
@@ -2012,10 +2046,10 @@ static int launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, con
     const dim3 grid((unsigned)cdiv((int64_t)c_in * c_out / 4, 64));
     const OrphanJob none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
     if (out_f32)
-        hipLaunchKernelGGL((k_bw_reduce<float>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
+        hipLaunchKernelGGL((k_bw_reduce<float, 2>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
                            p.splits, 1, c_in, c_out, FM, FN, WGM, WGN, nci, nco, (float*)out, (float*)nullptr, none);
     else
-        hipLaunchKernelGGL((k_bw_reduce<T>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
+        hipLaunchKernelGGL((k_bw_reduce<T, 2>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
                            p.splits, 1, c_in, c_out, FM, FN, WGM, WGN, nci, nco, (T*)out, (T*)nullptr, none);
     return SVTAD_OK;
 }

@@ -393,9 +393,12 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x2")  # the C = 256 shape
     assert _fused_plan(lib, 3136, 192, 192, 1)[0] == -1
-    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 7))  # the plan's 7 splits
+    # C = 256 splits the center offset in four units (12 per split): the
+    # workspace sized for the plan's 7 splits of 10 units holds 5
+    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 5))
     # forced split counts are clamped to what the launch accepts: no more than
-    # the plan's (the workspace holds that many), no split above 4096 rows
+    # the workspace holds (the plan's count at C = 192), no split above 4096
+    # rows
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x3:1000")
     assert _fused_plan(lib, 3136, 192, 192, 1) == (1, (3, 3, 7))
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x1:1")

@@ -9,8 +9,10 @@ SVTAD_BWD_FUSED=off turns it off and "<gfm>x<gfn>[:<splits>]" forces a tile
 shape and split count. Checked:
 
 * forced tiles with the two-launch path's row tile and the plan's split
-  count: bit-identical (same row tiles, same offsets per wave set, same
-  splits);
+  count: bit-identical at C = 192 (same row tiles, same offsets per wave set,
+  same splits). At C = 256 the one-launch backward splits the center offset
+  in four units, not two, and its workspace holds fewer splits: grad_x is
+  bit-identical, the weight and bias gradients within one rounding;
 * the automatic choice (which may take fewer splits), other row tiles and
   forced split counts: within one rounding of the two-launch path, and every
   result against the fp64 oracle at the north-star bar;
@@ -155,21 +157,20 @@ def test_fused_per_sample_table(dev, oracle, monkeypatch, keep):
 
 def test_fused_config4(dev, oracle, monkeypatch):
     """Config 4 at 10 % keep (C = 256 bf16, N = 4916): 128-column tiles of
-    three row fragments beside 128 x 256 backward-weight units. With the
-    plan's split count the results equal the two launches bit for bit; the
-    automatic choice takes 2 splits."""
+    three row fragments beside 128 x 256 backward-weight units, the center
+    offset in four units per split. The backward-input tiles are the two
+    launches' (grad_x bit for bit); the weight and bias gradients sum over
+    other splits and parts. The automatic choice takes 2 splits."""
     ops, P = _problem(dev, oracle, 0.10, "bfloat16", 3600, c=256, grid=(2, 96, 16, 16))
     _say(f"fused backward, config 4, n = {P['n']}")
     ref = _bwd(ops, P, monkeypatch, "off")
-    got = _bwd(ops, P, monkeypatch, "3x2")
-    for name, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref):
-        assert np.array_equal(a, b), (name, _scaled(a, b))
-    for mode in (None, "3x2:3"):
+    for mode in (None, "3x2", "3x2:3"):
         got = _bwd(ops, P, monkeypatch, mode)
         d = {k: _scaled(a, b) for k, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref)}
         e = _oracle_errs(oracle, P, got)
         _say(f"  {mode or 'automatic'}: vs two-launch", {k: f"{v:.2e}" for k, v in d.items()},
              "vs oracle", {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
+        assert np.array_equal(got[0], ref[0]), mode
         for k, v in d.items():
             assert v <= 4e-3, (mode, k, v)
         for k, v in e.items():
