@@ -1856,13 +1856,12 @@ static int fused_env(FusedChoice* c) {
 
 // Center-offset units per split of the one-launch backward (two in the
 // separate backward-weight launch). Its grid must fit one round, so it runs
-// few, long splits, and at low keep the off-center units visit few rows. At
-// C = 256 (config 4 at 10 % keep: 2 splits of 2560 rows) the two center
-// halves of 20 stages each were by far the longest units, and four parts
-// took the step from 48.7 to 42.8 us. At C = 192 four parts measured slower
-// (10 / 25 / 40 % keep: 26.4 -> 27.6, 34.6 -> 35.4, 49.1 -> 50.5 us per
-// step), so it keeps two there.
-constexpr int fused_cparts(int c) { return c == 256 ? 4 : 2; }
+// few, long splits, and at low keep the off-center units visit few rows:
+// the center's halves were a split's longest units (config 4 at 10 % keep,
+// 2 splits of 2560 rows: 20 stages against about 4). Four parts: config 4
+// at 10 % keep 49.1 -> 40.8 us per step, c2 at 10 / 25 / 40 % keep 26.6 ->
+// 26.1, 34.0 -> 34.2, 49.7 -> 47.6 us.
+constexpr int kFusedCenterParts = 4;
 
 // C_in = C_out = C: backward-input tiles of GFM row fragments and GFN column
 // fragments per wave, backward-weight units on the large-tile configuration
@@ -1873,21 +1872,19 @@ static void launch_fused(const void* go, const int32_t* nbr, const void* wb, voi
                          int64_t n_gg, int64_t n_bw, bool sym, hipStream_t s) {
     constexpr int NCI = C / (16 * BWM * BFM), NCO = C / (16 * BWN * BFN);
     static_assert(NCI * 16 * BWM * BFM == C && NCO * 16 * BWN * BFN == C, "whole tiles");
-    constexpr int CP = fused_cparts(C);
-    hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, BFM, BFN, BWM, BWN, CP>), dim3((unsigned)(n_gg + n_bw)),
-                       dim3(bw_big_threads(BFM, BFN, BWM, BWN)), 0, s, (const T*)go, nbr, (const T*)wb, (T*)gi, C,
+    hipLaunchKernelGGL((k_bwd_fused<T, C, GFM, GFN, 2, 2, BFM, BFN, BWM, BWN, kFusedCenterParts>),
+                       dim3((unsigned)(n_gg + n_bw)), dim3(bw_big_threads(BFM, BFN, BWM, BWN)), 0, s, (const T*)go, nbr, (const T*)wb, (T*)gi, C,
                        C / (64 * GFN), flag, (const T*)x, part, part_b, n, tpb, rps, NCI, NCO, n_bw, n_gg + n_bw, sym);
 }
 
 // Workgroups per split of the one-launch backward's large-tile configuration
-// at width c (8 + fused_cparts(c) work units per ci x co tile): c = 192
+// at width c (8 + kFusedCenterParts work units per ci x co tile): c = 192
 // takes one 192 x 192 tile, c = 256 two 128 x 256 tiles.
-static int fused_units(int c) { return (8 + fused_cparts(c)) * (c == 192 ? 1 : (c == 256 ? 2 : 0)); }
-// Workspace bytes of the one-launch backward's partials for `splits` splits
-// (c_in = c_out): a c_in x c_out fp32 tile per work unit, then one bias row per
-// center unit.
+static int fused_units(int c) { return (8 + kFusedCenterParts) * (c == 192 ? 1 : (c == 256 ? 2 : 0)); }
+// Workspace bytes of the one-launch backward's partials for `splits` splits:
+// a c_in x c_out fp32 tile per work unit, then one bias row per center unit.
 static size_t fused_ws_bytes(int64_t splits, int c_in, int c_out) {
-    const int p = fused_cparts(c_in);
+    constexpr int p = kFusedCenterParts;
     return (size_t)splits * ((size_t)(8 + p) * c_in * c_out + (size_t)p * c_out) * 4;
 }
 
@@ -1980,7 +1977,7 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     if (st) return st;
     auto n_gg = [&](int fm, int fn) { return cdiv(n, 16 * fm) * (c_in / (64 * fn)); };
     float* part = (float*)ws;
-    float* part_b = gb ? part + (int64_t)p.splits * (8 + fused_cparts(c_in)) * c_in * c_out : nullptr;
+    float* part_b = gb ? part + (int64_t)p.splits * (8 + kFusedCenterParts) * c_in * c_out : nullptr;
     const int64_t gg = n_gg(ch.gfm, ch.gfn), bw = (int64_t)fused_units(c_in) * p.splits;
     bool launched = false;
 #define SVTAD_FUSED_CASE(C, FM, FN, BFM, BFN, BWM, BWN)                                                   \
@@ -2004,7 +2001,7 @@ int bwd_fused_mfma(int dtype, const BwPlan& p0, const void* go, const void* x, c
     const OrphanJob job{go, nbr, w, gi, n, c_in, c_out, tpb, flag};
     BigCfg bc;
     big_cfg(c_in, c_out, &bc);  // the configuration launch_fused used (6,3,2,4 / 4,4,2,4)
-    bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, &job, fused_cparts(c_in), s);
+    bw_big_reduce(dtype, bc, p.splits, part, part_b, gw, gb, c_in, c_out, &job, kFusedCenterParts, s);
     return 1;
 }
 

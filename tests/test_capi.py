@@ -354,18 +354,22 @@ def _fused_plan(lib, n, ci, co, dt):
 def test_bwd_fused_plan_at_config_2(lib, monkeypatch):
     """The one-launch backward's choice at config 2 (C = 192 fp16, 256 CUs
     assumed on a host without a GPU): the backward-input tiles and the
-    backward-weight units fit one workgroup per CU at 10-40 % keep, with
-    splits of at most 2560 rows; 55 % keep and above keep two launches.
-    Other widths than 192 and 256, and f32, never fuse."""
+    backward-weight units (12 per split: the center offset in four parts)
+    fit one workgroup per CU at 10-40 % keep, with splits of at most 2560
+    rows whose partials fit the backward-weight workspace; 55 % keep and above
+    keep two launches. Other widths than 192 and 256, and f32, never fuse."""
     monkeypatch.delenv("SVTAD_BWD_FUSED", raising=False)
-    want = {3136: (1, (3, 1, 5)), 7840: (1, (3, 3, 8)), 12544: (1, (4, 3, 6)),
+    want = {3136: (1, (3, 1, 4)), 7840: (1, (3, 3, 7)), 12544: (1, (4, 3, 5)),
             17248: (0, (0, 0, 0)), 21952: (0, (0, 0, 0)), 31360: (0, (0, 0, 0))}
+    lib.svtad_bwd_w_workspace_bytes.restype = ctypes.c_size_t
     for n, w in want.items():
         st, got = _fused_plan(lib, n, 192, 192, 1)
         assert (st, got) == w, (n, st, got)
         for tr, tc, sp in [got] if st == 1 else []:
             tiles = -(-n // (16 * tr)) * (192 // (64 * tc))
-            assert tiles + 10 * sp <= 256  # one workgroup per CU
+            assert tiles + 12 * sp <= 256  # one workgroup per CU
+            need = sp * (12 * 192 * 192 + 4 * 192) * 4
+            assert need <= lib.svtad_bwd_w_workspace_bytes(ctypes.c_int64(n), 192, 192, 1)
     assert _fused_plan(lib, 3136, 192, 192, 2)[0] == 1  # bf16
     assert _fused_plan(lib, 3136, 192, 192, 0)[0] == 0  # f32: VALU kernels
     # config 4 (C = 256 bf16): 128-column tiles of three row fragments and 2
@@ -383,8 +387,10 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x3:4")
     st, (tr, tc, sp) = _fused_plan(lib, 3136, 192, 192, 1)
     assert (st, tr, tc, sp) == (1, 3, 3, 4)
-    monkeypatch.setenv("SVTAD_BWD_FUSED", "4x3")  # the plan's split count (7 at 3136 rows)
-    assert _fused_plan(lib, 3136, 192, 192, 1) == (1, (4, 3, 7))
+    # without a count: the most splits whose partials the backward-weight
+    # workspace holds (sized for 7 splits of 10 units at 3136 rows: 5 of 12)
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "4x3")
+    assert _fused_plan(lib, 3136, 192, 192, 1) == (1, (4, 3, 5))
     monkeypatch.setenv("SVTAD_BWD_FUSED", "5x3")
     st, _ = _fused_plan(lib, 3136, 192, 192, 1)
     assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
@@ -393,14 +399,11 @@ def test_bwd_fused_plan_override(lib, monkeypatch):
     assert st == -1 and b"SVTAD_BWD_FUSED" in lib.svtad_last_error()
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x2")  # the C = 256 shape
     assert _fused_plan(lib, 3136, 192, 192, 1)[0] == -1
-    # C = 256 splits the center offset in four units (12 per split): the
-    # workspace sized for the plan's 7 splits of 10 units holds 5
-    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 5))
+    assert _fused_plan(lib, 4916, 256, 256, 2) == (1, (3, 2, 5))  # 5 of 12 units in the workspace of 7 x 10
     # forced split counts are clamped to what the launch accepts: no more than
-    # the workspace holds (the plan's count at C = 192), no split above 4096
-    # rows
+    # the workspace holds, no split above 4096 rows
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x3:1000")
-    assert _fused_plan(lib, 3136, 192, 192, 1) == (1, (3, 3, 7))
+    assert _fused_plan(lib, 3136, 192, 192, 1) == (1, (3, 3, 5))
     monkeypatch.setenv("SVTAD_BWD_FUSED", "3x1:1")
     st, (tr, tc, sp) = _fused_plan(lib, 12544, 192, 192, 1)
     assert st == 1 and (tr, tc) == (3, 1) and sp == 4  # 3328 rows each

@@ -8,11 +8,10 @@ needed);
 SVTAD_BWD_FUSED=off turns it off and "<gfm>x<gfn>[:<splits>]" forces a tile
 shape and split count. Checked:
 
-* forced tiles with the two-launch path's row tile and the plan's split
-  count: bit-identical at C = 192 (same row tiles, same offsets per wave set,
-  same splits). At C = 256 the one-launch backward splits the center offset
-  in four units, not two, and its workspace holds fewer splits: grad_x is
-  bit-identical, the weight and bias gradients within one rounding;
+* forced tiles with the two-launch path's row tile: grad_x bit-identical
+  (same row tiles, same offsets per wave set). The one-launch backward
+  splits the center offset in four units per split, not two, and takes
+  fewer splits, so the weight and bias gradients sum in another order;
 * the automatic choice (which may take fewer splits), other row tiles and
   forced split counts: within one rounding of the two-launch path, and every
   result against the fp64 oracle at the north-star bar;
@@ -103,9 +102,9 @@ def _scaled(a, b):
 
 
 # Tile shapes with the row tile of the two-launch backward-input at that N
-# (three row fragments below 40 % keep, four at 40 %): with the plan's split
-# count they give bit-identical results. The automatic choice (fewer splits
-# where the grid needs it) and the other forced shapes sum in another order.
+# (three row fragments below 40 % keep, four at 40 %) give grad_x bit for
+# bit. Every mode's weight and bias gradients (other splits, the center in
+# four parts) and the other shapes' grad_x sum in another order.
 @pytest.mark.parametrize("keep,dname,same,other", [
     (0.10, "float16", ("3x1", "3x3"), (None, "4x3", "3x3:4")),
     (0.25, "float16", ("3x1", "3x3"), (None, "4x3", "3x3:4")),
@@ -118,10 +117,9 @@ def test_fused_matches_two_launch(dev, oracle, monkeypatch, keep, dname, same, o
     ref = _bwd(ops, P, monkeypatch, "off")
     for mode in same:
         got = _bwd(ops, P, monkeypatch, mode)
-        for name, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref):
-            assert np.array_equal(a, b), (mode, name, _scaled(a, b))
-    _say(f"  {', '.join(same)}: bit-identical to the two-launch path")
-    for mode in other:
+        assert np.array_equal(got[0], ref[0]), (mode, "grad_x", _scaled(got[0], ref[0]))
+    _say(f"  {', '.join(same)}: grad_x bit-identical to the two-launch path")
+    for mode in (*same, *other):
         got = _bwd(ops, P, monkeypatch, mode)
         d = {k: _scaled(a, b) for k, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref)}
         e = _oracle_errs(oracle, P, got)
@@ -140,14 +138,16 @@ def test_fused_matches_two_launch(dev, oracle, monkeypatch, keep, dname, same, o
 @pytest.mark.parametrize("keep", [0.10, 0.25])
 def test_fused_per_sample_table(dev, oracle, monkeypatch, keep):
     """Per-sample neighbor indices (tokens_per_batch = n / B): the one-launch
-    backward equals the two-launch path bit for bit with the same tile and
-    splits, and the oracle (on the global form of the same table)."""
+    backward's grad_x equals the two-launch path's bit for bit with the same
+    tile, its weight and bias gradients within one rounding, and every result
+    the oracle's (on the global form of the same table)."""
     ops, P = _problem(dev, oracle, keep, "float16", 3500 + int(keep * 100), per_sample=True)
     _say(f"fused backward, per-sample table, keep {keep}, n = {P['n']}, tpb = {P['tpb']}")
     ref = _bwd(ops, P, monkeypatch, "off")
     got = _bwd(ops, P, monkeypatch, "3x1")
-    for name, a, b in zip(("grad_x", "grad_w", "grad_b"), got, ref):
-        assert np.array_equal(a, b), (name, _scaled(a, b))
+    assert np.array_equal(got[0], ref[0]), _scaled(got[0], ref[0])
+    for name, a, b in zip(("grad_w", "grad_b"), got[1:], ref[1:]):
+        assert _scaled(a, b) <= 4e-3, (name, _scaled(a, b))
     got = _bwd(ops, P, monkeypatch, None)
     e = _oracle_errs(oracle, P, got)
     _say("  automatic vs oracle", {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
@@ -190,10 +190,8 @@ def test_fused_orphans(dev, oracle, monkeypatch):
         _say(f"  {mode or 'automatic'}: grad_x vs two-launch {d:.2e}, vs oracle",
              {k: f"{v:.2e}" for k, v in e.items()}, f"(bar {TOL:g})")
         assert d <= 4e-3, (mode, d)
-        if mode is None:  # possibly fewer splits: another summation order
-            assert _scaled(got[1], ref[1]) <= 4e-3 and _scaled(got[2], ref[2]) <= 4e-3
-        else:
-            assert np.array_equal(got[1], ref[1]) and np.array_equal(got[2], ref[2]), mode
+        # other splits and the center in four parts: another summation order
+        assert _scaled(got[1], ref[1]) <= 4e-3 and _scaled(got[2], ref[2]) <= 4e-3, mode
         for k, v in e.items():
             assert v <= TOL, (mode, k, v)
 

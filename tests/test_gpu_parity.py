@@ -341,13 +341,16 @@ def test_orphan_flag_wide_path(dev, oracle, c, dname):
 
 @pytest.mark.parametrize("ci,co,dname", [(192, 192, "float16"), (64, 64, "bfloat16"),
                                          (48, 64, "float16"), (128, 96, "bfloat16")])
-def test_bwd_packed_matches(dev, oracle, ci, co, dname):
+def test_bwd_packed_matches(dev, oracle, ci, co, dname, monkeypatch):
     """bwd_packed (the autograd backward in one call) gives what bwd_in_packed +
-    bwd_w_bias give: bit-identical on symmetric tables (same kernels, no
-    atomics), within tolerance of the oracle when one-way links send work to
-    the orphan pass (inside the reduction for the large-tile shapes, a pass of
-    its own for 48 -> 64; 128 -> 96 has no packed backward-input layout and
-    falls back to the two calls)."""
+    bwd_w_bias give: bit-identical on symmetric tables in its two-launch form
+    (same kernels, no atomics); its one-launch form at 192 channels gives
+    grad_x bit for bit and sums the weight and bias gradients in another
+    order (fewer splits, the center offset in four parts). Within tolerance of
+    the oracle when one-way links send work to the orphan pass (inside the
+    reduction for the large-tile shapes, a pass of its own for 48 -> 64;
+    128 -> 96 has no packed backward-input layout and falls back to the two
+    calls)."""
     import opentad_sparse_ops as ops
     import torch
 
@@ -360,12 +363,19 @@ def test_bwd_packed_matches(dev, oracle, ci, co, dname):
     Ts = _t(sym, dev, _dt("int32"))
     _, pb = ops.pack_weight(W, False, True)
     assert (pb.numel() > 0) == (co in (64, 128, 192, 256, 512))
-    gi, gw, gb = ops.bwd_packed(G, X, Ts, W, pb, ci, 0, True)
     gi2 = ops.bwd_in_packed(G, Ts, W, pb, n, ci, 0)
     gw2, gb2 = ops.bwd_w_bias(G, X, Ts, ci, 0, True)
+    monkeypatch.setenv("SVTAD_BWD_FUSED", "off")
+    gi, gw, gb = ops.bwd_packed(G, X, Ts, W, pb, ci, 0, True)
     assert torch.equal(gi, gi2) and torch.equal(gw, gw2) and torch.equal(gb, gb2)
     _, gw3, gb3 = ops.bwd_packed(G, X, Ts, W, pb, ci, 0, False)
     assert torch.equal(gw3, gw2) and gb3.numel() == 0
+    monkeypatch.delenv("SVTAD_BWD_FUSED")
+    gi, gw, gb = ops.bwd_packed(G, X, Ts, W, pb, ci, 0, True)  # one launch where it applies
+    assert torch.equal(gi, gi2)
+    for a, r in ((gw, gw2), (gb, gb2)):
+        d = (a.double() - r.double()).abs().max() / r.double().abs().max().clamp_min(1e-30)
+        assert float(d) <= 4e-3, float(d)
     rng = np.random.default_rng(41)
     asym = sym.copy()
     for q, i in enumerate(rng.choice(n, size=10, replace=False)):
