@@ -850,7 +850,7 @@ def main():
     prune = None if args.no_sweep else prune_measure(dev, 20, not args.no_cpu)
     adapter = None if args.no_sweep else adapter_rows(dev, 20)
     depthwise = None if args.no_sweep else depthwise_measure(dev, 20)
-    large = None if args.no_sweep else large_channel_measure(dev, 10)
+    large = None if args.no_sweep else large_channel_measure(dev, 30)  # 30 steps: single runs of 10 moved by ~5 %
     if adapter is not None:
         log(f"bench: adapter {adapter}")
 
