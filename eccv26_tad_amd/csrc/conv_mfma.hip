@@ -1921,13 +1921,14 @@ int bwd_fused_plan(int dtype, const BwPlan& p0, int64_t n, int c_in, int c_out, 
         // The split count drops below the plan's so that the grid fits, while
         // splits stay within 2560 rows: the tile role takes as long as the
         // longer splits, and fewer partials shorten the reduction.
-        // Measured (step medians): c2 10 % keep 41.0 us two-launch, 36.8
-        // fused with full-width tiles and 7 splits, 32.5 with 64-column tiles
-        // and 5; c2 40 % keep 62.3 two-launch, 53.4 fused with 6 splits (55.1
-        // with 5, 61.1 with 4); c4 10 % keep (C = 256) 55.4 two-launch, 49.9
-        // fused with 2 splits (50.2 with 3, 50.4 with 4, 52.4 with the plan's
-        // 5 over more than one round). A grid over one round at c2 55 % was
-        // slower.
+        // Measured (step medians, the center offset then in two units per
+        // split, so the workspace held the plan's count): c2 10 % keep 41.0
+        // us two-launch, 36.8 fused with full-width tiles and 7 splits, 32.5
+        // with 64-column tiles and 5; c2 40 % keep 62.3 two-launch, 53.4
+        // fused with 6 splits (55.1 with 5, 61.1 with 4); c4 10 % keep
+        // (C = 256) 55.4 two-launch, 49.9 fused with 2 splits (50.2 with 3,
+        // 50.4 with 4, 52.4 with the plan's 5 over more than one round). A
+        // grid over one round at c2 55 % was slower.
         bool found = false;
         for (int q = 0; q < nc && !found; ++q) {
             const int64_t room = (cu - n_gg(cands[q].gfm, cands[q].gfn)) / U;
