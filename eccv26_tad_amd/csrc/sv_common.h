@@ -120,9 +120,9 @@ __device__ __forceinline__ void orphan_entry(int64_t e, const T* __restrict__ go
 // More than kOrphanCap one-way entries, or a table of more than 2^31 entries:
 // the atomic pass instead (each contribution added into gi with its own
 // rounding, order unfixed).
+constexpr int kOrphanCap = 2048;
 // Inlined into each caller: as an out-of-line call it made the reduction
 // kernels that hold it reserve registers for the call (58 -> 103 VGPRs).
-constexpr int kOrphanCap = 2048;
 template <typename T, bool DEPTHWISE, int NTH>
 __device__ __forceinline__ void orphan_exact(const T* __restrict__ go, const int32_t* __restrict__ nbr,
                              const T* __restrict__ w, T* __restrict__ gi, int64_t n, int c_in, int c_out,
