@@ -222,33 +222,41 @@ __global__ __launch_bounds__(256) void k_bw_valu(const T* __restrict__ go, const
 // 64 threads each sum a contiguous sixteenth of the splits (eight loads in
 // flight), and the 16 group sums are added in group order through LDS, so
 // the order of the sum is fixed.
+// Split reductions: a 1024-thread workgroup takes kRedLanes outputs; its
+// kRedGroups thread groups each sum a contiguous range of the splits (up to
+// 8 loads in flight), and the group sums are added in order through LDS. 32
+// groups keep each group's range to one round of loads up to 256 splits (16
+// groups of 64 outputs took two rounds at 150-254 splits).
+constexpr int kRedGroups = 32, kRedLanes = 1024 / kRedGroups;
+
 template <typename T, typename A>
 __global__ __launch_bounds__(1024) void k_split_reduce(const A* __restrict__ ws, int64_t count,
                                                        int splits, T* __restrict__ out, int64_t stride,
                                                        int64_t count0, T* __restrict__ out2) {
-    __shared__ A part[16][64];
-    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
-    const int spt = (splits + 15) / 16;
+    __shared__ A part[kRedGroups][kRedLanes];
+    const int lane = threadIdx.x % kRedLanes, g = threadIdx.x / kRedLanes;
+    const int64_t e = (int64_t)blockIdx.x * kRedLanes + lane;
+    const int spt = (splits + kRedGroups - 1) / kRedGroups;
     const int q0 = min(splits, g * spt), q1 = min(splits, q0 + spt);
     A s = 0;
     if (e < count) {
-        int q = q0;
-        for (; q + 8 <= q1; q += 8) {
+        // eight loads in flight, the last batch's extra slots reading the
+        // range's last split and adding zero (the sum and its order are those
+        // of the plain loop; loads stay unconditional, so no branch waits)
+        for (int q = q0; q < q1; q += 8) {
             A v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)(q + u) * stride + e];
+            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)min(q + u, q1 - 1) * stride + e];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) s += v[u];
+            for (int u = 0; u < 8; ++u) s += q + u < q1 ? v[u] : (A)0;
         }
-        for (; q < q1; ++q) s += ws[(int64_t)q * stride + e];
     }
     part[g][lane] = s;
     __syncthreads();
     if (g != 0 || e >= count) return;
     A t = part[0][lane];
 #pragma unroll
-    for (int h = 1; h < 16; ++h) t += part[h][lane];
+    for (int h = 1; h < kRedGroups; ++h) t += part[h][lane];
     if (e < count0) out[e] = from_acc<T>(t);
     else out2[e - count0] = from_acc<T>(t);
 }
@@ -615,29 +623,27 @@ __global__ __launch_bounds__(1024) void k_dw_bwd_reduce(const A* __restrict__ ws
                                                         const T* __restrict__ go, const int32_t* __restrict__ nbr,
                                                         const T* __restrict__ w, T* __restrict__ gi, int64_t n,
                                                         int c, int64_t tpb) {
-    __shared__ A part[16][64];
-    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const int64_t e = (int64_t)blockIdx.x * 64 + lane;
-    const int spt = (splits + 15) / 16;
+    __shared__ A part[kRedGroups][kRedLanes];
+    const int lane = threadIdx.x % kRedLanes, g = threadIdx.x / kRedLanes;
+    const int64_t e = (int64_t)blockIdx.x * kRedLanes + lane;
+    const int spt = (splits + kRedGroups - 1) / kRedGroups;
     const int q0 = min(splits, g * spt), q1 = min(splits, q0 + spt);
     A sum = 0;
-    if (e < count) {
-        int q = q0;
-        for (; q + 8 <= q1; q += 8) {
+    if (e < count) {  // as k_split_reduce
+        for (int q = q0; q < q1; q += 8) {
             A v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)(q + u) * stride + e];
+            for (int u = 0; u < 8; ++u) v[u] = ws[(int64_t)min(q + u, q1 - 1) * stride + e];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) sum += v[u];
+            for (int u = 0; u < 8; ++u) sum += q + u < q1 ? v[u] : (A)0;
         }
-        for (; q < q1; ++q) sum += ws[(int64_t)q * stride + e];
     }
     part[g][lane] = sum;
     __syncthreads();
     if (g == 0 && e < count) {
         A t = part[0][lane];
 #pragma unroll
-        for (int h = 1; h < 16; ++h) t += part[h][lane];
+        for (int h = 1; h < kRedGroups; ++h) t += part[h][lane];
         if (e < count0) gw[e] = from_acc<T>(t);
         else gb[e - count0] = from_acc<T>(t);
     }
@@ -672,7 +678,7 @@ template <typename T>
 static void launch_split_reduce(const void* part, int64_t count, int splits, void* out,
                                 hipStream_t s) {
     typedef typename Acc<T>::type A;
-    hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, 64))),
+    hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, kRedLanes))),
                        dim3(1024), 0, s, (const A*)part, count, splits, (T*)out, count, count, (T*)nullptr);
 }
 
@@ -803,7 +809,7 @@ static void launch_dw_bw(const BwPlan& p, const void* go, const void* x, const i
         hipLaunchKernelGGL((k_dw_bw_vec<T>), dim3((unsigned)p.splits), dim3(512), 0, s, (const T*)go,
                            (const T*)x, nbr, part, n, c, tpb, p.rows_per_split);
         const int64_t count = gb ? 10LL * c : 9LL * c;
-        hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, 64))),
+        hipLaunchKernelGGL((k_split_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, kRedLanes))),
                            dim3(1024), 0, s, (const A*)part, count, p.splits, (T*)gw, 10LL * c, 9LL * c,
                            (T*)gb);
         return;
@@ -825,7 +831,7 @@ static bool launch_dw_bwd(const BwPlan& p, const void* go, const void* x, const 
     hipLaunchKernelGGL((k_dw_bwd_vec<T>), dim3((unsigned)p.splits), dim3(512), 0, s, (const T*)go, (const T*)x,
                        nbr, (const T*)w, (T*)gi, (A*)ws, flags, n, c, tpb, p.rows_per_split, sym);
     const int64_t count = gb ? 10LL * c : 9LL * c;
-    hipLaunchKernelGGL((k_dw_bwd_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, 64))), dim3(1024),
+    hipLaunchKernelGGL((k_dw_bwd_reduce<T, A>), dim3((unsigned)std::max<int64_t>(1, cdiv(count, kRedLanes))), dim3(1024),
                        0, s, (const A*)ws, count, p.splits, (T*)gw, 10LL * c, 9LL * c, (T*)gb, (const uint32_t*)flags,
                        (const T*)go, nbr, (const T*)w, (T*)gi, n, c, tpb);
     return true;
