@@ -15,8 +15,10 @@ Printed: ONE JSON line on stdout. ``value`` is the algorithmic HBM throughput
 of fwd+bwd (GB/s) at the headline keep rate; ``sweep`` holds us / GB/s /
 TFLOP/s / speedup over a dense 3x3 conv (MIOpen, same shape) for every keep
 rate, and over the reference adapter's dense path on the same kept tokens
-(scatter -> conv2d -> gather, fwd + bwd); ``roofline`` covers the dominant kernel, timed with HIP events on the
-stream it is launched on; ``cpu_baseline`` times the OpenMP fp32 port of the
+(scatter -> conv2d -> gather, fwd + bwd), and ``gpu_us``, the step's GPU
+time with the steps queued ahead of the GPU (at low keep rates the host
+enqueues a step more slowly than the GPU runs it); ``roofline`` covers the
+dominant kernel, timed with HIP events on the stream it is launched on; ``cpu_baseline`` times the OpenMP fp32 port of the
 reference dataflow (oracle/, kind "port") on the host cores.
 """
 from __future__ import annotations
@@ -126,6 +128,36 @@ def time_events(fn, reps, warm=3):
     return s.elapsed_time(e) / reps
 
 
+def time_queued(fn, reps, warm=3):
+    """Average ms per call of fn() on the GPU alone: the calls are queued
+    behind a spinning kernel (torch.cuda._sleep) while the host enqueues
+    them, and the events bracket only their execution, so a call whose host
+    side takes longer than its GPU work is timed by the latter. The spin is
+    lengthened until the host is done before it ends (checked with an event
+    recorded at its end)."""
+    import torch
+
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    cycles = 1 << 21
+    for _ in range(6):
+        h0, s, e = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        h0.record()
+        torch.cuda._sleep(cycles)
+        s.record()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        host_ms = (time.perf_counter() - t0) * 1e3
+        e.record()
+        torch.cuda.synchronize()
+        if h0.elapsed_time(s) > 1.2 * host_ms:  # the spin outlasted the enqueueing
+            return s.elapsed_time(e) / reps
+        cycles *= 4
+    raise RuntimeError("time_queued: the host did not finish enqueueing within the spin")
+
+
 class Problem:
     def __init__(self, keep, dev, dtype):
         import torch
@@ -185,9 +217,10 @@ class Problem:
         return y, gi, gw, gb
 
 
-def dense_ms(dev, dtype, reps):
+def dense_ms(dev, dtype, reps, timer=None):
     """Dense 3x3 conv (MIOpen) fwd + input grad + weight grad + bias grad on the
-    full [B*T, C, H, W] grid; best of NCHW and channels_last."""
+    full [B*T, C, H, W] grid; best of NCHW and channels_last (timed by timer,
+    time_events by default)."""
     import torch
     import torch.nn.functional as F
 
@@ -207,7 +240,7 @@ def dense_ms(dev, dtype, reps):
             gx, gw, gb = torch.autograd.grad(y, (x, w, b), dy)
             return gx
 
-        t = time_events(run, reps, warm=5)
+        t = (timer or time_events)(run, reps, warm=5)
         best = t if best is None else min(best, t)
     return best
 
@@ -373,6 +406,8 @@ def depthwise_measure(dev, reps, keeps=None):
 
         td = time_events(run_dense, reps, warm=5)
         dense = td if dense is None else min(dense, td)
+        tq = time_queued(run_dense, reps, warm=5)
+        dense_q = tq if fmt is torch.contiguous_format else min(dense_q, tq)
     rows = []
     for kr in keeps or KEEPS:
         mask = blob_mask(kr).to(dev)
@@ -392,6 +427,7 @@ def depthwise_measure(dev, reps, keeps=None):
             return y, gi, gw, gb
 
         t = time_events(step, reps)
+        tq = time_queued(step, reps)
         parts = {"fwd": lambda: ops.dw_fwd(x, table, w, b, 0),
                  "bwd": lambda: ops.dw_bwd(go, x, table, w, 0, True, symmetric=sym),
                  "bwd_checked": lambda: ops.dw_bwd(go, x, table, w, 0, True),
@@ -403,10 +439,11 @@ def depthwise_measure(dev, reps, keeps=None):
         rows.append({"keep": kr, "n": n, "hit_rate": round(hit, 4), "us": round(t * 1e3, 2),
                      "gbs": round(by / (t * 1e-3) / 1e9, 1),
                      "hbm_frac": round(by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "pass_us": pt,
-                     "speedup_vs_dense": round(dense / t, 3)})
+                     "speedup_vs_dense": round(dense / t, 3), "gpu_us": round(tq * 1e3, 2),
+                     "speedup_vs_dense_gpu": round(dense_q / tq, 3)})
         log(f"bench: depthwise {rows[-1]}")
     return {"workload": f"depthwise 3x3, C={C} fp16, B{B} x T{T} x {H}x{W}, clustered (Gaussian-blob) keep masks",
-            "dense_us": round(dense * 1e3, 2), "sweep": rows}
+            "dense_us": round(dense * 1e3, 2), "dense_gpu_us": round(dense_q * 1e3, 2), "sweep": rows}
 
 
 def large_channel_measure(dev, reps, cases=None):
@@ -822,12 +859,14 @@ def main():
                                  "isolated_median": round(isolated[p][0] * 1e3, 2)} for p, v in kernels.items()}
 
     dense = None if args.no_dense else dense_ms(dev, dtype, 20)
+    dense_q = None if args.no_dense else dense_ms(dev, dtype, 20, timer=time_queued)
 
     sweep = []
     if not args.no_sweep:
         for kr in KEEPS:
             p = prob if abs(kr - args.keep) < 1e-9 else Problem(kr, dev, dtype)
             t = time_events(p.step, 20)
+            tq = time_queued(p.step, 20)
             b2 = sum(op_bytes(p.n, C, C, s).values())
             f9 = 3 * 2 * 9 * p.n * C * C
             fu = 3 * 2 * p.valid * C * C
@@ -836,8 +875,10 @@ def main():
                    "tflops_9n": round(f9 / (t * 1e-3) / 1e12, 2),
                    "roofline_frac": round(max(b2 / (HBM_PEAK_GBS * 1e9),
                                               fu / (MFMA_PEAK_TFLOPS[dname] * 1e12)) / (t * 1e-3), 4)}
+            row["gpu_us"] = round(tq * 1e3, 2)
             if dense is not None:
                 row["speedup_vs_dense"] = round(dense / t, 3)
+                row["speedup_vs_dense_gpu"] = round(dense_q / tq, 3)
                 da = dense_adapter_ms(p, dev, dtype, 20)
                 row["dense_adapter_us"] = round(da * 1e3, 2)
                 row["speedup_vs_dense_adapter"] = round(da / t, 3)
