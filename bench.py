@@ -134,7 +134,7 @@ def time_queued(fn, reps, warm=3):
     them, and the events bracket only their execution, so a call whose host
     side takes longer than its GPU work is timed by the latter. The spin is
     lengthened until the host is done before it ends (checked with an event
-    recorded at its end)."""
+    recorded at its end); None if it never is (the row then reports null)."""
     import torch
 
     for _ in range(warm):
@@ -155,7 +155,8 @@ def time_queued(fn, reps, warm=3):
         if h0.elapsed_time(s) > 1.2 * host_ms:  # the spin outlasted the enqueueing
             return s.elapsed_time(e) / reps
         cycles *= 4
-    raise RuntimeError("time_queued: the host did not finish enqueueing within the spin")
+    log("bench: time_queued: the host did not finish enqueueing within the spin")
+    return None
 
 
 class Problem:
@@ -241,7 +242,7 @@ def dense_ms(dev, dtype, reps, timer=None):
             return gx
 
         t = (timer or time_events)(run, reps, warm=5)
-        best = t if best is None else min(best, t)
+        best = min((v for v in (best, t) if v is not None), default=None)
     return best
 
 
@@ -392,7 +393,7 @@ def depthwise_measure(dev, reps, keeps=None):
     # / bias gradients on the full grid, best of NCHW and channels_last
     torch.backends.cudnn.benchmark = True
     gd = torch.Generator().manual_seed(SEED + 4)
-    dense = None
+    dense = dense_q = None
     for fmt in (torch.contiguous_format, torch.channels_last):
         xd = torch.randn(B * T, C, H, W, generator=gd).to(dev, torch.float16).contiguous(memory_format=fmt)
         xd.requires_grad_(True)
@@ -407,7 +408,7 @@ def depthwise_measure(dev, reps, keeps=None):
         td = time_events(run_dense, reps, warm=5)
         dense = td if dense is None else min(dense, td)
         tq = time_queued(run_dense, reps, warm=5)
-        dense_q = tq if fmt is torch.contiguous_format else min(dense_q, tq)
+        dense_q = min((v for v in (dense_q, tq) if v is not None), default=None)
     rows = []
     for kr in keeps or KEEPS:
         mask = blob_mask(kr).to(dev)
@@ -439,11 +440,13 @@ def depthwise_measure(dev, reps, keeps=None):
         rows.append({"keep": kr, "n": n, "hit_rate": round(hit, 4), "us": round(t * 1e3, 2),
                      "gbs": round(by / (t * 1e-3) / 1e9, 1),
                      "hbm_frac": round(by / (t * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "pass_us": pt,
-                     "speedup_vs_dense": round(dense / t, 3), "gpu_us": round(tq * 1e3, 2),
-                     "speedup_vs_dense_gpu": round(dense_q / tq, 3)})
+                     "speedup_vs_dense": round(dense / t, 3),
+                     "gpu_us": round(tq * 1e3, 2) if tq else None,
+                     "speedup_vs_dense_gpu": round(dense_q / tq, 3) if tq and dense_q else None})
         log(f"bench: depthwise {rows[-1]}")
     return {"workload": f"depthwise 3x3, C={C} fp16, B{B} x T{T} x {H}x{W}, clustered (Gaussian-blob) keep masks",
-            "dense_us": round(dense * 1e3, 2), "dense_gpu_us": round(dense_q * 1e3, 2), "sweep": rows}
+            "dense_us": round(dense * 1e3, 2), "dense_gpu_us": round(dense_q * 1e3, 2) if dense_q else None,
+            "sweep": rows}
 
 
 def large_channel_measure(dev, reps, cases=None):
@@ -875,10 +878,10 @@ def main():
                    "tflops_9n": round(f9 / (t * 1e-3) / 1e12, 2),
                    "roofline_frac": round(max(b2 / (HBM_PEAK_GBS * 1e9),
                                               fu / (MFMA_PEAK_TFLOPS[dname] * 1e12)) / (t * 1e-3), 4)}
-            row["gpu_us"] = round(tq * 1e3, 2)
+            row["gpu_us"] = round(tq * 1e3, 2) if tq else None
             if dense is not None:
                 row["speedup_vs_dense"] = round(dense / t, 3)
-                row["speedup_vs_dense_gpu"] = round(dense_q / tq, 3)
+                row["speedup_vs_dense_gpu"] = round(dense_q / tq, 3) if tq and dense_q else None
                 da = dense_adapter_ms(p, dev, dtype, 20)
                 row["dense_adapter_us"] = round(da * 1e3, 2)
                 row["speedup_vs_dense_adapter"] = round(da / t, 3)
