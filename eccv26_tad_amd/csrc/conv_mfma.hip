@@ -1565,16 +1565,23 @@ static void launch_wide_fm(const void* src, const int32_t* nbr, const void* wb, 
             // tiles of three row fragments instead. Each workgroup then streams
             // a third of the weight and the grid holds about as many tiles
             // (measured 10.8 -> 8.2 us at 3136 rows, 14.4 -> 11.5 us at 7840).
+            // The weight ring holds a whole slice (six steps, 24 registers
+            // with one column fragment): in a training step the packed weight
+            // is new, not yet in the XCD's L2, and two steps of lookahead left
+            // its fetches exposed (c2 step at 10 % keep 29.0 -> 27.5 us; the
+            // forward timed alone on a weight already in L2 does not change).
             if (fm <= 2) {
-                launch_wide<T, MODE, CR, 3, 1, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
+                launch_wide<T, MODE, CR, 3, 1, 6>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
                 return;
             }
         }
         if constexpr (CR == 256 && FN == 4) {
             // the same at C = 256: 128-column tiles of three row fragments
-            // (measured 14.4 -> 11.7 us at 4916 rows)
+            // (measured 14.4 -> 11.7 us at 4916 rows), with a four-step weight
+            // ring for the packed weight fresh from the pack (config 4 step at
+            // 10 % keep 43.2 -> 40.9 us)
             if (fm <= 2) {
-                launch_wide<T, MODE, CR, 3, 2, D>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
+                launch_wide<T, MODE, CR, 3, 2, 4>(src, nbr, wb, bias, bias_mode, out, n, n_out, tpb, flag, sym, s);
                 return;
             }
         }
