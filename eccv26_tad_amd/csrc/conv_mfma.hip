@@ -260,6 +260,7 @@ struct GgWideLds {
     int kvalid[9];
     int klist[10];
     int nk_s, lo_s, hi_s;
+    __align__(16) float bias[CR >= 512 ? 4 * FN * 16 : 4];  // the forward's bias (512 channels)
 };
 
 // One tile of the wide gathered GEMM, run by threads [0, 256 * WS) of a
@@ -355,6 +356,26 @@ __device__ __forceinline__ void gg_wide_tile(
         sp[q] = bload16(rs_src, e < SPEC_CHUNKS && gr >= 0 && gr < n
                                     ? (uint32_t)gr * (uint32_t)(CR * 2) + (uint32_t)(e - r * CPR) * 16u
                                     : kOOB);
+    }
+    // At 512 channels the forward's bias goes through LDS: one column per
+    // thread, one 32-bit load with no branch issued behind the window's loads,
+    // stored to LDS after the main loop. In registers (the other widths) each
+    // lane holds FN * 4 values through the main loop, and at 512 channels the
+    // kernel then spilled 10 registers (config 5 forward 70.4 -> 68.5 us).
+    // At 192 channels the LDS form measured 2 us slower per training step
+    // (c2 at 55 % keep) with no cause found, so the other widths keep the
+    // registers.
+    constexpr bool BIAS_LDS = CR >= 512;
+    const bool has_bias = MODE == MODE_FWD && bias_mode != SVTAD_BIAS_NONE;  // uniform
+    const bool bias32 = bias_mode == SVTAD_BIAS_FP32;
+    uint32_t bias_raw = 0u;
+    if constexpr (BIAS_LDS) {
+        if (has_bias) {
+            const rsrc_t rs_bias = make_rsrc(bias, (uint32_t)n_out * (bias32 ? 4u : 2u));
+            const uint32_t col = (uint32_t)(col0 + tid);
+            const uint32_t off = bias32 ? col * 4u : (col * 2u) & ~3u;  // n_out is even
+            bias_raw = __builtin_amdgcn_raw_buffer_load_b32(rs_bias, tid < BN && col < (uint32_t)n_out ? off : kOOB, 0, 0);
+        }
     }
 
     if (tid < 9) kvalid[tid] = 0;
@@ -471,32 +492,34 @@ __device__ __forceinline__ void gg_wide_tile(
     const int g = lane >> 4;  // reduction chunk of the lane within a step
     u16* const lds = &Ab[0][0];
 
-    // the bias of this lane's output columns, loaded now so the epilogue does
-    // not wait for it
-    float bv[FN][4];
+    // the bias of this lane's output columns in registers (below 512
+    // channels), loaded now so the epilogue does not wait for it
+    float bv[BIAS_LDS ? 1 : FN][4];
+    if constexpr (!BIAS_LDS) {
 #pragma unroll
-    for (int f = 0; f < FN; ++f)
+        for (int f = 0; f < FN; ++f)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bv[f][j] = 0.f;
-    if (MODE == MODE_FWD && set == 0 && bias_mode != SVTAD_BIAS_NONE) {  // uniform
-        // one straight-line loop per bias dtype
-        const int c0 = col0 + wave * FN * 16 + g * 4;
-        if (bias_mode == SVTAD_BIAS_FP32) {
+            for (int j = 0; j < 4; ++j) bv[f][j] = 0.f;
+        if (MODE == MODE_FWD && set == 0 && bias_mode != SVTAD_BIAS_NONE) {  // uniform
+            // one straight-line loop per bias dtype
+            const int c0 = col0 + wave * FN * 16 + g * 4;
+            if (bias_mode == SVTAD_BIAS_FP32) {
 #pragma unroll
-            for (int f = 0; f < FN; ++f)
+                for (int f = 0; f < FN; ++f)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int col = c0 + f * 16 + j;
-                    bv[f][j] = col < n_out ? ((const float*)bias)[col] : 0.f;
-                }
-        } else {
+                    for (int j = 0; j < 4; ++j) {
+                        const int col = c0 + f * 16 + j;
+                        bv[f][j] = col < n_out ? ((const float*)bias)[col] : 0.f;
+                    }
+            } else {
 #pragma unroll
-            for (int f = 0; f < FN; ++f)
+                for (int f = 0; f < FN; ++f)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int col = c0 + f * 16 + j;
-                    bv[f][j] = col < n_out ? (float)((const T*)bias)[col] : 0.f;
-                }
+                    for (int j = 0; j < 4; ++j) {
+                        const int col = c0 + f * 16 + j;
+                        bv[f][j] = col < n_out ? (float)((const T*)bias)[col] : 0.f;
+                    }
+            }
         }
     }
 
@@ -582,6 +605,12 @@ __device__ __forceinline__ void gg_wide_tile(
             __syncthreads();
         }
     }
+    // the bias into LDS for the epilogue (its load arrived long ago)
+    if constexpr (BIAS_LDS) {
+        if (has_bias && tid < BN)
+            L.bias[tid] = bias32 ? __builtin_bit_cast(float, bias_raw)
+                                 : (float)__builtin_bit_cast(T, (u16)(bias_raw >> (((col0 + tid) & 1) * 16)));
+    }
     __syncthreads();  // all waves are done reading the LDS rows
 
     if constexpr (WS > 1) {
@@ -624,15 +653,20 @@ __device__ __forceinline__ void gg_wide_tile(
 #pragma unroll
         for (int f = 0; f < FN; ++f) {
             const int lc = wave * FN * 16 + f * 16 + g * 4;
+            f32x4 bl = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (BIAS_LDS && M != 0) bl = *(const f32x4*)&L.bias[lc];
 #pragma unroll
             for (int a = 0; a < FM; ++a) {
                 unsigned h[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float v = acc[a][f][j];
+                    float bj = 0.f;
+                    if constexpr (BIAS_LDS) bj = bl[j];
+                    else bj = bv[f][j];
                     T o;
-                    if constexpr (M == 1) o = (T)(v + bv[f][j]);
-                    else if constexpr (M == 2) o = (T)((float)(T)v + bv[f][j]);
+                    if constexpr (M == 1) o = (T)(v + bj);
+                    else if constexpr (M == 2) o = (T)((float)(T)v + bj);
                     else o = (T)v;
                     h[j] = (unsigned)__builtin_bit_cast(u16, o);
                 }
