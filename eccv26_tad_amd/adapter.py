@@ -322,10 +322,11 @@ class SparseConvAdapterFunction(Function):
             if need[12]:
                 g_gate = (gi_pa.float() * sp_rows.index_select(0, hm_rows).float()).sum().view(hm_gate.shape)
                 g_gate = g_gate.to(hm_gate.dtype)
-            # g * gate as one fp32 product rounded to cd (PyTorch's multiply
-            # in cd, or the cast of its float32 product under autocast)
-            g_sp = g_sp.reshape(-1, hidden).index_add(0, hm_rows, (gi_pa.float() * hm_gate.float()).to(cd))
-            g_sp = g_sp.view(sp.shape)
+            # the products g * gate summed into the special-token gradient in
+            # float32 and rounded to cd once: an index_add in cd rounds at
+            # every atomic add, in an order that changes from run to run
+            g_sp = g_sp.reshape(-1, hidden).float().index_add(0, hm_rows, gi_pa.float() * hm_gate.float())
+            g_sp = g_sp.to(cd).view(sp.shape)
         # down projection: GELU backward from the two gradient buffers, then
         # the input gradient with the residual's go in the same GEMM
         du = _ops.gelu_backward_split(g_sp, gi_pa, pre, S)
@@ -519,10 +520,15 @@ class SparseConvAdapter(nn.Module):
             frame = indices // hw
             n_frames = total_num_patches // hw
             idx = frame.unsqueeze(-1).expand(-1, -1, C)
-            feats = patches.new_zeros(B, n_frames, C).scatter_add(1, idx, patches)
-            counts = patches.new_zeros(B, n_frames, 1).scatter_add(
-                1, frame.unsqueeze(-1), torch.ones_like(frame, dtype=patches.dtype).unsqueeze(-1))
-            feats = feats / (counts + 1e-6)
+            # The fused path sums the frames, and the gather's backward sums
+            # the patch gradients per frame, in float32 and rounds once; the
+            # reference's scatter_add in the module dtype rounds at every
+            # atomic add, in an order that changes from run to run.
+            acc = torch.float32 if fused else patches.dtype
+            feats = patches.new_zeros(B, n_frames, C, dtype=acc).scatter_add(1, idx, patches.to(acc))
+            counts = patches.new_zeros(B, n_frames, 1, dtype=acc).scatter_add(
+                1, frame.unsqueeze(-1), torch.ones_like(frame, dtype=acc).unsqueeze(-1))
+            feats = (feats / (counts + 1e-6)).to(patches.dtype)
             attn_in = torch.cat([special, feats], dim=1)
             xa = self.attn_norm(attn_in)
             qkv = self.qkv(xa).reshape(B, -1, 3, self.num_heads, C // self.num_heads).permute(2, 0, 3, 1, 4)
@@ -531,7 +537,7 @@ class SparseConvAdapter(nn.Module):
             coarse = xa + self.attn_mlp(xa)
             sp_out = coarse[:, :S]
             fr_out = coarse[:, S:]
-            pa_out = torch.gather(fr_out, 1, idx)
+            pa_out = torch.gather(fr_out.float(), 1, idx).to(fr_out.dtype) if fused else torch.gather(fr_out, 1, idx)
             return shortcut + torch.cat([sp_out, pa_out], dim=1)
         xa = self.down_attn(self.attn_norm(x_comb))
         A = xa.shape[-1]
