@@ -1027,6 +1027,11 @@ __device__ __forceinline__ void transpose8(const u32x4* in, u32x4* out) {
 // quarter of the splits with all its loads in flight, and the quarters are
 // added in order g = 0..3 through LDS, so the order of the sum is fixed.
 // The partials are read once: non-temporal loads.
+template <typename T>
+__device__ __forceinline__ void bw_store_quad(int64_t e, f32x4 acc, int c_in, int c_out, int fm, int fn,
+                                              int wgm, int wgn, int n_ci_tiles, int n_co_tiles,
+                                              T* __restrict__ gw);
+
 template <typename T, int CP>
 __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __restrict__ part,
                                                 int splits, int n_off, int c_in, int c_out, int fm, int fn,
@@ -1034,7 +1039,6 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
                                                 T* __restrict__ gw) {
     __shared__ f32x4 qsum[4][64];
     const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const int bm = wgm * fm * 16, bn = wgn * fn * 16;
     // a split's partials: one block of c_in * c_out per work unit (with the
     // 9 offsets: offsets 0-3, the center's CP parts, offsets 5-8)
     static_assert(CP == 2 || CP == 4, "center parts");
@@ -1084,7 +1088,15 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
     acc = qsum[0][lane] + qsum[1][lane];
     acc += qsum[2][lane];
     acc += qsum[3][lane];
-    // decode the fragment-order position
+    bw_store_quad<T>(e, acc, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles, n_co_tiles, gw);
+}
+
+// The store of quadruple e's sum into gw (its fragment-order position decoded).
+template <typename T>
+__device__ __forceinline__ void bw_store_quad(int64_t e, f32x4 acc, int c_in, int c_out, int fm, int fn,
+                                              int wgm, int wgn, int n_ci_tiles, int n_co_tiles,
+                                              T* __restrict__ gw) {
+    const int bm = wgm * fm * 16, bn = wgn * fn * 16;
     int64_t rest = e * 4;
     const int64_t tile_sz = (int64_t)bm * bn;
     const int64_t tile = rest / tile_sz;
@@ -1103,6 +1115,56 @@ __device__ __forceinline__ void bw_reduce_quads(int64_t blk, const float* __rest
     T* gp = gw + ((int64_t)k * c_in + ci) * c_out + co;
 #pragma unroll
     for (int j = 0; j < 4; ++j) gp[(int64_t)j * c_out] = (T)acc[j];
+}
+
+// bw_reduce_quads with at most two splits (up to four work): one thread per
+// quadruple sums each split (its center parts in order) and then the splits
+// in order, with every load in flight and no LDS. These are the same
+// additions in the same order as the four-thread form (a sum that starts at
+// +0 is never -0, so the zero terms that form adds change nothing): the
+// results are bit-identical. Config 4 at 10 % keep (2 splits): step 41.3 ->
+// 40.3 us; with 4 splits (c2 at 10 %, 16 loads per thread on the center
+// quadruples) the step was 1.4 us slower, so those keep the four threads.
+template <typename T, int CP>
+__device__ __forceinline__ void bw_reduce_quads_direct(int64_t e, const float* __restrict__ part,
+                                                       int splits, int n_off, int c_in, int c_out, int fm,
+                                                       int fn, int wgm, int wgn, int n_ci_tiles,
+                                                       int n_co_tiles, T* __restrict__ gw) {
+    const int units = n_off == 9 ? 8 + CP : n_off;
+    const int64_t per_off = (int64_t)c_in * c_out;
+    const int64_t per_split = units * per_off;
+    if (e >= (int64_t)n_off * per_off / 4) return;
+    const int ko = (int)(e * 4 / per_off);
+    const int64_t within = e * 4 - ko * per_off;
+    const int unit = n_off == 9 && ko > 4 ? ko + CP - 1 : ko;
+    const float* pe = part + unit * per_off + within;
+    const int np = n_off == 9 && ko == 4 ? CP : 1;  // the center's parts
+    f32x4 v[4][CP];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int pt = 0; pt < CP; ++pt)
+            v[q][pt] = q < splits && pt < np
+                           ? __builtin_nontemporal_load((const f32x4*)(pe + pt * per_off + (int64_t)q * per_split))
+                           : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 sq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        sq[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int pt = 0; pt < CP; ++pt) sq[q] += v[q][pt];
+    }
+    f32x4 acc = sq[0] + sq[1];
+    acc += sq[2];
+    acc += sq[3];
+    bw_store_quad<T>(e, acc, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles, n_co_tiles, gw);
+}
+
+// Workgroups of k_bw_reduce for the gw quadruples: 256 quadruples each with at
+// most two splits (bw_reduce_quads_direct), else 64.
+__host__ __device__ inline int64_t bw_quad_blocks(int64_t quads, int splits) {
+    const int64_t per = splits <= 2 ? 256 : 64;
+    return (quads + per - 1) / per;
 }
 
 // gb[c] = T(sum_s part_b[s][c]), splits summed in order.
@@ -1486,11 +1548,15 @@ __global__ __launch_bounds__(256) void k_bw_reduce(const float* __restrict__ par
                                                    T* __restrict__ gw, T* __restrict__ gb,
                                                    OrphanJob oj) {
     // workgroups [0, quad_blocks) reduce gw, the rest the bias
-    const int64_t quad_blocks = ((int64_t)n_off * c_in * c_out / 4 + 63) / 64;
-    if ((int64_t)blockIdx.x < quad_blocks)
-        bw_reduce_quads<T, CP>(blockIdx.x, part, splits, n_off, c_in, c_out, fm, fn, wgm, wgn, n_ci_tiles,
-                               n_co_tiles, gw);
-    else if (gb)
+    const int64_t quad_blocks = bw_quad_blocks((int64_t)n_off * c_in * c_out / 4, splits);
+    if ((int64_t)blockIdx.x < quad_blocks) {
+        if (splits <= 2)  // uniform
+            bw_reduce_quads_direct<T, CP>((int64_t)blockIdx.x * 256 + threadIdx.x, part, splits, n_off, c_in,
+                                          c_out, fm, fn, wgm, wgn, n_ci_tiles, n_co_tiles, gw);
+        else
+            bw_reduce_quads<T, CP>(blockIdx.x, part, splits, n_off, c_in, c_out, fm, fn, wgm, wgn,
+                                   n_ci_tiles, n_co_tiles, gw);
+    } else if (gb)
         bw_reduce_bias<T>(((int64_t)blockIdx.x - quad_blocks) * 256 + threadIdx.x, part_b,
                           n_off == 9 ? CP * splits : splits, c_out, gb);
     if (!oj.gi || (oj.flag && *oj.flag == 0u) || blockIdx.x != 0) return;
@@ -1847,7 +1913,7 @@ static int bw_dispatch(const BwPlan& p, const void* go, const void* x, const int
 static void bw_big_reduce(int dtype, const BigCfg& bc, int splits, const float* part, const float* part_b,
                           void* gw, void* gb, int c_in, int c_out, const OrphanJob* oj, int cparts, hipStream_t s) {
     const int nci = c_in / (16 * bc.wgm * bc.fm), nco = c_out / (16 * bc.wgn * bc.fn);
-    const int64_t blocks = cdiv((int64_t)9 * c_in * c_out / 4, 64) + (gb ? cdiv(c_out, 256) : 0);
+    const int64_t blocks = bw_quad_blocks((int64_t)9 * c_in * c_out / 4, splits) + (gb ? cdiv(c_out, 256) : 0);
     const dim3 grid((unsigned)blocks);
     const OrphanJob job = oj ? *oj : OrphanJob{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
 #define SVTAD_REDUCE(T, CP)                                                                                  \
@@ -2092,7 +2158,7 @@ static int launch_wgrad(const BwPlan& p, const void* g, const int32_t* rows, con
                        dim3(bw_big_threads(FM, FN, WGM, WGN)), 0, s, (const T*)x, (const T*)g, rows,
                        part, (float*)nullptr, n, c_in, c_out, (int64_t)0, p.rows_per_split, nci, nco,
                        blocks, 1, n_src);
-    const dim3 grid((unsigned)cdiv((int64_t)c_in * c_out / 4, 64));
+    const dim3 grid((unsigned)bw_quad_blocks((int64_t)c_in * c_out / 4, p.splits));
     const OrphanJob none{nullptr, nullptr, nullptr, nullptr, 0, 0, 0, 0, nullptr};
     if (out_f32)
         hipLaunchKernelGGL((k_bw_reduce<float, 2>), grid, dim3(256), 0, s, (const float*)part, (const float*)nullptr,
